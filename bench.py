@@ -1,0 +1,272 @@
+"""Benchmark of the MI355X FP8 linear path (one GPU).
+
+Workload (BASELINE.json metric "FP8 GEMM TFLOP/s + % FP8 MFMA peak, d12 block fwd+bwd @32768 tok", configs 3 + 4):
+one step = the forward and backward of a width-1024 (d12) JiT-T2I image block's four FP8 linears at one GPU's share
+of a step (128 images x 256 tokens = 32768 tokens), through the drop-in autograd API with every GEMM in FP8
+(recipe "native3"): qkv_x (1024 -> 3072), proj (1024 -> 1024), and the SwiGLU MLP w12 (1024 -> 8192) + w3
+(4096 -> 1024) -- 12 FP8 GEMMs (forward, dgrad, wgrad) = 3.2985 TFLOP, plus every cast, SwiGLU and transposing
+kernel the path runs. Inputs are seeded synthetic tensors already in HBM: X ~ N(0,1), W ~ N(0, 1/K), dY ~ N(0, 1e-2),
+bf16. value = 3.2985 TFLOP / measured step time.
+
+Also measured live: the 12 GEMM launches alone (the roofline's dominant kernel, HIP events on the launch stream),
+the config-2 cast ([32768 x 1024] bf16 -> e4m3, GB/s of algorithmic bytes), hipBLASLt's FP8 GEMM on the same 12
+shapes via torch._scaled_mm (a comparator only), and the CPU baseline (the oracle, a bounded sample).
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-compare]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nano-gpic_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "FP8 GEMM TFLOP/s + % FP8 MFMA peak, d12 block fwd+bwd @32768 tok"
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA (AMD spec)
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+M_TOK, C, H = 32768, 1024, 4096
+
+
+def gemm_shapes(M=M_TOK, C=C, H=H):
+    """(name, M, N, K) of the 12 GEMMs of one block's fwd + bwd (output [M, N], reduction K)."""
+    lin = {"qkv": (C, 3 * C), "proj": (C, C), "w12": (C, 2 * H), "w3": (H, C)}
+    out = []
+    for name, (k, n) in lin.items():
+        out.append((f"{name}.fwd", M, n, k))
+        out.append((f"{name}.dgrad", M, k, n))
+        out.append((f"{name}.wgrad", n, k, M))
+    return out
+
+
+def flops(shapes):
+    return sum(2.0 * m * n * k for _, m, n, k in shapes)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-compare", action="store_true")
+    return p.parse_args()
+
+
+def make_inputs(dev, seed=0):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def bf(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16)
+
+    t = {
+        "x_qkv": bf(M_TOK, C), "x_proj": bf(M_TOK, C), "x_mlp": bf(M_TOK, C),
+        "w_qkv": bf(3 * C, C, std=C ** -0.5), "w_proj": bf(C, C, std=C ** -0.5),
+        "w12": bf(2 * H, C, std=C ** -0.5), "w3": bf(C, H, std=H ** -0.5),
+        "dy_qkv": bf(M_TOK, 3 * C, std=0.1), "dy_proj": bf(M_TOK, C, std=0.1), "dy_mlp": bf(M_TOK, C, std=0.1),
+    }
+    for k in ("x_qkv", "x_proj", "x_mlp", "w_qkv", "w_proj", "w12", "w3"):
+        t[k].requires_grad_(True)
+    return t
+
+
+def step(G, t):
+    import torch
+    y1 = G.fp8_linear_f8(t["x_qkv"], t["w_qkv"])
+    y2 = G.fp8_linear_f8(t["x_proj"], t["w_proj"])
+    y3 = G.fp8_mlp_f8(t["x_mlp"], t["w12"], t["w3"])
+    torch.autograd.backward([y1, y2, y3], [t["dy_qkv"], t["dy_proj"], t["dy_mlp"]])
+
+
+def time_region(fn, steps, warmup):
+    """ms per call of fn, HIP events on the current stream around `steps` calls after `warmup` untimed ones."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def gemm_operands(G, dev, shapes):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(1)
+    ops = []
+    for name, m, n, k in shapes:
+        a = (torch.randn(m, k, generator=g, device=dev)).to(torch.bfloat16)
+        b = (torch.randn(n, k, generator=g, device=dev) / k ** 0.5).to(torch.bfloat16)
+        aq, sa = G.tcast(a)
+        bq, sb = G.tcast(b)
+        ops.append((aq, sa, bq, sb))
+        del a, b
+    return ops
+
+
+def cpu_baseline():
+    """The oracle on the host: the d12 block's casts (C restatement, one thread) and its 12 GEMMs as float32 numpy
+    matmuls of the dequantized operands (BLAS threads), on a bounded sample of 2048 of the 32768 tokens."""
+    import numpy as np
+    from oracle import oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    Ms = 2048
+    rng = np.random.default_rng(0)
+
+    def bf(shape, std=1.0):
+        return O.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+
+    def dq(q, s):
+        return O.e4m3_to_f32(q) * np.float32(s)
+
+    x = {k: bf((Ms, C)) for k in ("qkv", "proj", "mlp")}
+    w = {"qkv": bf((3 * C, C), C ** -0.5), "proj": bf((C, C), C ** -0.5)}
+    w12, w3 = bf((2 * H, C), C ** -0.5), bf((C, H), H ** -0.5)
+    dy = {"qkv": bf((Ms, 3 * C), 0.1), "proj": bf((Ms, C), 0.1), "mlp": bf((Ms, C), 0.1)}
+
+    def one():
+        for k in ("qkv", "proj"):
+            xq, sx, _ = O.tcast(x[k])
+            wq, sw, _ = O.tcast(w[k])
+            dxq = dq(xq, sx)
+            dwq = dq(wq, sw)
+            _ = dxq @ dwq.T                                   # forward
+            dyq, sdy, _ = O.tcast(dy[k])
+            ddy = dq(dyq, sdy)
+            _ = ddy @ dwq                                     # dgrad
+            _ = ddy.T @ dxq                                   # wgrad
+        xq, sx, _ = O.tcast(x["mlp"])
+        w12q, s12, _ = O.tcast(w12)
+        w3q, s3, _ = O.tcast(w3)
+        dxq, dw12, dw3 = dq(xq, sx), dq(w12q, s12), dq(w3q, s3)
+        z = O.f32_to_bf16(dxq @ dw12.T)
+        aq, sa, _ = O.swiglu_tcast(z)
+        da_ = dq(aq, sa)
+        _ = da_ @ dw3.T
+        dyq, sdy, _ = O.tcast(dy["mlp"])
+        ddy = dq(dyq, sdy)
+        da = O.f32_to_bf16(ddy @ dw3)
+        _ = ddy.T @ da_
+        dz, dzq, sdz, _ = O.swiglu_bwd(z, da)
+        ddz = dq(dzq, sdz)
+        _ = ddz @ dw12
+        _ = ddz.T @ dxq
+
+    one()                                                     # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 2 or time.perf_counter() - t0 < 10.0:
+        one()
+        reps += 1
+    sec = (time.perf_counter() - t0) / reps
+    fl = flops(gemm_shapes(M=Ms))
+    return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"d12 block fwd+bwd FP8 linear path on {Ms} of the {M_TOK} tokens (oracle casts in C, 1 thread; "
+                      f"GEMMs as float32 numpy matmuls of dequantized e4m3 operands); {reps} reps, "
+                      f"{sec * 1e3:.0f} ms per sample step", "ms_per_sample_step": round(sec * 1e3, 1)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import gpic_fp8 as G
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    # ---- the step: the whole FP8 linear path of a d12 block, fwd + bwd
+    t = make_inputs(dev)
+
+    def run():
+        for v in t.values():
+            v.grad = None
+        step(G, t)
+
+    shapes = gemm_shapes()
+    fl = flops(shapes)
+    ms = time_region(run, args.steps, args.warmup)
+
+    # ---- the 12 GEMM launches alone (dominant kernel), same shapes
+    ops = gemm_operands(G, dev, shapes)
+
+    def gemms():
+        for aq, sa, bq, sb in ops:
+            G.fp8_gemm(aq, sa, bq, sb, None, False)
+
+    gemm_ms = time_region(gemms, max(args.steps, 10), 3)
+    per_shape = {}
+    for (name, m, n, k), (aq, sa, bq, sb) in zip(shapes, ops):
+        tm = time_region(lambda: G.fp8_gemm(aq, sa, bq, sb, None, False), 10, 2)
+        per_shape[name] = {"M": m, "N": n, "K": k, "us": round(tm * 1e3, 1),
+                           "tflops": round(2.0 * m * n * k / tm / 1e9, 1)}
+
+    # ---- config 2: the cast alone
+    gx = torch.Generator().manual_seed(1)
+    xc = torch.randn(M_TOK, C, generator=gx)
+    cols = torch.randperm(C, generator=gx)[:round(0.01 * C)]
+    xc[:, cols] *= 50.0
+    xc = xc.to(torch.bfloat16).to(dev)
+    cast_ms = time_region(lambda: G.tcast(xc), 50, 10)
+    cast_bytes = xc.numel() * 3 + 4
+
+    # ---- comparator: hipBLASLt FP8 GEMM (torch._scaled_mm) on the same shapes
+    hip = None
+    if not args.no_compare:
+        try:
+            def blaslt():
+                for aq, sa, bq, sb in ops:
+                    torch._scaled_mm(aq, bq.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+            hip_ms = time_region(blaslt, max(args.steps, 10), 3)
+            hip = {"gemm_tflops": round(fl / hip_ms / 1e9, 1), "gemm_ms": round(hip_ms, 4)}
+        except Exception as e:     # a comparator only
+            hip = {"error": f"{type(e).__name__}: {str(e)[:200]}"}
+    del ops
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    gemm_tflops = fl / gemm_ms / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(fl / ms / 1e9, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {"workload": "d12 JiT-T2I image block, FP8 linear path fwd+bwd (recipe native3: qkv_x, proj, "
+                               "w12+SwiGLU+w3; 12 FP8 GEMMs + all casts), one GPU's 32768 tokens",
+                   "tokens": M_TOK, "width": C, "swiglu_hidden": H, "gemm_tflop_per_step": round(fl / 1e12, 4)},
+        "pct_fp8_peak": round(100.0 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_FP8_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_tn_kernel (+ split-K reduce)", "launches_per_step": len(shapes),
+                     "avg_launch_us": round(gemm_ms * 1e3 / len(shapes), 1), "gemm_ms_per_step": round(gemm_ms, 4),
+                     "per_shape": per_shape},
+        "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale", "us": round(cast_ms * 1e3, 2),
+                 "achieved_GBs": round(cast_bytes / cast_ms / 1e6, 1), "peak_GBs": PEAK_HBM_GBS,
+                 "frac": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4),
+                 "algorithmic_bytes": cast_bytes},
+        "hipblaslt_compare": hip,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

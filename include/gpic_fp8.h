@@ -1,0 +1,129 @@
+/*
+ * libgpic_fp8 -- the C ABI of the MI355X (gfx950) FP8 linear path of nano-gpic's JiT-T2I transformer.
+ *
+ * The reference path is baselines/PixelGen/src/models/layers/fp8_native.py (Python + Triton, with the GEMM in
+ * torch._scaled_mm). Each entry point below names the reference interface it replaces. The reference's "FFI" for
+ * this path is torch.library: its ops gpic::fp8_tcast / gpic::fp8_swiglu_tcast / gpic::fp8_swiglu_bwd and the
+ * aten::_scaled_mm call in _mm. The Python package gpic_fp8 registers ops of the same names and schemas over these
+ * functions (ctypes).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer (HBM), except where noted. bf16 tensors are passed as uint16_t bit patterns,
+ *     e4m3fn tensors as uint8_t bytes, scales as one fp32 each.
+ *   - `stream` is a hipStream_t (void * here so this header needs no HIP headers). Work is enqueued on it; nothing
+ *     synchronises with the host, nothing is allocated, and scales stay on the device.
+ *   - `ws` is a caller-provided device workspace of at least the size the matching *_workspace_bytes() returns,
+ *     16-byte aligned. The cast entry points keep no state in it between calls (it never needs zeroing); two calls
+ *     that may run concurrently (different streams) need different workspaces.
+ *   - Tensor data pointers are 16-byte aligned; leading dimensions are in elements.
+ *   - Return value: 0 on success, a negative GPIC_E* code for invalid arguments (nothing was launched), or a positive
+ *     hipError_t from the launch.
+ */
+#ifndef GPIC_FP8_H
+#define GPIC_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPIC_OK 0
+#define GPIC_EINVAL (-1)  /* null pointer, negative size */
+#define GPIC_EDTYPE (-2)  /* unsupported dtype code */
+#define GPIC_ESHAPE (-3)  /* a size or leading dimension breaks the alignment rules (multiples of 16 / 8) */
+#define GPIC_EALIGN (-4)  /* a pointer is not 16-byte aligned */
+#define GPIC_EWORKSPACE (-5) /* the workspace is smaller than required */
+
+#define GPIC_DTYPE_BF16 0
+#define GPIC_DTYPE_F32 1
+
+/* Library version string and a message for a status code (host memory, static). */
+const char *gpic_fp8_version(void);
+const char *gpic_fp8_status_string(int status);
+
+/* Bytes of workspace the cast entry points need (the partial maxima of the amax pass). */
+size_t gpic_fp8_cast_workspace_bytes(void);
+
+/*
+ * Tensorwise current-amax cast to e4m3fn.
+ * Replaces gpic::fp8_tcast (fp8_native.py:114-122: _amax_kernel :33-37, _cast_kernel :40-49, _cast_flat :105-111).
+ *   x        n contiguous elements, bf16 (dtype GPIC_DTYPE_BF16) or fp32 (GPIC_DTYPE_F32)
+ *   q        n bytes: e4m3(min(max(RN(x * scale), -448), 448)), scale = RN(448 / max(amax, 1e-12))
+ *   dequant  1 fp32: RN(max(amax, 1e-12) / 448); amax = max |x| over the non-NaN elements
+ * n == 0 writes only dequant (1e-12 / 448).
+ */
+int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *ws, void *stream);
+
+/*
+ * The same cast of x [rows, cols] (row-major, cols % 16 == 0), writing q [rows, cols] (skipped when q is NULL) and
+ * the transposed bytes qt [cols, ldt] (ldt % 16 == 0, ldt >= rows; columns rows..ldt-1 are written as zero bytes).
+ * Replaces the reference's tcast(w.t().contiguous()) (fp8_native.py:259,262), which has the same amax and therefore
+ * the same bytes transposed; qt is also the K-major operand of the FP8 wgrad (an extension of the reference, whose
+ * wgrads are bf16, fp8_native.py:202,225,264-265).
+ */
+int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,
+                     float *dequant, void *ws, void *stream);
+
+/*
+ * SwiGLU product cast. Replaces gpic::fp8_swiglu_tcast (fp8_native.py:130-144; _swiglu_tile :53-58,
+ * _swiglu_amax_kernel :61-66, _swiglu_cast_kernel :69-78).
+ *   z        [M, 2H] bf16, row stride sz (H % 8 == 0, sz % 8 == 0)
+ *   q        [M, H] e4m3 of a = bf16(bf16(z1 * sigmoid(z1)) * z2), row stride sq (sq % 8 == 0)
+ *   dequant  1 fp32
+ */
+int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, float *dequant,
+                          void *ws, void *stream);
+
+/*
+ * SwiGLU backward with the cast of its output. Replaces gpic::fp8_swiglu_bwd (fp8_native.py:153-166;
+ * _swiglu_bwd_kernel :83-98, then _cast_flat).
+ *   z [M, 2H] (row stride sz), da [M, H] (row stride sda) bf16 ->
+ *   dz [M, 2H] bf16 contiguous, dzq [M, 2H] e4m3 contiguous, dequant 1 fp32
+ */
+int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
+                        uint16_t *dz, uint8_t *dzq, float *dequant, void *ws, void *stream);
+
+/*
+ * gpic_fp8_swiglu_tcast plus the transposed bytes qt [H, ldt] (H % 16 == 0, ldt % 16 == 0, ldt >= M; columns
+ * M..ldt-1 zero): the K-major operand of w3's FP8 wgrad. Same bytes and scale as gpic_fp8_swiglu_tcast.
+ * No counterpart in the reference (its w3 wgrad is bf16, fp8_native.py:225,265); the FP8-wgrad extension.
+ */
+int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, uint8_t *qt,
+                            int64_t ldt, float *dequant, void *ws, void *stream);
+
+/*
+ * gpic_fp8_swiglu_bwd plus the transposed bytes dzqt [2H, ldt] (ldt % 16 == 0, ldt >= M; columns M..ldt-1 zero):
+ * the K-major operand of w12's FP8 wgrad. Same dz, dzq and scale as gpic_fp8_swiglu_bwd.
+ * No counterpart in the reference (its w12 wgrad is bf16, fp8_native.py:264); the FP8-wgrad extension.
+ */
+int gpic_fp8_swiglu_bwd_t(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
+                          uint16_t *dz, uint8_t *dzq, uint8_t *dzqt, int64_t ldt, float *dequant, void *ws,
+                          void *stream);
+
+/* Bytes of workspace gpic_fp8_gemm needs for this problem (0 when it runs without split-K). */
+size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * Scaled FP8 GEMM, "TN": both operands K-contiguous.
+ * Replaces _mm (fp8_native.py:175-178) = torch._scaled_mm(A, B.t(), scale_a, scale_b, out_dtype=bf16), and folds the
+ * bias add of _Fp8Linear.forward (fp8_native.py:189-190) into the epilogue with the same two roundings:
+ *   C[m, n] = bf16(sa * sb * sum_k A[m, k] * B[n, k]);  if bias: C[m, n] = bf16(C[m, n] + bias[n])
+ *   A [M, K] e4m3, row stride lda;  B [N, K] e4m3, row stride ldb;  C [M, N] bf16, row stride ldc
+ *   sa, sb   device fp32 scalars (the dequantization scales);  bias: [N] bf16 or NULL
+ *   K % 16 == 0, N % 16 == 0, lda / ldb % 16 == 0, ldc % 8 == 0; any M.
+ *   fast_accum is accepted for interface parity with use_fast_accum: MFMA accumulates in fp32 either way.
+ * The fp32 accumulation is the MFMA's; the result matches the scaled matmul of the same operands within the
+ * relative Frobenius error the path promises (1e-2), and is deterministic (split-K partials are summed in a fixed
+ * order).
+ */
+int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
+                  const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, int fast_accum,
+                  void *ws, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPIC_FP8_H */

@@ -1,0 +1,84 @@
+"""ctypes boundary to libgpic_fp8.so, the HIP kernels of the FP8 linear path (include/gpic_fp8.h).
+
+There is no CPU path: a missing library, a CPU tensor or a failed launch raises RuntimeError.
+
+torch is imported before the library is opened, so libgpic_fp8.so binds to the HIP runtime torch already loaded
+(both are SONAME libamdhip64.so.7): torch's stream handles and device pointers are valid in our calls.
+"""
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgpic_fp8.so")
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes), exactly the functions declared in include/gpic_fp8.h
+SIGNATURES = {
+    "gpic_fp8_version": (ctypes.c_char_p, []),
+    "gpic_fp8_status_string": (ctypes.c_char_p, [_int]),
+    "gpic_fp8_cast_workspace_bytes": (_sz, []),
+    "gpic_fp8_tcast": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _vp]),
+    "gpic_fp8_tcast_t": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
+    "gpic_fp8_swiglu_tcast": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "gpic_fp8_swiglu_tcast_t": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "gpic_fp8_swiglu_bwd": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "gpic_fp8_swiglu_bwd_t": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+    "gpic_fp8_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "gpic_fp8_gemm": (_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
+}
+
+DTYPE_CODE = {torch.bfloat16: 0, torch.float32: 1}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (opened once). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python nano-gpic_amd/gpic_fp8/build.py` "
+                               "(hipcc, gfx950). The FP8 path has no CPU fallback.")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status, what):
+    if status != 0:
+        msg = lib().gpic_fp8_status_string(status).decode()
+        raise RuntimeError(f"{what} failed: {msg} (status {status})")
+
+
+def require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(f"gpic_fp8 runs on the GPU only (HIP kernels); got a tensor on {t.device}")
+
+
+def stream_ptr(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def aligned(t):
+    """t itself if its storage pointer is 16-byte aligned, else an aligned copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def cast_workspace(device):
+    """Scratch for the partial maxima of one cast (stateless between calls: no zeroing needed)."""
+    n = lib().gpic_fp8_cast_workspace_bytes()
+    return torch.empty(n // 4, dtype=torch.int32, device=device)

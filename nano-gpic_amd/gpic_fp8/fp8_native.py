@@ -1,0 +1,495 @@
+"""Native FP8 linear path for MI355X (gfx950): the module / autograd API of nano-gpic's
+baselines/PixelGen/src/models/layers/fp8_native.py, over hand-written HIP kernels (libgpic_fp8.so, C ABI in
+include/gpic_fp8.h) instead of Triton kernels and torch._scaled_mm.
+
+Numerics (the reference's rules, fp8_native.py:24-49):
+- tensorwise scaling with the current amax (no state across steps): amax = max |x| over the non-NaN elements,
+  a = max(amax, 1e-12), scale = 448 / a and dequant = a / 448, both IEEE-rounded fp32 divisions;
+- q = e4m3fn(min(max(x * scale, -448), 448)), round to nearest even: bit-exact with the reference's cast;
+- the GEMM C = bf16(sa * sb * sum_k A q_k B q_k) with fp32 accumulation (MFMA), the optional bias added afterwards in
+  bf16 (fp8_native.py:189-190), fused into the GEMM epilogue with the same two roundings;
+- the SwiGLU roundings of fp8_native.py:55-58 and 88-94, with this build's sigmoid (see the C header).
+
+Phases (convert_native / convert_fp8 recipes):
+- phase 1 ("native"): forward GEMMs in FP8, backward in bf16 -- as the reference;
+- phase 2 ("native2"): the MLP as one function with FP8 dgrads, bf16 wgrads -- as the reference;
+- phase 3 ("native3", an extension): every forward, dgrad and wgrad GEMM of qkv_x, proj, w12 and w3 in FP8. The
+  forward keeps the e4m3 bytes of its inputs (transposed, K-major) for the wgrad instead of the bf16 inputs.
+"""
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+E4 = torch.float8_e4m3fn
+FMAX = 448.0          # the largest finite e4m3fn value
+TINY = 1e-12          # an all-zero tensor keeps scale FMAX / TINY: its values stay 0
+
+
+def _r16(n):
+    return (n + 15) // 16 * 16
+
+
+def _prep(x):
+    """x as a contiguous, 16-byte aligned bf16 or fp32 tensor (other float dtypes are widened to fp32 exactly as the
+    reference's in-kernel .to(tl.float32) does)."""
+    if x.dtype not in L.DTYPE_CODE:
+        x = x.float()
+    return L.aligned(x.contiguous())
+
+
+def _prep_rows(t, min_cols):
+    """A 2-D tensor whose rows are unit-stride, 16-byte aligned and with a row stride that is a multiple of 8 elements;
+    else a contiguous aligned copy."""
+    if t.stride(-1) != 1 or t.stride(0) % 8 != 0 or t.stride(0) < min_cols or t.data_ptr() % 16 != 0:
+        t = L.aligned(t.contiguous())
+    return t
+
+
+# ------------------------------------------------------------------------------------------------ casts
+
+@torch.library.custom_op("gpic::fp8_tcast", mutates_args=())
+def tcast(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x (any float dtype) -> e4m3 (contiguous, x's shape) and its tensorwise dequantization scale amax / 448 [1] fp32.
+    (fp8_native.py:114-122)"""
+    L.require_gpu(x)
+    xc = _prep(x)
+    q = torch.empty(x.shape, dtype=E4, device=x.device)
+    s = torch.empty(1, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        ws = L.cast_workspace(x.device)
+        L.check(L.lib().gpic_fp8_tcast(xc.data_ptr(), L.DTYPE_CODE[xc.dtype], xc.numel(), q.data_ptr(), s.data_ptr(),
+                                       ws.data_ptr(), L.stream_ptr(x.device)), "gpic_fp8_tcast")
+    return q, s
+
+
+@tcast.register_fake
+def _(x):
+    return x.new_empty(x.shape, dtype=E4), x.new_empty(1, dtype=torch.float32)
+
+
+@torch.library.custom_op("gpic::fp8_tcast_t", mutates_args=())
+def tcast_t(x: torch.Tensor, want_q: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x [R, C] (any float dtype, C % 16 == 0) -> (q [R, C] e4m3, or an empty tensor when want_q is False;
+    qt [C, R16] e4m3 = q transposed, R16 = R rounded up to 16, zero bytes in columns R..R16-1; dequant [1] fp32).
+    The same bytes and scale as tcast(x) (and as the reference's tcast(x.t().contiguous()), fp8_native.py:259)."""
+    L.require_gpu(x)
+    if x.dim() != 2 or x.shape[1] % 16:
+        raise ValueError(f"tcast_t needs a 2-D tensor with a multiple of 16 columns, got {tuple(x.shape)}")
+    xc = _prep(x)
+    R, C = xc.shape
+    q = torch.empty((R, C) if want_q else (0,), dtype=E4, device=x.device)
+    qt = torch.empty(C, _r16(R), dtype=E4, device=x.device)
+    s = torch.empty(1, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        ws = L.cast_workspace(x.device)
+        L.check(L.lib().gpic_fp8_tcast_t(xc.data_ptr(), L.DTYPE_CODE[xc.dtype], R, C, q.data_ptr() if want_q else None,
+                                         qt.data_ptr(), qt.shape[1], s.data_ptr(), ws.data_ptr(),
+                                         L.stream_ptr(x.device)), "gpic_fp8_tcast_t")
+    return q, qt, s
+
+
+@tcast_t.register_fake
+def _(x, want_q=True):
+    R, C = x.shape
+    return (x.new_empty((R, C) if want_q else (0,), dtype=E4), x.new_empty(C, _r16(R), dtype=E4),
+            x.new_empty(1, dtype=torch.float32))
+
+
+def _swiglu_prep(z):
+    L.require_gpu(z)
+    if z.dim() != 2 or z.shape[1] % 2 or (z.shape[1] // 2) % 8:
+        raise ValueError(f"the SwiGLU kernels need z [M, 2H] with H % 8 == 0, got {tuple(z.shape)}")
+    if z.dtype != torch.bfloat16:
+        raise ValueError(f"the SwiGLU kernels take bf16 z (w12's output), got {z.dtype}")
+    return _prep_rows(z, z.shape[1])
+
+
+@torch.library.custom_op("gpic::fp8_swiglu_tcast", mutates_args=())
+def swiglu_tcast(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """z [M, 2H] bf16 (w12's output) -> silu(z1) * z2 as e4m3 [M, H] and its tensorwise scale [1] fp32.
+    (fp8_native.py:130-144)"""
+    zc = _swiglu_prep(z)
+    M, H2 = zc.shape
+    H = H2 // 2
+    q = torch.empty(M, H, dtype=E4, device=z.device)
+    s = torch.empty(1, dtype=torch.float32, device=z.device)
+    with torch.cuda.device(z.device):
+        ws = L.cast_workspace(z.device)
+        L.check(L.lib().gpic_fp8_swiglu_tcast(zc.data_ptr(), M, H, zc.stride(0), q.data_ptr(), q.stride(0),
+                                              s.data_ptr(), ws.data_ptr(), L.stream_ptr(z.device)),
+                "gpic_fp8_swiglu_tcast")
+    return q, s
+
+
+@swiglu_tcast.register_fake
+def _(z):
+    M, H2 = z.shape
+    return z.new_empty(M, H2 // 2, dtype=E4), z.new_empty(1, dtype=torch.float32)
+
+
+@torch.library.custom_op("gpic::fp8_swiglu_tcast_t", mutates_args=())
+def swiglu_tcast_t(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """swiglu_tcast plus the transposed bytes qt [H, M16] (zero past M): the K-major operand of w3's FP8 wgrad."""
+    zc = _swiglu_prep(z)
+    M, H2 = zc.shape
+    H = H2 // 2
+    if H % 16:
+        raise ValueError(f"swiglu_tcast_t needs H % 16 == 0, got H = {H}")
+    q = torch.empty(M, H, dtype=E4, device=z.device)
+    qt = torch.empty(H, _r16(M), dtype=E4, device=z.device)
+    s = torch.empty(1, dtype=torch.float32, device=z.device)
+    with torch.cuda.device(z.device):
+        ws = L.cast_workspace(z.device)
+        L.check(L.lib().gpic_fp8_swiglu_tcast_t(zc.data_ptr(), M, H, zc.stride(0), q.data_ptr(), q.stride(0),
+                                                qt.data_ptr(), qt.shape[1], s.data_ptr(), ws.data_ptr(),
+                                                L.stream_ptr(z.device)), "gpic_fp8_swiglu_tcast_t")
+    return q, qt, s
+
+
+@swiglu_tcast_t.register_fake
+def _(z):
+    M, H2 = z.shape
+    return (z.new_empty(M, H2 // 2, dtype=E4), z.new_empty(H2 // 2, _r16(M), dtype=E4),
+            z.new_empty(1, dtype=torch.float32))
+
+
+def _bwd_prep(z, da):
+    zc = _swiglu_prep(z)
+    M, H2 = zc.shape
+    if da.shape != (M, H2 // 2) or da.dtype != torch.bfloat16:
+        raise ValueError(f"da must be bf16 [{M}, {H2 // 2}], got {da.dtype} {tuple(da.shape)}")
+    L.require_gpu(da)
+    return zc, _prep_rows(da, H2 // 2)
+
+
+@torch.library.custom_op("gpic::fp8_swiglu_bwd", mutates_args=())
+def swiglu_bwd(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """z [M, 2H] bf16, da [M, H] bf16 -> dz [M, 2H] bf16, dz as e4m3 [M, 2H] and its tensorwise scale [1] fp32.
+    (fp8_native.py:153-166)"""
+    zc, dac = _bwd_prep(z, da)
+    M, H2 = zc.shape
+    dz = torch.empty(M, H2, dtype=torch.bfloat16, device=z.device)
+    dq = torch.empty(M, H2, dtype=E4, device=z.device)
+    s = torch.empty(1, dtype=torch.float32, device=z.device)
+    with torch.cuda.device(z.device):
+        ws = L.cast_workspace(z.device)
+        L.check(L.lib().gpic_fp8_swiglu_bwd(zc.data_ptr(), dac.data_ptr(), M, H2 // 2, zc.stride(0), dac.stride(0),
+                                            dz.data_ptr(), dq.data_ptr(), s.data_ptr(), ws.data_ptr(),
+                                            L.stream_ptr(z.device)), "gpic_fp8_swiglu_bwd")
+    return dz, dq, s
+
+
+@swiglu_bwd.register_fake
+def _(z, da):
+    M, H2 = z.shape
+    return z.new_empty(M, H2), z.new_empty(M, H2, dtype=E4), z.new_empty(1, dtype=torch.float32)
+
+
+@torch.library.custom_op("gpic::fp8_swiglu_bwd_t", mutates_args=())
+def swiglu_bwd_t(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """swiglu_bwd plus the transposed bytes dzqt [2H, M16] (zero past M): the K-major operand of w12's FP8 wgrad."""
+    zc, dac = _bwd_prep(z, da)
+    M, H2 = zc.shape
+    dz = torch.empty(M, H2, dtype=torch.bfloat16, device=z.device)
+    dq = torch.empty(M, H2, dtype=E4, device=z.device)
+    dqt = torch.empty(H2, _r16(M), dtype=E4, device=z.device)
+    s = torch.empty(1, dtype=torch.float32, device=z.device)
+    with torch.cuda.device(z.device):
+        ws = L.cast_workspace(z.device)
+        L.check(L.lib().gpic_fp8_swiglu_bwd_t(zc.data_ptr(), dac.data_ptr(), M, H2 // 2, zc.stride(0), dac.stride(0),
+                                              dz.data_ptr(), dq.data_ptr(), dqt.data_ptr(), dqt.shape[1], s.data_ptr(),
+                                              ws.data_ptr(), L.stream_ptr(z.device)), "gpic_fp8_swiglu_bwd_t")
+    return dz, dq, dqt, s
+
+
+@swiglu_bwd_t.register_fake
+def _(z, da):
+    M, H2 = z.shape
+    return (z.new_empty(M, H2), z.new_empty(M, H2, dtype=E4), z.new_empty(H2, _r16(M), dtype=E4),
+            z.new_empty(1, dtype=torch.float32))
+
+
+# ------------------------------------------------------------------------------------------------ GEMM
+
+def _gemm_operand(t, name):
+    if t.dtype != E4 or t.dim() != 2:
+        raise ValueError(f"{name} must be a 2-D float8_e4m3fn tensor, got {t.dtype} {tuple(t.shape)}")
+    if t.stride(1) != 1 or t.stride(0) % 16 or t.stride(0) < t.shape[1] or t.data_ptr() % 16:
+        t = L.aligned(t.contiguous())
+    return t
+
+
+@torch.library.custom_op("gpic::fp8_gemm", mutates_args=())
+def fp8_gemm(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
+             bias: Optional[torch.Tensor] = None, fast: bool = True) -> torch.Tensor:
+    """a [M, K] e4m3, b [N, K] e4m3 (both K-contiguous), sa / sb [1] fp32 dequantization scales ->
+    C [M, N] bf16 = bf16(sa * sb * a @ b^T), then bf16(C + bias) when bias [N] is given.
+    Replaces torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=bf16) of _mm (fp8_native.py:175-178) and the
+    bias add of _Fp8Linear.forward (:189-190). `fast` (use_fast_accum) changes nothing: MFMA accumulates in fp32."""
+    L.require_gpu(a, b, sa, sb, bias)
+    a = _gemm_operand(a, "a")
+    b = _gemm_operand(b, "b")
+    M, K = a.shape
+    N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError(f"fp8_gemm: a is [{M}, {K}] but b is {tuple(b.shape)}")
+    if K % 16 or N % 16:
+        raise ValueError(f"fp8_gemm needs K % 16 == 0 and N % 16 == 0, got M={M} N={N} K={K}")
+    sa = sa.to(torch.float32).reshape(1)
+    sb = sb.to(torch.float32).reshape(1)
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+        if bias.numel() != N:
+            raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
+        bias = bias if bias.data_ptr() % 8 == 0 else bias.clone()
+    c = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    with torch.cuda.device(a.device):
+        nws = L.lib().gpic_fp8_gemm_workspace_bytes(M, N, K)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=a.device) if nws else None
+        L.check(L.lib().gpic_fp8_gemm(a.data_ptr(), a.stride(0), sa.data_ptr(), b.data_ptr(), b.stride(0),
+                                      sb.data_ptr(), L.ptr(bias), c.data_ptr(), c.stride(0), M, N, K, int(fast),
+                                      L.ptr(ws), nws, L.stream_ptr(a.device)), "gpic_fp8_gemm")
+    return c
+
+
+@fp8_gemm.register_fake
+def _(a, sa, b, sb, bias=None, fast=True):
+    return a.new_empty(a.shape[0], b.shape[0], dtype=torch.bfloat16)
+
+
+def _mm(xq, sx, wq, sw, fast=True):
+    """[M, K] e4m3 x [N, K] e4m3 (each with its tensorwise scale) -> [M, N] bf16 (fp8_native.py:175-178)."""
+    return fp8_gemm(xq, sx, wq, sw, None, fast)
+
+
+# ------------------------------------------------------------------------------------------------ autograd
+
+class _Fp8Linear(torch.autograd.Function):
+    """fp8_native.py:181-204: FP8 forward GEMM; bf16 dgrad and wgrad from the saved bf16 input and weight."""
+    @staticmethod
+    def forward(ctx, x, w, b):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        xq, sx = tcast(x2)
+        wq, sw = tcast(w)
+        y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
+        ctx.save_for_backward(x2, w)
+        ctx.has_b, ctx.shape, ctx.wdt = b is not None, shape, w.dtype
+        return y.view(*shape[:-1], w.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
+        dx = (dy2 @ w.to(torch.bfloat16)).view(ctx.shape)
+        dw = (dy2.t() @ x2).to(ctx.wdt)
+        db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
+        return dx, dw, db
+
+
+class _Fp8LinearF8(torch.autograd.Function):
+    """Phase 3: forward, dgrad and wgrad GEMMs all in FP8. The forward keeps x's e4m3 bytes transposed (K-major over
+    the tokens, the wgrad's B operand) and w's transposed bytes (the dgrad's B operand) instead of bf16 copies."""
+    @staticmethod
+    def forward(ctx, x, w, b):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        xq, xqt, sx = tcast_t(x2)
+        wq, wqt, sw = tcast_t(w)
+        y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
+        ctx.save_for_backward(xqt, sx, wqt, sw)
+        ctx.has_b, ctx.shape, ctx.wdt = b is not None, shape, w.dtype
+        return y.view(*shape[:-1], w.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        xqt, sx, wqt, sw = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
+        dyq, dyqt, sdy = tcast_t(dy2)
+        dx = fp8_gemm(dyq, sdy, wqt, sw, None, False).view(ctx.shape)     # [M, N] . [K, N]^T
+        dw = fp8_gemm(dyqt, sdy, xqt, sx, None, False).to(ctx.wdt)      # [N, M16] . [K, M16]^T
+        db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
+        return dx, dw, db
+
+
+class _SwiGLUw3(torch.autograd.Function):
+    """y = w3(silu(z1) * z2), the product written as FP8 rows for the GEMM (fp8_native.py:207-232)."""
+    @staticmethod
+    def forward(ctx, z, w3):
+        shape = z.shape
+        z2d = z.reshape(-1, shape[-1])
+        aq, sa = swiglu_tcast(z2d)
+        wq, sw = tcast(w3)
+        y = _mm(aq, sa, wq, sw)
+        ctx.save_for_backward(z2d, aq, sa, w3)
+        ctx.shape, ctx.wdt = shape, w3.dtype
+        return y.view(*shape[:-1], w3.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        z, aq, sa, w3 = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
+        da = dy2 @ w3.to(torch.bfloat16)
+        dw3 = (dy2.t() @ (aq.to(torch.float32) * sa).to(torch.bfloat16)).to(ctx.wdt)
+        z1, z2 = z.chunk(2, dim=-1)
+        z1f = z1.float()
+        sg = torch.sigmoid(z1f)
+        sl = (z1f * sg).to(torch.bfloat16)
+        dz2 = da * sl
+        dz1 = (da.float() * z2.float() * (sg * (1 + z1f * (1 - sg)))).to(torch.bfloat16)
+        return torch.cat([dz1, dz2], dim=-1).view(ctx.shape), dw3
+
+
+class _Fp8MLP(torch.autograd.Function):
+    """Phase 2 (fp8_native.py:235-266): the whole SwiGLU MLP, FP8 forward GEMMs and FP8 dgrads of w3 and w12; the
+    SwiGLU backward kernel writes dz in bf16 (w12's weight gradient) and its FP8 copy (w12's dgrad); weight
+    gradients in bf16. The weights' FP8 copies for the dgrads are the transposed casts."""
+    @staticmethod
+    def forward(ctx, x, w12, w3):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        xq, sx = tcast(x2)
+        w12q, s12 = tcast(w12)
+        z = _mm(xq, sx, w12q, s12)
+        aq, sa = swiglu_tcast(z)
+        w3q, s3 = tcast(w3)
+        y = _mm(aq, sa, w3q, s3)
+        ctx.save_for_backward(x2, z, aq, sa, w12, w3)
+        ctx.shape, ctx.dt = shape, (w12.dtype, w3.dtype)
+        return y.view(*shape[:-1], w3.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, z, aq, sa, w12, w3 = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
+        dyq, sdy = tcast(dy2)
+        _, w3tq, s3t = tcast_t(w3, False)                  # [H, C]: the dgrad's B operand
+        da = _mm(dyq, sdy, w3tq, s3t, fast=False)          # [M, H]
+        dz, dzq, sdz = swiglu_bwd(z, da)
+        _, w12tq, s12t = tcast_t(w12, False)               # [C, 2H]
+        dx = _mm(dzq, sdz, w12tq, s12t, fast=False)        # [M, C]
+        dw12 = (dz.t() @ x2).to(ctx.dt[0])
+        dw3 = (dy2.t() @ (aq.to(torch.float32) * sa).to(torch.bfloat16)).to(ctx.dt[1])
+        return dx.view(ctx.shape), dw12, dw3
+
+
+class _Fp8MLPF8(torch.autograd.Function):
+    """Phase 3: the SwiGLU MLP with every GEMM in FP8 -- forward, both dgrads and both wgrads. The forward saves x's
+    and the SwiGLU product's transposed e4m3 bytes (the wgrads' K-major operands), z, and the weights' transposed
+    bytes (the dgrads' B operands)."""
+    @staticmethod
+    def forward(ctx, x, w12, w3):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        xq, xqt, sx = tcast_t(x2)
+        w12q, w12qt, s12 = tcast_t(w12)
+        z = fp8_gemm(xq, sx, w12q, s12)
+        aq, aqt, sa = swiglu_tcast_t(z)
+        w3q, w3qt, s3 = tcast_t(w3)
+        y = fp8_gemm(aq, sa, w3q, s3)
+        ctx.save_for_backward(xqt, sx, z, aqt, sa, w12qt, s12, w3qt, s3)
+        ctx.shape, ctx.dt = shape, (w12.dtype, w3.dtype)
+        return y.view(*shape[:-1], w3.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        xqt, sx, z, aqt, sa, w12qt, s12, w3qt, s3 = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
+        dyq, dyqt, sdy = tcast_t(dy2)
+        da = fp8_gemm(dyq, sdy, w3qt, s3, None, False)           # [M, H]
+        dw3 = fp8_gemm(dyqt, sdy, aqt, sa, None, False)          # [C, H]
+        _, dzq, dzqt, sdz = swiglu_bwd_t(z, da)
+        dx = fp8_gemm(dzq, sdz, w12qt, s12, None, False)         # [M, C]
+        dw12 = fp8_gemm(dzqt, sdz, xqt, sx, None, False)         # [2H, C]
+        return dx.view(ctx.shape), dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1])
+
+
+def fp8_mlp(x, w12, w3):
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8MLP.apply(x.to(torch.bfloat16), w12, w3)
+
+
+def fp8_linear(x, w, b=None):
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8Linear.apply(x.to(torch.bfloat16), w, b)
+
+
+def fp8_swiglu_w3(z, w3):
+    with torch.autocast("cuda", enabled=False):
+        return _SwiGLUw3.apply(z.to(torch.bfloat16), w3)
+
+
+def fp8_linear_f8(x, w, b=None):
+    """Phase 3 fp8_linear: FP8 dgrad and wgrad as well."""
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b)
+
+
+def fp8_mlp_f8(x, w12, w3):
+    """Phase 3 fp8_mlp: every GEMM of the SwiGLU MLP in FP8."""
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8MLPF8.apply(x.to(torch.bfloat16), w12, w3)
+
+
+class Fp8Linear(torch.nn.Linear):
+    """nn.Linear with the FP8 forward GEMM (the same parameters and state-dict keys)."""
+    def forward(self, x):
+        return fp8_linear(x, self.weight, self.bias)
+
+
+class Fp8LinearF8(torch.nn.Linear):
+    """nn.Linear with FP8 forward, dgrad and wgrad GEMMs (phase 3; the same parameters and state-dict keys)."""
+    def forward(self, x):
+        return fp8_linear_f8(x, self.weight, self.bias)
+
+
+def convert_native(net, phase=1):
+    """Phase 1: the image blocks' qkv_x, proj, w12 to Fp8Linear and their SwiGLU's w3 GEMM to the fused path. Phase 2:
+    qkv_x and proj as in phase 1, the MLP as one fused FP8 function with FP8 dgrads. Phase 3: qkv_x and proj to
+    Fp8LinearF8, the MLP as one function with every GEMM in FP8. Returns the count of GEMMs converted
+    (fp8_native.py:290-317)."""
+    n = 0
+    for blk in getattr(net, "blocks", []):
+        if phase >= 2:
+            lin_cls = Fp8LinearF8 if phase >= 3 else Fp8Linear
+            mlp_fn = fp8_mlp_f8 if phase >= 3 else fp8_mlp
+            for name in ("qkv_x", "proj"):
+                lin = getattr(blk.attn, name)
+                if type(lin) is torch.nn.Linear:
+                    lin.__class__ = lin_cls
+                    n += 1
+            mlp = blk.mlp
+            if not getattr(mlp, "_fp8", False):
+                mlp._fp8 = True
+                mlp.forward = (lambda m, f: (lambda x: f(x, m.w12.weight, m.w3.weight)))(mlp, mlp_fn)
+                n += 2
+            continue
+        for parent, name in ((blk.attn, "qkv_x"), (blk.attn, "proj"), (blk.mlp, "w12")):
+            lin = getattr(parent, name)
+            if type(lin) is torch.nn.Linear:
+                lin.__class__ = Fp8Linear
+                n += 1
+        mlp = blk.mlp
+        if not getattr(mlp, "_fp8", False):
+            mlp._fp8 = True
+            mlp.forward = (lambda m: (lambda x: fp8_swiglu_w3(m.w12(x), m.w3.weight)))(mlp)
+            n += 1
+    return n
+
+
+def reference(x, w, b=None):
+    """The tensorwise FP8 forward in plain torch ops (tests); fp8_native.py:320-331 as written, including its eager
+    FMAX / a (torch computes it as reciprocal(a) * 448, which can differ from the kernels' IEEE 448 / a in the last
+    bit of the scale)."""
+    def q(t):
+        a = t.float().abs().amax().clamp_min(TINY)
+        return (t.float() * (FMAX / a)).clamp(-FMAX, FMAX).to(E4), a / FMAX
+    x2 = x.reshape(-1, x.shape[-1])
+    xq, sx = q(x2)
+    wq, sw = q(w)
+    y = (xq.float() * sx) @ (wq.float() * sw).t()
+    if b is not None:
+        y = y + b.float()
+    return y.to(torch.bfloat16).view(*x.shape[:-1], w.shape[0])

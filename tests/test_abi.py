@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports exactly what include/gpic_fp8.h declares; argument validation returns the
+documented status codes before anything is launched (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from gpic_fp8 import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gpic_fp8.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    return set(re.findall(r"^(?:int|size_t|const char \*)\s*(gpic_fp8_\w+)\(", src, flags=re.M))
+
+
+def test_header_declares_the_bound_functions():
+    assert declared() == set(L.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.gpic_fp8_version().startswith(b"gpic_fp8")
+
+
+def test_status_strings():
+    lib = L.lib()
+    for code in (0, -1, -2, -3, -4, -5):
+        assert lib.gpic_fp8_status_string(code)
+    assert lib.gpic_fp8_status_string(-99) == b"unknown status"
+
+
+def test_cast_workspace_size():
+    assert L.lib().gpic_fp8_cast_workspace_bytes() >= 4096
+
+
+def test_validation_codes():
+    lib = L.lib()
+    ws = ctypes.create_string_buffer(4096 + 16)
+    wsp = (ctypes.addressof(ws) + 15) // 16 * 16
+    # negative size / null output
+    assert lib.gpic_fp8_tcast(None, 0, -1, None, wsp, wsp, None) == -1
+    assert lib.gpic_fp8_tcast(None, 0, 0, None, None, wsp, None) == -1
+    # unsupported dtype
+    assert lib.gpic_fp8_tcast(wsp, 7, 16, wsp, wsp, wsp, None) == -2
+    # misaligned input
+    assert lib.gpic_fp8_tcast(wsp + 2, 0, 16, wsp, wsp, wsp, None) == -4
+    # transposing cast: columns must be a multiple of 16, ldt >= rows
+    assert lib.gpic_fp8_tcast_t(wsp, 0, 4, 24, wsp, wsp, 16, wsp, wsp, None) == -3
+    assert lib.gpic_fp8_tcast_t(wsp, 0, 40, 32, wsp, wsp, 32, wsp, wsp, None) == -3
+    # SwiGLU: H % 8, strides
+    assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 12, 24, wsp, 12, wsp, wsp, None) == -3
+    assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 16, 16, wsp, 16, wsp, wsp, None) == -3
+    assert lib.gpic_fp8_swiglu_bwd(wsp, wsp, 4, 16, 32, 8, wsp, wsp, wsp, wsp, None) == -3
+    assert lib.gpic_fp8_swiglu_tcast_t(wsp, 40, 16, 32, wsp, 16, wsp, 32, wsp, wsp, None) == -3
+    # GEMM: K % 16, N % 16, leading dimensions, null scales
+    g = lib.gpic_fp8_gemm
+    assert g(wsp, 24, wsp, wsp, 24, wsp, None, wsp, 16, 4, 16, 24, 1, None, 0, None) == -3
+    assert g(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 24, 4, 24, 32, 1, None, 0, None) == -3
+    assert g(wsp, 16, wsp, wsp, 32, wsp, None, wsp, 16, 4, 16, 32, 1, None, 0, None) == -3
+    assert g(wsp, 32, None, wsp, 32, wsp, None, wsp, 16, 4, 16, 32, 1, None, 0, None) == -1
+    # empty output: nothing to do
+    assert g(None, 32, wsp, None, 32, wsp, None, None, 16, 0, 16, 32, 1, None, 0, None) == 0
+
+
+def test_loader_fails_loudly_without_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(L, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        L.lib()

@@ -1,0 +1,123 @@
+"""Host-side logic of the drop-in API: the converters (GEMM counts, state-dict keys, phases), the torchao recipe
+guard, the op registrations and fake kernels, the refusal of CPU tensors, and the reference() helper."""
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import gpic_fp8 as G
+from gpic_fp8 import fp8_native as F
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+
+
+class Attn(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.qkv_x = nn.Linear(d, 3 * d, bias=False)
+        self.kv_y = nn.Linear(d, 2 * d, bias=False)
+        self.proj = nn.Linear(d, d)
+
+
+class SwiGLU(nn.Module):
+    """baselines/PixelGen/src/models/layers/swiglu.py:4-15"""
+    def __init__(self, d, h):
+        super().__init__()
+        self.w12 = nn.Linear(d, 2 * h, bias=False)
+        self.w3 = nn.Linear(h, d, bias=False)
+
+    def forward(self, x):
+        x1, x2 = self.w12(x).chunk(2, dim=-1)
+        return self.w3(torch.nn.functional.silu(x1) * x2)
+
+
+class Block(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.attn = Attn(d)
+        self.mlp = SwiGLU(d, 4 * d)
+        self.adaLN_modulation = nn.Sequential(nn.Linear(d, 6 * d))
+
+
+class Net(nn.Module):
+    def __init__(self, d=32, n=3):
+        super().__init__()
+        self.blocks = nn.ModuleList(Block(d) for _ in range(n))
+        self.text_refine_blocks = nn.ModuleList(Block(d) for _ in range(1))
+
+
+@pytest.mark.parametrize("phase,per_block", [(1, 4), (2, 4), (3, 4)])
+def test_convert_native_counts_and_keys(phase, per_block):
+    net = Net()
+    keys = set(net.state_dict())
+    assert G.convert_native(net, phase=phase) == 3 * per_block
+    assert set(net.state_dict()) == keys
+    assert G.convert_native(net, phase=phase) == 0          # idempotent
+    lin = {1: G.Fp8Linear, 2: G.Fp8Linear, 3: G.Fp8LinearF8}[phase]
+    for b in net.blocks:
+        assert type(b.attn.qkv_x) is lin and type(b.attn.proj) is lin
+        assert type(b.attn.kv_y) is nn.Linear and type(b.adaLN_modulation[0]) is nn.Linear
+        assert b.mlp._fp8
+        assert (type(b.mlp.w12) is G.Fp8Linear) == (phase == 1)
+    for b in net.text_refine_blocks:                          # image blocks only (fp8_native.py:294)
+        assert type(b.attn.qkv_x) is nn.Linear
+
+
+def test_convert_fp8_recipes(capsys):
+    for recipe, n in (("native", 12), ("native2", 12), ("native3", 12)):
+        assert G.convert_fp8(Net(), recipe) == n
+    assert "GEMMs of the image blocks converted" in capsys.readouterr().out
+    with pytest.raises(ImportError):
+        G.convert_fp8(Net(), "tensorwise")
+
+
+def test_fp8_filter():
+    net = Net(d=32)
+    names = {n for n, m in net.named_modules() if G.fp8_filter(m, n)}
+    assert "blocks.0.attn.qkv_x" in names and "text_refine_blocks.0.mlp.w3" in names
+    assert not any("adaLN" in n for n in names)
+    assert not G.fp8_filter(nn.Linear(24, 32), "blocks.0.x")
+
+
+def test_ops_registered_with_reference_schemas():
+    assert str(torch.ops.gpic.fp8_tcast.default._schema).startswith("gpic::fp8_tcast(Tensor x) -> (Tensor, Tensor)")
+    assert "gpic::fp8_swiglu_tcast(Tensor z)" in str(torch.ops.gpic.fp8_swiglu_tcast.default._schema)
+    assert "gpic::fp8_swiglu_bwd(Tensor z, Tensor da)" in str(torch.ops.gpic.fp8_swiglu_bwd.default._schema)
+
+
+def test_fake_kernels_shapes():
+    m = torch.empty(40, 48, device="meta", dtype=torch.bfloat16)
+    q, s = torch.ops.gpic.fp8_tcast(m)
+    assert q.shape == (40, 48) and q.dtype == torch.float8_e4m3fn and s.shape == (1,)
+    q, qt, s = torch.ops.gpic.fp8_tcast_t(m)
+    assert qt.shape == (48, 48)
+    z = torch.empty(8, 64, device="meta", dtype=torch.bfloat16)
+    q, s = torch.ops.gpic.fp8_swiglu_tcast(z)
+    assert q.shape == (8, 32)
+    dz, dq, s = torch.ops.gpic.fp8_swiglu_bwd(z, torch.empty(8, 32, device="meta", dtype=torch.bfloat16))
+    assert dz.shape == (8, 64) and dq.dtype == torch.float8_e4m3fn
+    a = torch.empty(8, 32, device="meta", dtype=torch.float8_e4m3fn)
+    b = torch.empty(16, 32, device="meta", dtype=torch.float8_e4m3fn)
+    c = torch.ops.gpic.fp8_gemm(a, torch.empty(1, device="meta"), b, torch.empty(1, device="meta"))
+    assert c.shape == (8, 16) and c.dtype == torch.bfloat16
+
+
+def test_cpu_tensors_are_refused():
+    x = torch.randn(16, 16, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        G.tcast(x)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        G.fp8_linear(x, torch.randn(16, 16))
+
+
+def test_reference_helper_matches_golden():
+    """reference() (plain torch, CPU-capable) is within bf16 rounding of the IEEE-scale golden linear."""
+    with np.load(GOLD, allow_pickle=False) as g:
+        x = torch.from_numpy(g["lin_x"].view(np.int16)).view(torch.bfloat16)
+        w = torch.from_numpy(g["lin_w"].view(np.int16)).view(torch.bfloat16)
+        b = torch.from_numpy(g["lin_b"].view(np.int16)).view(torch.bfloat16)
+        y = torch.from_numpy(g["lin_y"].view(np.int16)).view(torch.bfloat16)
+    r = G.reference(x, w, b).float()
+    assert torch.linalg.norm(r - y.float()) / torch.linalg.norm(y.float()) < 1e-2

@@ -1,0 +1,200 @@
+"""The drop-in autograd API on the GPU: Fp8Linear / fp8_linear / fp8_swiglu_w3 / fp8_mlp (phases 1 and 2, as the
+reference) and the phase-3 all-FP8 functions, against the golden vectors and against fp32 autograd of the same
+dequantized formulas (tolerance 1e-2 relative Frobenius), plus convert_native on a small model."""
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import gpic_fp8 as G
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+TOL = 1e-2
+
+
+def rel(x, ref):
+    x, ref = x.float(), ref.float()
+    return (torch.linalg.norm(x - ref) / torch.linalg.norm(ref)).item()
+
+
+def deq(q, s):
+    return q.float() * s
+
+
+@pytest.fixture(autouse=True)
+def no_tf32():
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+
+def test_linear_forward_golden(dev):
+    with np.load(GOLD, allow_pickle=False) as g:
+        t = {k: torch.from_numpy(g[k].view(np.int16)).view(torch.bfloat16).to(dev)
+             for k in ("lin_x", "lin_w", "lin_b", "lin_y")}
+    y = G.fp8_linear(t["lin_x"], t["lin_w"], t["lin_b"])
+    assert rel(y, t["lin_y"]) < 5e-3
+    y3 = G.fp8_linear_f8(t["lin_x"], t["lin_w"], t["lin_b"])
+    assert torch.equal(y, y3)                               # phases share the forward bit for bit
+
+
+def test_linear_phase1_backward_is_the_references(dev):
+    """Phase 1 backward = bf16 matmuls of the saved bf16 input and weight (fp8_native.py:198-204)."""
+    x = torch.randn(4, 64, 256, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    w = (torch.randn(512, 256, device=dev) / 16).requires_grad_()           # fp32 master weight (DDP)
+    b = torch.zeros(512, device=dev, requires_grad=True)
+    y = G.fp8_linear(x, w, b)
+    assert y.dtype == torch.bfloat16 and y.shape == (4, 64, 512)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    dy2 = dy.reshape(-1, 512)
+    assert torch.equal(x.grad, (dy2 @ w.detach().to(torch.bfloat16)).view(4, 64, 256))
+    assert torch.equal(w.grad, (dy2.t() @ x.detach().reshape(-1, 256)).float())
+    assert torch.equal(b.grad, dy2.sum(0).float())
+
+
+def test_linear_phase3_all_fp8(dev):
+    M, K, N = 1024, 512, 768
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16).requires_grad_()
+    w = (torch.randn(N, K, device=dev) / K ** 0.5).to(torch.bfloat16).requires_grad_()
+    b = (torch.randn(N, device=dev) * 0.1).to(torch.bfloat16).requires_grad_()
+    y = G.fp8_linear_f8(x, w, b)
+    dy = (torch.randn(M, N, device=dev) * 0.1).to(torch.bfloat16)
+    y.backward(dy)
+    # the same quantized operands, fp32 products
+    xq, sx = G.tcast(x.detach())
+    wq, sw = G.tcast(w.detach())
+    dyq, sdy = G.tcast(dy)
+    assert rel(x.grad, deq(dyq, sdy) @ deq(wq, sw)) < 4e-3
+    assert rel(w.grad, deq(dyq, sdy).t() @ deq(xq, sx)) < 4e-3
+    assert torch.equal(b.grad, dy.sum(0).to(torch.bfloat16))
+    # and close to the unquantized bf16 gradients
+    assert rel(x.grad, dy.float() @ w.detach().float()) < 0.1
+
+
+def _mlp_ref(x, w12, w3):
+    """fp32 autograd of the SwiGLU MLP with the FP8 forward's quantization points (for the phase-3 gradients)."""
+    xf = x.float().requires_grad_()
+    w12f = w12.float().requires_grad_()
+    w3f = w3.float().requires_grad_()
+    z = xf @ w12f.t()
+    z1, z2 = z.chunk(2, -1)
+    y = (torch.nn.functional.silu(z1) * z2) @ w3f.t()
+    return xf, w12f, w3f, y
+
+
+@pytest.mark.parametrize("fn", ["fp8_mlp", "fp8_mlp_f8"])
+def test_mlp_phases(dev, fn):
+    M, C, H = 1024, 256, 1024
+    x = torch.randn(M, C, device=dev).to(torch.bfloat16).requires_grad_()
+    w12 = (torch.randn(2 * H, C, device=dev) / C ** 0.5).to(torch.bfloat16).requires_grad_()
+    w3 = (torch.randn(C, H, device=dev) / H ** 0.5).to(torch.bfloat16).requires_grad_()
+    y = getattr(G, fn)(x, w12, w3)
+    dy = (torch.randn(M, C, device=dev) * 0.1).to(torch.bfloat16)
+    y.backward(dy)
+    xf, w12f, w3f, yf = _mlp_ref(x.detach(), w12.detach(), w3.detach())
+    yf.backward(dy.float())
+    assert rel(y, yf) < 0.1                     # e4m3 inputs: a few percent from the bf16 / fp32 model
+    assert rel(x.grad, xf.grad) < 0.15
+    assert rel(w12.grad, w12f.grad) < 0.15
+    assert rel(w3.grad, w3f.grad) < 0.15
+    # both phases run the same forward bit for bit
+    y_other = (G.fp8_mlp_f8 if fn == "fp8_mlp" else G.fp8_mlp)(x.detach(), w12.detach(), w3.detach())
+    assert torch.equal(y.detach(), y_other)
+
+
+def test_mlp_phase3_grads_match_quantized_formula(dev):
+    """Each phase-3 gradient equals the fp32 product of the very e4m3 operands it was given."""
+    M, C, H = 512, 256, 512
+    x = torch.randn(M, C, device=dev).to(torch.bfloat16).requires_grad_()
+    w12 = (torch.randn(2 * H, C, device=dev) / C ** 0.5).to(torch.bfloat16).requires_grad_()
+    w3 = (torch.randn(C, H, device=dev) / H ** 0.5).to(torch.bfloat16).requires_grad_()
+    y = G.fp8_mlp_f8(x, w12, w3)
+    dy = (torch.randn(M, C, device=dev) * 0.1).to(torch.bfloat16)
+    y.backward(dy)
+    xq, sx = G.tcast(x.detach())
+    w12q, s12 = G.tcast(w12.detach())
+    z = G.fp8_gemm(xq, sx, w12q, s12)
+    aq, sa = G.swiglu_tcast(z)
+    w3q, s3 = G.tcast(w3.detach())
+    dyq, sdy = G.tcast(dy)
+    da = G.fp8_gemm(dyq, sdy, G.tcast_t(w3.detach(), False)[1], s3)
+    assert rel(w3.grad, deq(dyq, sdy).t() @ deq(aq, sa)) < 4e-3
+    _, dzq, sdz = G.swiglu_bwd(z, da)
+    assert rel(x.grad, deq(dzq, sdz) @ deq(w12q, s12)) < 4e-3
+    assert rel(w12.grad, deq(dzq, sdz).t() @ deq(xq, sx)) < 4e-3
+
+
+def test_swiglu_w3_phase1(dev):
+    M, C, H = 256, 128, 512
+    z = (torch.randn(M, 2 * H, device=dev) * 2).to(torch.bfloat16).requires_grad_()
+    w3 = (torch.randn(C, H, device=dev) / H ** 0.5).requires_grad_()
+    y = G.fp8_swiglu_w3(z, w3)
+    z1, z2 = z.detach().float().chunk(2, -1)
+    yref = (torch.nn.functional.silu(z1) * z2) @ w3.detach().t()
+    assert rel(y, yref) < 0.1
+    y.backward(torch.ones_like(y))
+    assert z.grad.shape == z.shape and w3.grad.dtype == torch.float32 and torch.isfinite(z.grad.float()).all()
+
+
+class _Attn(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.qkv_x = nn.Linear(d, 3 * d, bias=False)
+        self.proj = nn.Linear(d, d)
+
+    def forward(self, x):
+        q, k, v = self.qkv_x(x).chunk(3, -1)
+        a = torch.softmax((q.float() @ k.float().transpose(-1, -2)) / q.shape[-1] ** 0.5, -1)
+        return self.proj((a @ v.float()).to(x.dtype))
+
+
+class _MLP(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.w12 = nn.Linear(d, 8 * d, bias=False)
+        self.w3 = nn.Linear(4 * d, d, bias=False)
+
+    def forward(self, x):
+        x1, x2 = self.w12(x).chunk(2, -1)
+        return self.w3(torch.nn.functional.silu(x1) * x2)
+
+
+class _Block(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.attn = _Attn(d)
+        self.mlp = _MLP(d)
+
+    def forward(self, x):
+        x = x + self.attn(x)
+        return x + self.mlp(x)
+
+
+class _Net(nn.Module):
+    def __init__(self, d, n):
+        super().__init__()
+        self.blocks = nn.ModuleList(_Block(d) for _ in range(n))
+
+    def forward(self, x):
+        for b in self.blocks:
+            x = b(x)
+        return x
+
+
+@pytest.mark.parametrize("recipe", ["native", "native2", "native3"])
+def test_convert_and_train_step(dev, recipe):
+    torch.manual_seed(0)
+    net = _Net(128, 2).to(dev).to(torch.bfloat16)
+    ref = _Net(128, 2).to(dev).to(torch.bfloat16)
+    ref.load_state_dict(net.state_dict())
+    assert G.convert_fp8(net, recipe) == 8
+    x = torch.randn(4, 64, 128, device=dev).to(torch.bfloat16)
+    y, yr = net(x), ref(x)
+    assert rel(y, yr) < 0.1
+    y.float().square().mean().backward()
+    yr.float().square().mean().backward()
+    for (n, p), (_, pr) in zip(net.named_parameters(), ref.named_parameters()):
+        assert p.grad is not None and torch.isfinite(p.grad.float()).all(), n
+        assert rel(p.grad, pr.grad) < 0.25, n

@@ -1,0 +1,154 @@
+"""GPU parity of the cast kernels (gpic_fp8_tcast / gpic_fp8_tcast_t) against the pinned oracle and the golden vectors.
+The bar is bit-exact: every e4m3 byte and every fp32 scale."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import gpic_fp8 as G
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def to_bf16(h, dev):
+    return torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def qb(t):
+    return t.contiguous().view(torch.uint8).cpu().numpy()
+
+
+def config2_input(rows=32768, cols=1024, seed=1):
+    """fp32 randn (seed 1), round(0.01 * cols) outlier columns x50 in fp32, rounded once to bf16."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, cols, generator=g)
+    c = torch.randperm(cols, generator=g)[:round(0.01 * cols)]
+    x[:, c] *= 50.0
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("name", ["cast_bf16", "cast_tail", "cast_range"])
+def test_golden_bf16(dev, gold, name):
+    q, s = G.tcast(to_bf16(gold[f"{name}_x"], dev))
+    assert np.array_equal(qb(q), gold[f"{name}_q"])
+    assert s.item() == gold[f"{name}_s"][0]
+
+
+def test_golden_f32_weight(dev, gold):
+    q, s = G.tcast(torch.from_numpy(gold["cast_f32_x"]).to(dev))
+    assert np.array_equal(qb(q), gold["cast_f32_q"]) and s.item() == gold["cast_f32_s"][0]
+
+
+def test_golden_zero_and_empty(dev, gold):
+    q, s = G.tcast(torch.zeros(16, 16, dtype=torch.bfloat16, device=dev))
+    assert np.array_equal(qb(q), gold["cast_zero_q"]) and s.item() == gold["cast_zero_s"][0]
+    q, s = G.tcast(torch.empty(0, 64, dtype=torch.bfloat16, device=dev))
+    assert q.shape == (0, 64) and s.item() == np.float32(np.float32(1e-12) / np.float32(448.0))
+
+
+def test_golden_cast_t(dev, gold):
+    q, qt, s = G.tcast_t(to_bf16(gold["cast_t_x"], dev))
+    assert np.array_equal(qb(q), gold["cast_t_q"]) and np.array_equal(qb(qt), gold["cast_t_qt"])
+    assert s.item() == gold["cast_t_s"][0]
+
+
+def test_config2_full_size_bitexact(dev):
+    """[32768 x 1024] bf16 with 1% outlier channels: bytes and scale equal the oracle's."""
+    x = config2_input()
+    xh = bits(x)
+    q, s = G.tcast(x.to(dev))
+    oq, od, _ = O.tcast(xh)
+    assert s.item() == od
+    assert np.array_equal(qb(q), oq)
+
+
+def test_config2_fp32_bitexact(dev):
+    x = config2_input(rows=4096).float() * 0.37
+    q, s = G.tcast(x.to(dev))
+    oq, od, _ = O.tcast(x.numpy())
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_hw_e4m3_conversion_exhaustive(dev):
+    """Every fp32 magnitude in [0, 448], both signs, through the product cast: the input's amax is 448, so the scale
+    is exactly 1 and each byte is e4m3(x) -- gfx950's conversion against the oracle's (itself equal to torch's)."""
+    top = int(np.float32(448.0).view(np.uint32)) + 1
+    chunk = 1 << 28
+    for sign_bit in (0, 1 << 31):
+        for s0 in range(0, top, chunk):
+            s1 = min(s0 + chunk, top)
+            u = torch.arange(s0, s1, dtype=torch.int64, device=dev).bitwise_or(sign_bit).to(torch.int32)
+            x = torch.cat([u.view(torch.float32), torch.tensor([448.0], device=dev)])
+            q, s = G.tcast(x)
+            assert s.item() == 1.0
+            f = (np.arange(s0, s1, dtype=np.uint32) | np.uint32(sign_bit)).view(np.float32)
+            bad = np.flatnonzero(qb(q)[:-1] != O.e4m3(f))
+            assert bad.size == 0, f"first mismatch at fp32 {f[bad[0]]!r}"
+            del u, x, q
+
+
+def test_tcast_t_matches_oracle(dev):
+    g = torch.Generator().manual_seed(11)
+    for rows, cols, dt in ((1000, 1024, torch.bfloat16), (77, 48, torch.float32), (3, 16, torch.bfloat16)):
+        x = (torch.randn(rows, cols, generator=g) * 7).to(dt)
+        q, qt, s = G.tcast_t(x.to(dev))
+        xn = bits(x) if dt == torch.bfloat16 else x.numpy()
+        oq, od, _ = O.tcast(xn)
+        r16 = (rows + 15) // 16 * 16
+        assert s.item() == od and np.array_equal(qb(q), oq)
+        qtn = qb(qt)
+        assert qtn.shape == (cols, r16)
+        assert np.array_equal(qtn[:, :rows], oq.T) and not qtn[:, rows:].any()
+
+
+def test_transpose_invariant(dev):
+    """tcast_t(w).qt == tcast(w.t().contiguous()).q: the reference casts the transposed weight (fp8_native.py:259)."""
+    w = (torch.randn(1024, 4096, device=dev) / 64).to(torch.bfloat16)
+    _, qt, s1 = G.tcast_t(w, False)
+    q2, s2 = G.tcast(w.t().contiguous())
+    assert s1.item() == s2.item() and torch.equal(qt.view(torch.uint8), q2.view(torch.uint8))
+
+
+def test_misaligned_and_strided_inputs(dev):
+    base = config2_input(rows=64, cols=256).to(dev)
+    x = base.view(-1)[3:3 + 5000]             # 6-byte offset: not 16-byte aligned
+    q, s = G.tcast(x)
+    oq, od, _ = O.tcast(bits(x))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+    xs = base[:, ::2]                          # non-contiguous view
+    q, s = G.tcast(xs)
+    oq, od, _ = O.tcast(bits(xs))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_nan_and_inf_rules(dev):
+    x = config2_input(rows=16, cols=64)
+    x[3, 5] = float("nan")
+    x[9, 1] = -float("nan")
+    q, s = G.tcast(x.to(dev))
+    oq, od, _ = O.tcast(bits(x))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+    x[0, 0] = float("inf")                     # amax inf -> scale 0: finite values -> 0, inf * 0 -> -448
+    q, s = G.tcast(x.to(dev))
+    oq, od, _ = O.tcast(bits(x))
+    assert np.isinf(s.item()) and np.isinf(od) and np.array_equal(qb(q), oq)
+
+
+def test_other_float_dtypes_widen(dev):
+    x = torch.randn(333, 17, device=dev).to(torch.float16)
+    q, s = G.tcast(x)
+    q2, s2 = G.tcast(x.float())
+    assert s.item() == s2.item() and torch.equal(q.view(torch.uint8), q2.view(torch.uint8))

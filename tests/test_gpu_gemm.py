@@ -1,0 +1,130 @@
+"""GPU parity of the FP8 MFMA GEMM (gpic_fp8_gemm). Exact cases (small-integer operands, power-of-two scales, identity)
+are bit-exact; general cases are within the north-star tolerance of the scaled matmul of the same e4m3 operands:
+relative Frobenius error <= 1e-2 (asserted tighter where the bf16 output rounding is the only error)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import gpic_fp8 as G
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+E4 = torch.float8_e4m3fn
+TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def e4(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).view(E4).to(dev)
+
+
+def rand_e4(shape, scale, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(*shape, generator=g, device=dev) * scale).clamp(-448, 448).to(E4)
+
+
+def ref_fp32(a, sa, b, sb):
+    """The scaled matmul of the same operands on the GPU in fp32 (no TF32): the reference's reference() formula."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    return (a.float() * sa) @ (b.float() * sb).t()
+
+
+def rel(x, ref):
+    return (torch.linalg.norm(x.float() - ref) / torch.linalg.norm(ref)).item()
+
+
+def test_exact_golden(dev, gold):
+    a, b = e4(gold["gemm_a"], dev), e4(gold["gemm_b"], dev)
+    sa = torch.tensor(gold["gemm_sa"], device=dev)
+    sb = torch.tensor(gold["gemm_sb"], device=dev)
+    c = G.fp8_gemm(a, sa, b, sb)
+    assert np.array_equal(bits(c), gold["gemm_c"])
+    bias = torch.from_numpy(gold["gemm_bias"].view(np.int16)).view(torch.bfloat16).to(dev)
+    c = G.fp8_gemm(a, sa, b, sb, bias)
+    assert np.array_equal(bits(c), gold["gemm_cbias"])
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 16), (300, 272, 1040), (512, 1024, 4096), (64, 64, 32768)])
+def test_exact_integers(dev, M, N, K):
+    """Integers in [-4, 4] with power-of-two scales: every partial sum is exact in fp32, so C is bit-exact."""
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    a = torch.randint(-4, 5, (M, K), generator=g, device=dev).float().to(E4)
+    b = torch.randint(-4, 5, (N, K), generator=g, device=dev).float().to(E4)
+    sa = torch.tensor([0.5], device=dev)
+    sb = torch.tensor([0.25], device=dev)
+    c = G.fp8_gemm(a, sa, b, sb)
+    exact = (a.double() @ b.double().t()) * 0.125
+    assert torch.equal(c, exact.float().to(torch.bfloat16))
+
+
+def test_identity(dev):
+    a = rand_e4((200, 256), 30.0, 1, dev)
+    eye = torch.eye(256, device=dev).to(E4)
+    c = G.fp8_gemm(a, torch.tensor([2.0], device=dev), eye, torch.tensor([0.5], device=dev))
+    assert torch.equal(c, a.float().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 48, 160), (1000, 1024, 1024), (333, 3072, 1024), (2048, 1024, 8192),
+                                   (1024, 1024, 32768), (3072, 1024, 32768)])
+def test_against_oracle(dev, M, N, K):
+    a = rand_e4((M, K), 40.0, 2, dev)
+    b = rand_e4((N, K), 40.0, 3, dev)
+    sa = torch.tensor([0.013], device=dev)
+    sb = torch.tensor([0.021], device=dev)
+    c = G.fp8_gemm(a, sa, b, sb)
+    if M * N * K <= 2 ** 31:
+        ref = torch.from_numpy(O.mm64(a.view(torch.uint8).cpu().numpy(), np.float32(0.013),
+                                      b.view(torch.uint8).cpu().numpy(), np.float32(0.021))).float().to(dev)
+    else:
+        ref = ref_fp32(a, sa, b, sb)
+    r = rel(c, ref)
+    assert r <= TOL and r < 4e-3
+    # deterministic, including the split-K shapes
+    assert torch.equal(c, G.fp8_gemm(a, sa, b, sb))
+
+
+def test_bias_epilogue(dev):
+    a = rand_e4((256, 1024), 20.0, 4, dev)
+    b = rand_e4((1024, 1024), 20.0, 5, dev)
+    sa = torch.tensor([0.01], device=dev)
+    sb = torch.tensor([0.02], device=dev)
+    bias = torch.randn(1024, device=dev).to(torch.bfloat16)
+    c0 = G.fp8_gemm(a, sa, b, sb)
+    c1 = G.fp8_gemm(a, sa, b, sb, bias)
+    assert torch.equal(c1, (c0.float() + bias.float()).to(torch.bfloat16))   # the two roundings of :188-190
+
+
+def test_strided_operands(dev):
+    wide = rand_e4((128, 1024), 30.0, 6, dev)
+    a = wide[:, 256:768]                      # row stride 1024, K = 512
+    b = rand_e4((64, 512), 30.0, 7, dev)
+    s = torch.tensor([1.0], device=dev)
+    c = G.fp8_gemm(a, s, b, s)
+    assert torch.equal(c, G.fp8_gemm(a.contiguous(), s, b, s))
+    assert rel(c, ref_fp32(a, 1.0, b, 1.0)) < 4e-3
+
+
+@pytest.mark.parametrize("name,M,N,K", [("qkv", 32768, 3072, 1024), ("proj", 32768, 1024, 1024),
+                                        ("w12", 32768, 8192, 1024), ("w3", 32768, 1024, 4096),
+                                        ("wgrad_qkv", 3072, 1024, 32768), ("wgrad_w12", 8192, 1024, 32768)])
+def test_d12_shapes(dev, name, M, N, K):
+    """BASELINE config 3 / 4 shapes: X ~ N(0,1), W ~ N(0, 1/K), per-tensor casts, against the fp32 scaled matmul."""
+    g = torch.Generator(device=dev).manual_seed(42)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16)
+    xq, sx = G.tcast(x)
+    wq, sw = G.tcast(w)
+    c = G.fp8_gemm(xq, sx, wq, sw)
+    assert rel(c, ref_fp32(xq, sx, wq, sw)) < 4e-3

@@ -1,0 +1,137 @@
+"""GPU parity of the SwiGLU kernels (gpic_fp8_swiglu_tcast / _bwd and their transposing variants) against the oracle
+(bit-exact) and the torch-written golden vectors (bit-exact for the product cast, within 1 bf16 ulp for dz, whose
+sigmoid is this build's definition)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import gpic_fp8 as G
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def to_bf16(h, dev):
+    return torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def qb(t):
+    return t.contiguous().view(torch.uint8).cpu().numpy()
+
+
+def rand_bf16(shape, scale, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def test_golden_product_cast(dev, gold):
+    q, s = G.swiglu_tcast(to_bf16(gold["swiglu_z"], dev))
+    assert np.array_equal(qb(q), gold["swiglu_q"]) and s.item() == gold["swiglu_s"][0]
+
+
+def test_golden_bwd(dev, gold):
+    dz, dzq, s = G.swiglu_bwd(to_bf16(gold["swiglu_z"], dev), to_bf16(gold["bwd_da"], dev))
+    diff = np.abs(bits(dz).astype(np.int32) - gold["bwd_dz"].astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.99
+    oz, oq, od, _ = O.swiglu_bwd(gold["swiglu_z"], gold["bwd_da"])
+    assert np.array_equal(bits(dz), oz) and np.array_equal(qb(dzq), oq) and s.item() == od
+
+
+def test_sigmoid_exhaustive_all_bf16(dev):
+    """z1 = every bf16 value, z2 = da = 1: d2 = bf16(1 * sl) = sl and d1 = bf16(1 * g) expose the device's
+    sl(z1) = bf16(z1 * sigmoid(z1)) and g(z1) = sigmoid * (1 + z1 * (1 - sigmoid)) for all 65536 inputs."""
+    H = 256
+    z1 = np.arange(65536, dtype=np.uint16).reshape(-1, H)
+    M = z1.shape[0]
+    z = np.concatenate([z1, np.full((M, H), 0x3F80, np.uint16)], axis=1)
+    da = np.full((M, H), 0x3F80, np.uint16)
+    dz, _, _ = G.swiglu_bwd(to_bf16(z, dev), to_bf16(da, dev))
+    oz, _, _, _ = O.swiglu_bwd(z, da)
+    d = bits(dz)
+    nan_o = np.isnan(O.bf16_to_f32(oz))
+    assert np.array_equal(np.isnan(O.bf16_to_f32(d)), nan_o)
+    assert np.array_equal(d[~nan_o], oz[~nan_o])
+    # and the forward product: a = bf16(sl * 1) = sl, through the cast with a common scale
+    q, s = G.swiglu_tcast(to_bf16(np.where(np.isfinite(O.bf16_to_f32(z)), z, 0).astype(np.uint16), dev))
+    oq, od, _ = O.swiglu_tcast(np.where(np.isfinite(O.bf16_to_f32(z)), z, 0).astype(np.uint16))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+@pytest.mark.parametrize("M,H", [(256, 512), (33, 64), (1, 8)])
+def test_product_cast_matches_oracle(dev, M, H):
+    z = rand_bf16((M, 2 * H), 3.0, seed=M + H)
+    q, s = G.swiglu_tcast(z.to(dev))
+    oq, od, _ = O.swiglu_tcast(bits(z))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_product_cast_row_stride(dev):
+    """z as a column slice of a wider tensor (row stride > 2H), as the reference allows (fp8_native.py:135)."""
+    wide = rand_bf16((128, 3 * 256), 2.0, seed=5).to(dev)
+    z = wide[:, :512]
+    q, s = G.swiglu_tcast(z)
+    oq, od, _ = O.swiglu_tcast(bits(z))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_product_cast_d12_rows(dev):
+    """4096 tokens of d12's SwiGLU (H = 4096)."""
+    z = rand_bf16((4096, 8192), 1.5, seed=12)
+    q, s = G.swiglu_tcast(z.to(dev))
+    oq, od, _ = O.swiglu_tcast(bits(z))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+@pytest.mark.parametrize("M,H", [(200, 256), (17, 16)])
+def test_bwd_matches_oracle(dev, M, H):
+    z = rand_bf16((M, 2 * H), 3.0, seed=M)
+    da = rand_bf16((M, H), 0.05, seed=M + 1)
+    dz, dzq, s = G.swiglu_bwd(z.to(dev), da.to(dev))
+    oz, oq, od, _ = O.swiglu_bwd(bits(z), bits(da))
+    assert np.array_equal(bits(dz), oz) and np.array_equal(qb(dzq), oq) and s.item() == od
+
+
+def test_transposing_variants(dev):
+    M, H = 300, 512
+    z = rand_bf16((M, 2 * H), 2.0, seed=9).to(dev)
+    da = rand_bf16((M, H), 0.1, seed=10).to(dev)
+    q, s = G.swiglu_tcast(z)
+    q2, qt, s2 = G.swiglu_tcast_t(z)
+    m16 = (M + 15) // 16 * 16
+    assert s.item() == s2.item() and torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+    assert qt.shape == (H, m16) and torch.equal(qt.view(torch.uint8)[:, :M], q.view(torch.uint8).t())
+    assert not qt.view(torch.uint8)[:, M:].any()
+    dz, dq, sd = G.swiglu_bwd(z, da)
+    dz2, dq2, dqt, sd2 = G.swiglu_bwd_t(z, da)
+    assert torch.equal(dz.view(torch.int16), dz2.view(torch.int16)) and sd.item() == sd2.item()
+    assert torch.equal(dq.view(torch.uint8), dq2.view(torch.uint8))
+    assert torch.equal(dqt.view(torch.uint8)[:, :M], dq.view(torch.uint8).t())
+    assert not dqt.view(torch.uint8)[:, M:].any()
+
+
+def test_bwd_matches_eager_torch_within_one_ulp(dev):
+    """The eager phase-1 backward (fp8_native.py:226-231, torch.sigmoid) agrees with the kernel's dz within 1 ulp."""
+    M, H = 512, 1024
+    z = rand_bf16((M, 2 * H), 3.0, seed=21).to(dev)
+    da = rand_bf16((M, H), 0.1, seed=22).to(dev)
+    dz, _, _ = G.swiglu_bwd(z, da)
+    z1, z2 = z.float().chunk(2, dim=-1)
+    sg = torch.sigmoid(z1)
+    dz1 = (da.float() * z2 * (sg * (1 + z1 * (1 - sg)))).to(torch.bfloat16)
+    dz2 = da * (z1 * sg).to(torch.bfloat16)
+    ref = torch.cat([dz1, dz2], -1)
+    diff = (dz.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert diff.max().item() <= 1 and (diff == 0).float().mean().item() > 0.99

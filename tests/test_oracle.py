@@ -1,0 +1,259 @@
+"""Pins the CPU oracle (oracle/) before it is trusted to check the HIP kernels.
+
+Each oracle function is checked against something independent of it: torch's own CPU routines (the float8 conversion,
+IEEE division, sigmoid, matmul), the committed golden vectors (tests/golden, written with torch ops only), closed
+forms and invariants (transpose, power-of-two scaling, exact integer GEMMs). Mutants of the oracle's rules (a truncating
+e4m3 rounding, the eager reciprocal * 448 scale, a dropped clamp, a transposed operand) are shown to fail these checks.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+E4 = torch.float8_e4m3fn
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def torch_e4m3(f):
+    return torch.from_numpy(np.ascontiguousarray(f, dtype=np.float32)).to(E4).view(torch.uint8).numpy()
+
+
+# ---------------------------------------------------------------- e4m3 rounding
+
+def test_e4m3_exhaustive_against_torch():
+    """Every fp32 magnitude up to 464 (the last value that still rounds to 448), both signs: 2.28e9 values."""
+    top = int(np.float32(464.0).view(np.uint32)) + 1
+    chunk = 1 << 26
+    bad = 0
+    for s in range(0, top, chunk):
+        f = np.arange(s, min(s + chunk, top), dtype=np.uint32).view(np.float32)
+        ref = torch_e4m3(f)
+        bad += int((O.e4m3(f) != ref).sum())
+        bad += int((O.e4m3(-f) != (ref | 0x80)).sum())
+    assert bad == 0
+
+
+def test_e4m3_specials():
+    f = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 448.0, 464.0, 465.0, 2.0 ** -9, 2.0 ** -10,
+                  1.5 * 2.0 ** -9, 2.0 ** -6], dtype=np.float32)
+    ours, ref = O.e4m3(f), torch_e4m3(f)
+    # NaN payload bits aside, torch and the oracle agree on every special value
+    assert (ours == ref).all(), (ours, ref)
+
+
+def test_e4m3_decode_all_bytes():
+    b = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(b).view(E4).float().numpy()
+    ours = O.e4m3_to_f32(b)
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    m = ~np.isnan(ref)
+    assert (ours[m] == ref[m]).all()
+    assert O.e4m3_to_f32(np.uint8(0x7E)) == 448.0 and O.e4m3_to_f32(np.uint8(0x01)) == 2.0 ** -9
+
+
+def test_e4m3_mutant_truncation_fails():
+    """A truncating (round-toward-zero) e4m3 disagrees with torch on many values: the check above has teeth."""
+    f = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 10
+    f = np.clip(f, -448, 448)
+    u = f.view(np.uint32)
+    trunc = O.e4m3_to_f32(O.e4m3(((u >> 20) << 20).view(np.float32)))   # chop the mantissa to 3 bits
+    assert (O.e4m3(trunc) != torch_e4m3(f)).mean() > 0.1
+
+
+# ---------------------------------------------------------------- amax and scales
+
+def test_scales_ieee_division():
+    rng = np.random.default_rng(1)
+    amax = np.concatenate([rng.uniform(0, 1000, 50000), np.exp(rng.uniform(-40, 40, 50000)),
+                           [0.0, 1e-13, 1e-12, 448.0]]).astype(np.float32)
+    s = np.empty_like(amax)
+    d = np.empty_like(amax)
+    for i, a in enumerate(amax):
+        s[i], d[i] = O.scales(int(np.float32(a).view(np.uint32)))
+    at = torch.clamp_min(torch.from_numpy(amax), 1e-12)
+    assert np.array_equal(s, torch.div(torch.tensor(448.0), at).numpy())
+    assert np.array_equal(d, torch.div(at, torch.tensor(448.0)).numpy())
+    # the eager 448.0 / a (reciprocal(a) * 448) is a different rule: it disagrees on a sizeable share of values
+    eager = (448.0 / at).numpy()
+    assert (eager != s).mean() > 0.05
+
+
+def test_amax_closed_form():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(10001).astype(np.float32)
+    h = O.f32_to_bf16(x)
+    assert O.amax_bits(h) == int(np.abs(O.bf16_to_f32(h)).max().view(np.uint32))
+    assert O.amax_bits(x) == int(np.abs(x).max().view(np.uint32))
+    x[17] = np.nan                                   # tl.max (maxnum) ignores NaN
+    assert O.amax_bits(x) == int(np.nanmax(np.abs(x)).view(np.uint32))
+    assert O.amax_bits(np.zeros(0, np.uint16)) == 0
+
+
+@pytest.mark.parametrize("name", ["cast_bf16", "cast_tail", "cast_f32", "cast_range"])
+def test_tcast_golden(gold, name):
+    q, d, _ = O.tcast(gold[f"{name}_x"])
+    assert np.array_equal(q, gold[f"{name}_q"])
+    assert d == gold[f"{name}_s"][0]
+
+
+def test_tcast_zero_golden(gold):
+    q, d, am = O.tcast(np.zeros((16, 16), np.uint16))
+    assert np.array_equal(q, gold["cast_zero_q"]) and d == gold["cast_zero_s"][0] and am == 0
+    q, d, _ = O.tcast(np.zeros(0, np.uint16))
+    assert q.size == 0 and d == np.float32(np.float32(1e-12) / np.float32(448.0))
+
+
+def test_tcast_mutant_eager_scale_fails(gold):
+    """Casting config-2-like data with the eager reciprocal * 448 scale changes bytes for some amax values."""
+    rng = np.random.default_rng(3)
+    changed = 0
+    for _ in range(40):
+        x = O.f32_to_bf16(rng.standard_normal(4096).astype(np.float32) * rng.uniform(0.1, 100))
+        q, _, am = O.tcast(x)
+        a = torch.tensor(np.uint32(am).view(np.float32)).clamp_min(1e-12)
+        q2 = O.cast(x, np.float32((448.0 / a).item()))
+        changed += int((q2 != q).any())
+    assert changed > 0
+
+
+def test_transpose_invariant():
+    rng = np.random.default_rng(4)
+    x = O.f32_to_bf16(rng.standard_normal((48, 80)).astype(np.float32))
+    q, d, _ = O.tcast(x)
+    qt, dt, _ = O.tcast(np.ascontiguousarray(x.T))
+    assert np.array_equal(qt, q.T) and d == dt
+
+
+def test_pow2_scale_invariant():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(5000).astype(np.float32)
+    q, d, _ = O.tcast(x)
+    for k in (-20, -3, 1, 7, 30):
+        qk, dk, _ = O.tcast((x * np.float32(2.0 ** k)).astype(np.float32))
+        assert np.array_equal(qk, q) and dk == np.float32(d * np.float32(2.0 ** k))
+
+
+def test_cast_clamp_and_nan_rule():
+    """x * scale beyond +-448 saturates (tl.minimum / tl.maximum); a NaN product saturates to -448 (maxNum)."""
+    x = np.array([1.0, -1.0, 500.0, -500.0, np.nan, np.inf, -np.inf], np.float32)
+    q = O.cast(x, np.float32(448.0))
+    assert list(q) == [0x7E, 0xFE, 0x7E, 0xFE, 0xFE, 0x7E, 0xFE]
+
+
+# ---------------------------------------------------------------- SwiGLU
+
+def test_exp_accuracy_all_bf16():
+    h = np.arange(65536, dtype=np.uint16)
+    f = O.bf16_to_f32(h)
+    ok = np.isfinite(f) & (f > -87) & (f < 88)
+    e = O.exp(f[ok]).astype(np.float64)
+    ex = np.array([math.exp(v) for v in f[ok].astype(np.float64)])
+    ulp = np.abs(e - ex) / np.spacing(ex.astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 1.0
+    assert O.exp(np.float32([0.0]))[0] == 1.0 and O.exp(np.float32([-np.inf]))[0] == 0.0
+
+
+def test_sigmoid_against_torch_all_bf16():
+    f = O.bf16_to_f32(np.arange(65536, dtype=np.uint16))
+    fin = np.isfinite(f)
+    ours = O.sigmoid(f[fin])
+    ref = torch.sigmoid(torch.from_numpy(f[fin])).numpy()
+    ulp = np.abs(ours.astype(np.float64) - ref) / np.maximum(np.spacing(np.abs(ref)), 1e-45)
+    assert ulp.max() <= 2 and (ours == ref).mean() > 0.99
+
+
+def test_silu_table_equals_torch_all_bf16():
+    """sl = bf16(z1 * sigmoid(z1)) equals torch's eager value for every finite bf16 z1 (so the SwiGLU product, a
+    function of sl and z2, is torch's to the bit)."""
+    h = np.arange(65536, dtype=np.uint16)
+    fin = np.isfinite(O.bf16_to_f32(h))
+    z1 = torch.from_numpy(h.view(np.int16)).view(torch.bfloat16).float()
+    ref = (z1 * torch.sigmoid(z1)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.swiglu_table()[fin], ref[fin])
+
+
+def test_swiglu_tcast_golden(gold):
+    z = gold["swiglu_z"]
+    assert np.array_equal(O.swiglu_product(z), gold["swiglu_a"])
+    q, d, _ = O.swiglu_tcast(z)
+    assert np.array_equal(q, gold["swiglu_q"]) and d == gold["swiglu_s"][0]
+
+
+def test_swiglu_bwd_golden(gold):
+    z, da = gold["swiglu_z"], gold["bwd_da"]
+    dz, dzq, d, _ = O.swiglu_bwd(z, da)
+    ref = gold["bwd_dz"]
+    diff = np.abs(dz.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.99          # within 1 bf16 ulp of torch's sigmoid
+    q2, d2, _ = O.tcast(dz)                                         # the bytes are the cast of dz itself
+    assert np.array_equal(q2, dzq) and d2 == d
+
+
+def test_swiglu_bwd_mutant_fused_fails():
+    """Fusing 1 + z1 * (1 - sg) into one fma changes some dz values: the bwd rounding order is pinned. (Such a change
+    moves g by an fp32 ulp, which flips dz's bf16 rounding about once per 3e4 elements: 4M elements are checked.)"""
+    rng = np.random.default_rng(6)
+    M, H = 1024, 4096
+    z = O.f32_to_bf16(rng.standard_normal((M, 2 * H)).astype(np.float32) * 3)
+    da = O.f32_to_bf16(rng.standard_normal((M, H)).astype(np.float32))
+    dz, _, _, _ = O.swiglu_bwd(z, da)
+    sg_tab = O.sigmoid(O.bf16_to_f32(np.arange(65536, dtype=np.uint16)))
+    z1 = O.bf16_to_f32(z[:, :H])
+    z2 = O.bf16_to_f32(z[:, H:])
+    dav = O.bf16_to_f32(da)
+    sg = sg_tab[z[:, :H]]
+    unfused = (np.float32(1) + z1 * (np.float32(1) - sg)).astype(np.float32)
+    fused = (z1.astype(np.float64) * (np.float32(1) - sg).astype(np.float64) + 1).astype(np.float32)
+    d1u = O.f32_to_bf16((dav * z2) * (sg * unfused))
+    d1f = O.f32_to_bf16((dav * z2) * (sg * fused))
+    assert np.array_equal(d1u, dz[:, :H])          # the oracle is the unfused expression
+    assert (d1f != dz[:, :H]).sum() > 0
+
+
+# ---------------------------------------------------------------- GEMM
+
+def test_mm_exact_golden(gold):
+    c = O.mm(gold["gemm_a"], gold["gemm_sa"][0], gold["gemm_b"], gold["gemm_sb"][0])
+    assert np.array_equal(c, gold["gemm_c"])
+    cb = O.mm(gold["gemm_a"], gold["gemm_sa"][0], gold["gemm_b"], gold["gemm_sb"][0], gold["gemm_bias"])
+    assert np.array_equal(cb, gold["gemm_cbias"])
+
+
+def test_mm_mutant_transposed_operand_fails(gold):
+    a, b = gold["gemm_a"], gold["gemm_b"]
+    c = O.mm(a, 1.0, b, 1.0)
+    # a swapped-operand result is C^T: a different matrix
+    ct = O.mm(b, 1.0, a, 1.0)
+    assert ct.shape != c.shape or not np.array_equal(ct, c)
+
+
+def test_mm_identity():
+    rng = np.random.default_rng(7)
+    a = O.e4m3(rng.standard_normal((32, 64)).astype(np.float32) * 20)
+    eye = O.e4m3(np.eye(64, dtype=np.float32))
+    c = O.mm(a, np.float32(0.5), eye, np.float32(2.0))
+    assert np.array_equal(c, O.f32_to_bf16(O.e4m3_to_f32(a)))
+
+
+def test_mm_against_torch_fp32():
+    rng = np.random.default_rng(8)
+    a = O.e4m3(np.clip(rng.standard_normal((64, 256)) * 50, -448, 448).astype(np.float32))
+    b = O.e4m3(np.clip(rng.standard_normal((80, 256)) * 50, -448, 448).astype(np.float32))
+    ref = (torch.from_numpy(a).view(E4).float() * 0.01) @ (torch.from_numpy(b).view(E4).float() * 0.02).t()
+    assert O.rel_fro(O.mm64(a, np.float32(0.01), b, np.float32(0.02)), ref.numpy()) < 1e-6
+
+
+def test_linear_forward_golden(gold):
+    y = O.linear_forward(gold["lin_x"], gold["lin_w"], gold["lin_b"])
+    ref = O.bf16_to_f32(gold["lin_y"])
+    assert O.rel_fro(O.bf16_to_f32(y), ref) < 5e-3
