@@ -52,6 +52,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-compare", action="store_true")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="only copy a 1 GiB buffer (the known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -185,6 +187,14 @@ def main():
     import gpic_fp8 as G
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.copy_probe:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4, "launches": 3}), flush=True)
+        return
 
     # ---- the step: the whole FP8 linear path of a d12 block, fwd + bwd
     t = make_inputs(dev)
@@ -236,6 +246,11 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline()
     gemm_tflops = fl / gemm_ms / 1e9
+    traffic = None          # HBM bytes per GEMM launch, from the committed FETCH_SIZE / WRITE_SIZE summary
+    tpath = os.path.join(ROOT, "profiles", "gemm_d12_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": round(fl / ms / 1e9, 2),
@@ -254,7 +269,7 @@ def main():
                    "tokens": M_TOK, "width": C, "swiglu_hidden": H, "gemm_tflop_per_step": round(fl / 1e12, 4)},
         "pct_fp8_peak": round(100.0 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_FP8_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
                      "kernel": "gemm_tn_kernel (+ split-K reduce)", "launches_per_step": len(shapes),
                      "avg_launch_us": round(gemm_ms * 1e3 / len(shapes), 1), "gemm_ms_per_step": round(gemm_ms, 4),
                      "per_shape": per_shape},

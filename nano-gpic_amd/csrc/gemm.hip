@@ -1,16 +1,24 @@
 // Scaled FP8 (e4m3fn) GEMM for gfx950, "TN" layout: C[M, N] = bf16(sa * sb * A[M, K] . B[N, K]^T) (+ bias).
 //
 // Design (CDNA4):
-//  * Macro tile BM x BN x 128 per workgroup; waves arranged WM x WN, each owning a (BM/WM) x (BN/WN) sub-tile made
-//    of 16 x 16 MFMA tiles (v_mfma_f32_16x16x128_f8f6f4, both operands e4m3, fp32 accumulators).
-//  * Global -> LDS with buffer_load_dwordx4 ... lds (no VGPR round trip). One wave instruction fills 1 KiB of LDS
-//    = 8 rows x 128 bytes of K. Out-of-range rows / K chunks are handled by the buffer descriptor's range check
-//    (they read as zeros), so any M and any K % 16 == 0 work without branches in the main loop.
-//  * LDS rows are XOR-swizzled: 16-byte chunk c of row r lives in slot c ^ (r & 7), so the ds_read_b128 of 8
-//    consecutive rows at the same K chunk hit 8 different bank groups.
-//  * Two LDS stages: the loads of K tile t+1 are in flight while tile t is multiplied.
-//  * The MFMA is issued as B-fragment x A-fragment, so each lane's 4 accumulators are 4 consecutive columns n of
-//    one row m of C: the epilogue writes 8-byte (bf16) or 16-byte (fp32 partial) chunks.
+//  * Macro tile 256 x 256 x 128 per workgroup of 8 waves, two per SIMD. Wave w owns the 64 x 128 sub-tile
+//    (rows 64 * (w >> 1), columns 128 * (w & 1)) as 2 x 4 MFMA tiles of v_mfma_f32_32x32x64_f8f6f4 (both operands
+//    e4m3, fp32 accumulators in AGPRs).
+//  * Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share the SIMDs pairwise and run one phase apart. In each
+//    phase one group issues its 16 MFMAs of a K tile while the other reads its fragments of the next K tile from LDS
+//    (and, for group 0, sends the following K tile to LDS); a workgroup barrier separates phases. The MFMA pipe of
+//    every SIMD sees the two groups' MFMA blocks back to back.
+//  * Global -> LDS with buffer_load_dwordx4 ... lds (no VGPR round trip), issued by group 0: one wave instruction
+//    fills 1 KiB of LDS = 8 rows x 128 bytes of K. Rows past M / N read as zeros through the buffer descriptor's range
+//    check; the last, partial K tile masks its chunks the same way, so any M and any K % 16 == 0 need no branches in
+//    the main loop. Per-lane offsets are computed once; the K position travels in the scalar soffset.
+//  * LDS rows are XOR-swizzled: 16-byte chunk c of row r lives in slot c ^ ((r >> 1) & 7). gfx950's LDS serves
+//    256 B per clock to 16 lanes at a time; the fragment reads of 16 consecutive rows at one chunk then hit 16
+//    different 16-byte bank groups (measured: no SQ_LDS_BANK_CONFLICT cycles).
+//  * Two LDS stages: K tile t is read by group 0 in phase 2t and by group 1 in phase 2t + 1; group 0 sends tile t + 1
+//    into the other stage during phase 2t and waits for it at the end of its MFMA phase 2t + 1.
+//  * The MFMA is issued as B-fragment x A-fragment, so each lane's accumulators hold runs of 4 consecutive columns
+//    n of one row m of C: the epilogue writes 8-byte (bf16) or 16-byte (fp32 partial) chunks.
 //  * Tile order: workgroups are dealt to the 8 XCDs round robin; the id is remapped so each XCD walks a contiguous
 //    range of tiles in groups of kGroupM tile rows (neighbouring workgroups share A and B panels in that XCD's L2).
 //  * Split-K (for the small-output wgrad shapes): each split writes fp32 partials; a second kernel sums them in
@@ -22,23 +30,21 @@ namespace gpic {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 #define GPIC_LDS __attribute__((address_space(3)))
 
-constexpr int kBK = 128;
+constexpr int kBM = 256, kBN = 256, kBK = 128;
+constexpr int kThreads = 512;                          // 8 waves: 2 groups x 4
+constexpr int kWTM = 64, kWTN = 128;                   // wave tile
+constexpr int kTM = kWTM / 32, kTN = kWTN / 32;        // 32 x 32 MFMA tiles per wave: 2 x 4
+constexpr int kStageBytes = (kBM + kBN) * kBK;         // 64 KiB
+constexpr int kLoaders = 4;                            // group 0 issues the global loads
+constexpr int kLoads = (kBM + kBN) / 8 / kLoaders;     // 16 wave-instructions per stage per loading wave
 constexpr int kGroupM = 4;
-constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 for gfx9-family targets
+constexpr int kBufferFlags = 0x00020000;               // raw buffer descriptor word 3 for gfx9-family targets
+constexpr int kOOB = (int)0x80000000;                  // an offset past any descriptor's range: reads zeros
 
-template <int BM, int BN, int WM, int WN>
-struct GemmCfg {
-  static constexpr int kWaves = WM * WN;
-  static constexpr int kThreads = kWaves * 64;
-  static constexpr int kWTM = BM / WM, kWTN = BN / WN;
-  static constexpr int kTM = kWTM / 16, kTN = kWTN / 16;
-  static constexpr int kStageBytes = (BM + BN) * kBK;
-  static constexpr int kLoadsPerWave = (BM + BN) / 8 / kWaves;
-  static_assert((BM + BN) % (8 * kWaves) == 0, "rows per stage must split evenly over the waves");
-  static_assert(kWTM % 16 == 0 && kWTN % 16 == 0, "wave tile must be a multiple of the 16x16 MFMA");
-};
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
 // Logical tile id for workgroup `bid` out of G: XCD x (= bid % 8) gets the contiguous range of ids
 // [start_x, start_x + count_x).
@@ -47,24 +53,20 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(WM *WN * 64) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
-                                                               const uint8_t *__restrict__ B, int ldb,
-                                                               const float *__restrict__ sa,
-                                                               const float *__restrict__ sb,
-                                                               const uint16_t *__restrict__ bias,
-                                                               uint16_t *__restrict__ C, int64_t ldc,
-                                                               float *__restrict__ P, int M, int N, int K, int ksplit,
-                                                               int tiles_m, int tiles_n, int splits) {
-  using Cfg = GemmCfg<BM, BN, WM, WN>;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * Cfg::kStageBytes];
-  // Declaring an AGPR clobber makes the compiler select the MFMA form that keeps accumulators in AGPRs, leaving
-  // the 256 architectural VGPRs for operands and addresses.
+__global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
+                                                            const uint8_t *__restrict__ B, int ldb,
+                                                            const float *__restrict__ sa, const float *__restrict__ sb,
+                                                            const uint16_t *__restrict__ bias, uint16_t *__restrict__ C,
+                                                            int64_t ldc, float *__restrict__ P, int M, int N, int K,
+                                                            int ksplit, int tiles_m, int tiles_n, int splits) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
+  // Declaring an AGPR clobber makes the compiler select the MFMA form that keeps accumulators in AGPRs.
   asm volatile("" ::: "a0");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  const int group = wave >> 2;
+  const int wm = wave >> 1, wn = wave & 1;
 
   // ---- which tile / split this workgroup owns
   const int tiles = tiles_m * tiles_n;
@@ -76,101 +78,149 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_tn_kernel(const uint8_t *__r
   const int gsz = min(tiles_m - first_m, kGroupM);
   const int tm = first_m + (tile % per_group) % gsz;
   const int tn = (tile % per_group) / gsz;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * kBM, n0 = tn * kBN;
   const int kbeg = split * ksplit;
   const int kend = min(K, kbeg + ksplit);
+  const int nk = (kend - kbeg + kBK - 1) / kBK;
 
-  // ---- buffer descriptors covering this tile's rows of A and B (rows past M / N read as zero)
-  const int rows_a = min(M - m0, BM), rows_b = min(N - n0, BN);
+  // ---- buffer descriptors over this tile's rows of A and B (rows past M / N read as zero)
+  const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBN);
   const __amdgpu_buffer_rsrc_t rA =
       __builtin_amdgcn_make_buffer_rsrc((void *)(A + (int64_t)m0 * lda), 0, rows_a * lda, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rB =
       __builtin_amdgcn_make_buffer_rsrc((void *)(B + (int64_t)n0 * ldb), 0, rows_b * ldb, kBufferFlags);
 
-  // ---- global -> LDS for one stage: wave instruction i covers stacked rows [R0, R0 + 8) of [A tile; B tile]
+  // ---- loads (group 0). Wave instruction i fills stacked rows [R0, R0 + 8) of [A tile; B tile],
+  // R0 = (i * 4 + wave) * 8; lane j writes slot j & 7 of row R0 + j / 8, i.e. K chunk (j & 7) ^ swz(row). swz(row)
+  // does not depend on i, so every instruction's offset is a per-lane base plus i * 32 rows. Row offsets stay in
+  // the VGPR offset (the part the descriptor range-checks); only the K position goes to the scalar offset.
+  const int lrow = (wave & 3) * 8 + (lane >> 3);
+  const int kchunk = 16 * ((lane & 7) ^ swz(lrow));
+  const int baseA = lrow * lda + kchunk, baseB = lrow * ldb + kchunk;
   auto issue = [&](int stage, int k0) {
-    GPIC_LDS uint8_t *sbase = (GPIC_LDS uint8_t *)smem + stage * Cfg::kStageBytes;
+    GPIC_LDS uint8_t *sbase = (GPIC_LDS uint8_t *)smem + stage * kStageBytes;
+    if (k0 + kBK <= kend) {
 #pragma unroll
-    for (int i = 0; i < Cfg::kLoadsPerWave; i++) {
-      const int R0 = (i * Cfg::kWaves + wave) * 8;
-      const int s = lane & 7;
-      if (R0 < BM) {
-        const int r = R0 + (lane >> 3);
-        const int kk = k0 + 16 * (s ^ (r & 7));
-        const int voff = kk < kend ? r * lda + kk : (int)0x80000000;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (GPIC_LDS void *)(sbase + R0 * kBK), 16, voff, 0, 0, 0);
-      } else {
-        const int r = R0 - BM + (lane >> 3);
-        const int kk = k0 + 16 * (s ^ (r & 7));
-        const int voff = kk < kend ? r * ldb + kk : (int)0x80000000;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (GPIC_LDS void *)(sbase + R0 * kBK), 16, voff, 0, 0, 0);
+      for (int i = 0; i < kLoads; i++) {
+        const int R0 = (i * kLoaders + (wave & 3)) * 8;
+        const bool isA = i < kLoads / 2;
+        const int vo = isA ? baseA + i * 32 * lda : baseB + (i - kLoads / 2) * 32 * ldb;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, (GPIC_LDS void *)(sbase + R0 * kBK), 16, vo, k0, 0,
+                                                 0);
+      }
+    } else {  // the last, partial K tile: chunks at or past kend read zeros
+      const bool kin = k0 + kchunk < kend;
+#pragma unroll
+      for (int i = 0; i < kLoads; i++) {
+        const int R0 = (i * kLoaders + (wave & 3)) * 8;
+        const bool isA = i < kLoads / 2;
+        const int vo = (isA ? baseA + i * 32 * lda : baseB + (i - kLoads / 2) * 32 * ldb) + k0;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, (GPIC_LDS void *)(sbase + R0 * kBK), 16,
+                                                 kin ? vo : kOOB, 0, 0, 0);
       }
     }
   };
 
-  // ---- one MFMA operand: row `row` of a stage's A or B area, K chunks 2g and 2g+1 (g = lane / 16)
-  auto frag = [&](const GPIC_LDS uint8_t *base, int row) -> v8i {
-    const int g = lane >> 4;
-    const GPIC_LDS uint8_t *p = base + row * kBK;
-    const u32x4 lo = *(const GPIC_LDS u32x4 *)(p + 16 * ((2 * g) ^ (row & 7)));
-    const u32x4 hi = *(const GPIC_LDS u32x4 *)(p + 16 * ((2 * g + 1) ^ (row & 7)));
-    return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5)
+  v8i fa[2][kTM], fb[2][kTN];
+  const int frow = lane & 31;
+  const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
+  const int c0 = 2 * (lane >> 5);
+  auto read = [&](int stage) {
+    const GPIC_LDS uint8_t *sA = (const GPIC_LDS uint8_t *)smem + stage * kStageBytes;
+    const GPIC_LDS uint8_t *sB = sA + kBM * kBK;
+#pragma unroll
+    for (int step = 0; step < 2; step++) {
+      const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
+#pragma unroll
+      for (int t = 0; t < kTM; t++) {
+        const GPIC_LDS uint8_t *pa = sA + (wm * kWTM + t * 32 + frow) * kBK;
+        const u32x4 a0 = *(const GPIC_LDS u32x4 *)(pa + lo), a1 = *(const GPIC_LDS u32x4 *)(pa + hi);
+        fa[step][t] = v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+      }
+#pragma unroll
+      for (int t = 0; t < kTN; t++) {
+        const GPIC_LDS uint8_t *pb = sB + (wn * kWTN + t * 32 + frow) * kBK;
+        const u32x4 b0 = *(const GPIC_LDS u32x4 *)(pb + lo), b1 = *(const GPIC_LDS u32x4 *)(pb + hi);
+        fb[step][t] = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+      }
+    }
   };
 
-  v4f acc[Cfg::kTN][Cfg::kTM];
+  v16f acc[kTN][kTM];
 #pragma unroll
-  for (int i = 0; i < Cfg::kTN; i++)
+  for (int i = 0; i < kTN; i++)
 #pragma unroll
-    for (int j = 0; j < Cfg::kTM; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kTM; j++) acc[i][j] = v16f{};
 
-  const int nk = (kend - kbeg + kBK - 1) / kBK;
-  if (nk > 0) issue(0, kbeg);
+  // Phase boundary: a bare s_barrier (no fence: the waits each side needs are explicit, so the loads group 0 issued
+  // in its memory phase stay in flight through it), pinned with sched_barrier so the compiler cannot move MFMAs
+  // (register-only instructions) across it into the other group's phase.
+  auto phase_barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: group 0 sends tile 0; every wave waits for its own loads, then all meet, so tile 0 is complete in LDS
+  // before anyone reads it. Group 1 then passes one extra barrier to run one phase behind group 0.
+  if (group == 0 && nk > 0) issue(0, kbeg);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
+  phase_barrier();
+  if (group == 1) phase_barrier();
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & 1;
-    if (kt + 1 < nk) issue(st ^ 1, kbeg + (kt + 1) * kBK);
-    const GPIC_LDS uint8_t *sA = (const GPIC_LDS uint8_t *)smem + st * Cfg::kStageBytes;
-    const GPIC_LDS uint8_t *sB = sA + BM * kBK;
-    v8i af[Cfg::kTM];
+    // memory phase: send tile kt + 1 (group 0), read this wave's fragments of tile kt
+    if (group == 0 && kt + 1 < nk) issue(st ^ 1, kbeg + (kt + 1) * kBK);
+    read(st);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stage before anyone overwrites it
+    phase_barrier();
+    // MFMA phase
 #pragma unroll
-    for (int mi = 0; mi < Cfg::kTM; mi++) af[mi] = frag(sA, wm * Cfg::kWTM + mi * 16 + (lane & 15));
+    for (int step = 0; step < 2; step++)
 #pragma unroll
-    for (int ni = 0; ni < Cfg::kTN; ni++) {
-      const v8i bf = frag(sB, wn * Cfg::kWTN + ni * 16 + (lane & 15));
+      for (int ni = 0; ni < kTN; ni++)
 #pragma unroll
-      for (int mi = 0; mi < Cfg::kTM; mi++)
-        acc[ni][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af[mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+        for (int mi = 0; mi < kTM; mi++)
+          acc[ni][mi] =
+              __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[step][ni], fa[step][mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
+    if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kt + 1 has landed in LDS
+    phase_barrier();
   }
+  if (group == 0) phase_barrier();
 
-  // ---- epilogue: lane holds C[m][n..n+3] for each MFMA tile
+  // ---- epilogue: acc[ni][mi] lane l holds D[n][m] for m = mi * 32 + (l & 31) and
+  // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns
   const float s = sa[0] * sb[0];
 #pragma unroll
-  for (int ni = 0; ni < Cfg::kTN; ni++) {
-    const int n = n0 + wn * Cfg::kWTN + ni * 16 + 4 * (lane >> 4);
+  for (int ni = 0; ni < kTN; ni++) {
 #pragma unroll
-    for (int mi = 0; mi < Cfg::kTM; mi++) {
-      const int m = m0 + wm * Cfg::kWTM + mi * 16 + (lane & 15);
-      if (m >= M || n >= N) continue;
-      const v4f v = acc[ni][mi];
-      if (P) {
-        *reinterpret_cast<v4f *>(P + ((int64_t)split * M + m) * N + n) = v;
-      } else {
-        uint32_t h[4];
+    for (int mi = 0; mi < kTM; mi++) {
+      const int m = m0 + wm * kWTM + mi * 32 + (lane & 31);
+      if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < 4; j++) h[j] = bf16_rne(v[j] * s);
-        if (bias) {
-          const u32x2 bw = *reinterpret_cast<const u32x2 *>(bias + n);
-          h[0] = bf16_rne(bf16_lo(h[0]) + bf16_lo(bw.x));
-          h[1] = bf16_rne(bf16_lo(h[1]) + bf16_hi(bw.x));
-          h[2] = bf16_rne(bf16_lo(h[2]) + bf16_lo(bw.y));
-          h[3] = bf16_rne(bf16_lo(h[3]) + bf16_hi(bw.y));
+      for (int q = 0; q < 4; q++) {
+        const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (lane >> 5);
+        if (n >= N) continue;
+        const v16f &v = acc[ni][mi];
+        if (P) {
+          *reinterpret_cast<v4f *>(P + ((int64_t)split * M + m) * N + n) =
+              v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int j = 0; j < 4; j++) h[j] = bf16_rne(v[4 * q + j] * s);
+          if (bias) {
+            const u32x2 bw = *reinterpret_cast<const u32x2 *>(bias + n);
+            h[0] = bf16_rne(bf16_lo(h[0]) + bf16_lo(bw.x));
+            h[1] = bf16_rne(bf16_lo(h[1]) + bf16_hi(bw.x));
+            h[2] = bf16_rne(bf16_lo(h[2]) + bf16_lo(bw.y));
+            h[3] = bf16_rne(bf16_lo(h[3]) + bf16_hi(bw.y));
+          }
+          *reinterpret_cast<u32x2 *>(C + (int64_t)m * ldc + n) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
         }
-        *reinterpret_cast<u32x2 *>(C + (int64_t)m * ldc + n) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
     }
   }
@@ -203,9 +253,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 }
 
 // ------------------------------------------------------------------------------------------- host side
-
-constexpr int kBM = 256, kBN = 256, kWM = 2, kWN = 2;
-using MainCfg = GemmCfg<kBM, kBN, kWM, kWN>;
 
 struct Plan {
   int tiles_m, tiles_n, splits, ksplit;
@@ -270,7 +317,7 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
     P = static_cast<float *>(ws);
   }
   const int grid = p.tiles_m * p.tiles_n * p.splits;
-  gemm_tn_kernel<kBM, kBN, kWM, kWN><<<grid, MainCfg::kThreads, 0, st>>>(
+  gemm_tn_kernel<<<grid, kThreads, 0, st>>>(
       A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
       p.splits);
   if (P) {

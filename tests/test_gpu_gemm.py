@@ -45,6 +45,28 @@ def rel(x, ref):
     return (torch.linalg.norm(x.float() - ref) / torch.linalg.norm(ref)).item()
 
 
+def assert_elementwise(c, a, sa, b, sb):
+    """Every element within one bf16 rounding of the exact scaled product (2^-8 relative) plus an fp32
+    accumulation-order allowance (2^-16 of the sum of |terms|). Catches localised corruption that a Frobenius norm
+    over millions of elements would average away."""
+    af = a.double() * float(sa)
+    bf = b.double() * float(sb)
+    exact = af @ bf.t()
+    bound = exact.abs() * 2.0 ** -8 + (af.abs() @ bf.abs().t()) * 2.0 ** -16
+    err = (c.double() - exact).abs()
+    bad = (err > bound).sum().item()
+    assert bad == 0, f"{bad} elements out of bounds; worst excess {(err - bound).max().item():.3g}"
+
+
+def pollute(dev):
+    """Run a GEMM over other data first, so every CU's LDS holds something else: a read of LDS before the loads that
+    should fill it would then show up as wrong values instead of lucky leftovers."""
+    g = torch.Generator(device=dev).manual_seed(99)
+    x = (torch.randn(4096, 2048, generator=g, device=dev) * 300).clamp(-448, 448).to(E4)
+    y = (torch.randn(2048, 2048, generator=g, device=dev) * 300).clamp(-448, 448).to(E4)
+    G.fp8_gemm(x, torch.ones(1, device=dev), y, torch.ones(1, device=dev))
+
+
 def test_exact_golden(dev, gold):
     a, b = e4(gold["gemm_a"], dev), e4(gold["gemm_b"], dev)
     sa = torch.tensor(gold["gemm_sa"], device=dev)
@@ -64,6 +86,7 @@ def test_exact_integers(dev, M, N, K):
     b = torch.randint(-4, 5, (N, K), generator=g, device=dev).float().to(E4)
     sa = torch.tensor([0.5], device=dev)
     sb = torch.tensor([0.25], device=dev)
+    pollute(dev)
     c = G.fp8_gemm(a, sa, b, sb)
     exact = (a.double() @ b.double().t()) * 0.125
     assert torch.equal(c, exact.float().to(torch.bfloat16))
@@ -83,7 +106,9 @@ def test_against_oracle(dev, M, N, K):
     b = rand_e4((N, K), 40.0, 3, dev)
     sa = torch.tensor([0.013], device=dev)
     sb = torch.tensor([0.021], device=dev)
+    pollute(dev)
     c = G.fp8_gemm(a, sa, b, sb)
+    assert_elementwise(c, a, 0.013, b, 0.021)
     if M * N * K <= 2 ** 31:
         ref = torch.from_numpy(O.mm64(a.view(torch.uint8).cpu().numpy(), np.float32(0.013),
                                       b.view(torch.uint8).cpu().numpy(), np.float32(0.021))).float().to(dev)
@@ -91,7 +116,8 @@ def test_against_oracle(dev, M, N, K):
         ref = ref_fp32(a, sa, b, sb)
     r = rel(c, ref)
     assert r <= TOL and r < 4e-3
-    # deterministic, including the split-K shapes
+    # deterministic, including the split-K shapes, whatever ran before
+    pollute(dev)
     assert torch.equal(c, G.fp8_gemm(a, sa, b, sb))
 
 
@@ -126,5 +152,7 @@ def test_d12_shapes(dev, name, M, N, K):
     w = (torch.randn(N, K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16)
     xq, sx = G.tcast(x)
     wq, sw = G.tcast(w)
+    pollute(dev)
     c = G.fp8_gemm(xq, sx, wq, sw)
     assert rel(c, ref_fp32(xq, sx, wq, sw)) < 4e-3
+    assert_elementwise(c, xq, sx.item(), wq, sw.item())
