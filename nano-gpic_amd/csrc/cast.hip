@@ -12,38 +12,54 @@
 
 namespace gpic {
 
+constexpr int kUnroll = 4;    // 16-element units per thread in flight in the streaming passes
+
 // ------------------------------------------------------------------------------------------- pass 1: amax
 
-// x: n elements of T (bf16 as uint16_t, or float), 16-byte aligned. Units of 16 elements; the n % 16 tail is read
-// by the first threads of workgroup 0.
+__device__ __forceinline__ uint32_t absbits_bf16(uint16_t h) { return (uint32_t)(h & 0x7fffu) << 16; }
+__device__ __forceinline__ uint32_t absbits_f32(float f) { return __float_as_uint(f) & 0x7fffffffu; }
+
+// Max of |x| over a 16-byte word: packed u16 maxima for bf16 (NaN included; caught by the caller), u32 for fp32.
+template <typename T>
+__device__ __forceinline__ uint32_t word_max(uint32_t m, u32x4 w) {
+  if constexpr (sizeof(T) == 2) {
+    m = pk_max_u16(m, w.x & 0x7fff7fffu);
+    m = pk_max_u16(m, w.y & 0x7fff7fffu);
+    m = pk_max_u16(m, w.z & 0x7fff7fffu);
+    return pk_max_u16(m, w.w & 0x7fff7fffu);
+  } else {
+    const uint32_t a = max(max(w.x & 0x7fffffffu, w.y & 0x7fffffffu), max(w.z & 0x7fffffffu, w.w & 0x7fffffffu));
+    return max(m, a);
+  }
+}
+
+// x: n elements of T (bf16 as uint16_t, or float), 16-byte aligned, read as units of 16 elements (kUnroll units per
+// thread per iteration, all loads issued first); the n % 16 tail is read by the first threads of workgroup 0.
+// Writes max |x| over the non-NaN elements of this workgroup's share to partial[blockIdx.x].
 template <typename T>
 __global__ __launch_bounds__(kCastThreads) void amax_kernel(const T *__restrict__ x, int64_t n,
                                                              uint32_t *__restrict__ partial) {
-  constexpr int kWords = 16 * sizeof(T) / 16;  // 16-byte words per unit: 2 (bf16) or 4 (fp32)
+  constexpr int kWords = sizeof(T);   // 16-byte words per 16-element unit: 2 (bf16) or 4 (fp32)
   const int64_t units = n / 16;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const u32x4 *xv = reinterpret_cast<const u32x4 *>(x);
   uint32_t m = 0;
-  bool nan = false;
-  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x) {
-    u32x4 w[kWords];
+  int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; u + (kUnroll - 1) * stride < units; u += kUnroll * stride) {
+    u32x4 w[kUnroll][kWords];
 #pragma unroll
-    for (int i = 0; i < kWords; i++) w[i] = __builtin_nontemporal_load(xv + u * kWords + i);
-    if constexpr (sizeof(T) == 2) {
+    for (int k = 0; k < kUnroll; k++)
 #pragma unroll
-      for (int i = 0; i < kWords; i++) {
-        m = pk_max_u16(m, w[i].x & 0x7fff7fffu);
-        m = pk_max_u16(m, w[i].y & 0x7fff7fffu);
-        m = pk_max_u16(m, w[i].z & 0x7fff7fffu);
-        m = pk_max_u16(m, w[i].w & 0x7fff7fffu);
-      }
-    } else {
+      for (int i = 0; i < kWords; i++) w[k][i] = __builtin_nontemporal_load(xv + (u + k * stride) * kWords + i);
 #pragma unroll
-      for (int i = 0; i < kWords; i++) {
-        uint32_t a = max(max(w[i].x & 0x7fffffffu, w[i].y & 0x7fffffffu), max(w[i].z & 0x7fffffffu, w[i].w & 0x7fffffffu));
-        m = max(m, a);
-      }
-    }
+    for (int k = 0; k < kUnroll; k++)
+#pragma unroll
+      for (int i = 0; i < kWords; i++) m = word_max<T>(m, w[k][i]);
   }
+  for (; u < units; u += stride)
+#pragma unroll
+    for (int i = 0; i < kWords; i++) m = word_max<T>(m, __builtin_nontemporal_load(xv + u * kWords + i));
+  bool nan;
   if constexpr (sizeof(T) == 2) {
     m = max(m & 0xffffu, m >> 16);
     nan = m > 0x7f80u;
@@ -53,17 +69,17 @@ __global__ __launch_bounds__(kCastThreads) void amax_kernel(const T *__restrict_
   }
   if (nan) {  // rare: this thread saw a NaN; fold its elements again without them (tl.max is maxnum)
     m = 0;
-    for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x)
+    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < units; v += stride)
       for (int i = 0; i < 16; i++) {
-        uint32_t a = sizeof(T) == 2 ? ((uint32_t)(reinterpret_cast<const uint16_t *>(x)[u * 16 + i] & 0x7fffu) << 16)
-                                    : (__float_as_uint(reinterpret_cast<const float *>(x)[u * 16 + i]) & 0x7fffffffu);
+        const uint32_t a = sizeof(T) == 2 ? absbits_bf16(reinterpret_cast<const uint16_t *>(x)[v * 16 + i])
+                                          : absbits_f32(reinterpret_cast<const float *>(x)[v * 16 + i]);
         if (a <= 0x7f800000u) m = max(m, a);
       }
   }
   if (blockIdx.x == 0 && threadIdx.x < (n & 15)) {
     const int64_t i = units * 16 + threadIdx.x;
-    uint32_t a = sizeof(T) == 2 ? ((uint32_t)(reinterpret_cast<const uint16_t *>(x)[i] & 0x7fffu) << 16)
-                                : (__float_as_uint(reinterpret_cast<const float *>(x)[i]) & 0x7fffffffu);
+    const uint32_t a = sizeof(T) == 2 ? absbits_bf16(reinterpret_cast<const uint16_t *>(x)[i])
+                                      : absbits_f32(reinterpret_cast<const float *>(x)[i]);
     if (a <= 0x7f800000u) m = max(m, a);
   }
   m = block_max_u32(m);
@@ -80,58 +96,143 @@ __device__ __forceinline__ uint32_t fold_partials(const uint32_t *__restrict__ p
 // ------------------------------------------------------------------------------------------- pass 2: flat cast
 
 template <typename T>
+__device__ __forceinline__ u32x4 cast_unit(const u32x4 (&w)[sizeof(T)], float scale) {
+  if constexpr (sizeof(T) == 2) {
+    const u32x2 a = cast8_bf16(w[0], scale), b = cast8_bf16(w[1], scale);
+    return u32x4{a.x, a.y, b.x, b.y};
+  } else {
+    return u32x4{cast4_f32(w[0], scale), cast4_f32(w[1], scale), cast4_f32(w[2], scale), cast4_f32(w[3], scale)};
+  }
+}
+
+template <typename T>
 __global__ __launch_bounds__(kCastThreads) void cast_kernel(const T *__restrict__ x, int64_t n,
                                                              const uint32_t *__restrict__ partial, int nparts,
                                                              uint8_t *__restrict__ q, float *__restrict__ dequant) {
-  constexpr int kWords = 16 * sizeof(T) / 16;
+  constexpr int kWords = sizeof(T);
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);
   if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
   const int64_t units = n / 16;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const u32x4 *xv = reinterpret_cast<const u32x4 *>(x);
   u32x4 *qv = reinterpret_cast<u32x4 *>(q);
-  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x) {
+  int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; u + (kUnroll - 1) * stride < units; u += kUnroll * stride) {
+    u32x4 w[kUnroll][kWords];
+#pragma unroll
+    for (int k = 0; k < kUnroll; k++)
+#pragma unroll
+      for (int i = 0; i < kWords; i++) w[k][i] = __builtin_nontemporal_load(xv + (u + k * stride) * kWords + i);
+#pragma unroll
+    for (int k = 0; k < kUnroll; k++) __builtin_nontemporal_store(cast_unit<T>(w[k], scale), qv + u + k * stride);
+  }
+  for (; u < units; u += stride) {
     u32x4 w[kWords];
 #pragma unroll
     for (int i = 0; i < kWords; i++) w[i] = __builtin_nontemporal_load(xv + u * kWords + i);
-    u32x4 o;
-    if constexpr (sizeof(T) == 2) {
-      u32x2 a = cast8_bf16(w[0], scale), b = cast8_bf16(w[1], scale);
-      o = u32x4{a.x, a.y, b.x, b.y};
-    } else {
-      o = u32x4{cast4_f32(w[0], scale), cast4_f32(w[1], scale), cast4_f32(w[2], scale), cast4_f32(w[3], scale)};
-    }
-    __builtin_nontemporal_store(o, qv + u);
+    __builtin_nontemporal_store(cast_unit<T>(w, scale), qv + u);
   }
   if (blockIdx.x == 0 && threadIdx.x < (n & 15)) {
     const int64_t i = units * 16 + threadIdx.x;
-    float v = sizeof(T) == 2 ? bf16_lo(reinterpret_cast<const uint16_t *>(x)[i])
-                             : reinterpret_cast<const float *>(x)[i];
+    const float v = sizeof(T) == 2 ? bf16_lo(reinterpret_cast<const uint16_t *>(x)[i])
+                                   : reinterpret_cast<const float *>(x)[i];
     q[i] = (uint8_t)e4m3x4(sat(v * scale), 0.f, 0.f, 0.f);
   }
+}
+
+// ------------------------------------------------------------------------------------------- SwiGLU sigmoid table
+
+// sigmoid(z1) for the bf16 values z1 with exponent field in [kLutELo, kLutEHi], i.e. 2^-16 <= |z1| < 2^8, both signs
+// (6144 floats = 24 KiB of LDS). Each workgroup fills its table with the same sigmoid() the other values use, so a
+// lookup returns exactly what the computation would; values outside the range (rare: tiny, huge, zero, NaN) are
+// computed directly.
+constexpr int kLutELo = 111, kLutEHi = 134;
+constexpr int kLutHalf = (kLutEHi - kLutELo + 1) * 128;
+constexpr int kLutSize = 2 * kLutHalf;
+static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kCastWorkspaceBytes, "cast workspace too small");
+
+// The workspace: partial maxima at the start, the sigmoid table after them.
+__host__ __device__ inline float *ws_table(void *ws) { return reinterpret_cast<float *>((char *)ws + kMaxParts * 4); }
+
+__device__ __forceinline__ void lut_build(float *lut) {
+  for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) {
+    const uint32_t neg = i >= kLutHalf;
+    const uint32_t mag = (kLutELo << 7) + (uint32_t)(i - (neg ? kLutHalf : 0));
+    lut[i] = sigmoid(bf16_lo(mag | (neg << 15)));
+  }
+  __syncthreads();
+}
+
+// The same table copied from global memory (written by an earlier pass of the same call).
+__device__ __forceinline__ void lut_load(float *lut, const float *__restrict__ g) {
+  for (int i = threadIdx.x; i < kLutSize / 4; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(lut)[i] = reinterpret_cast<const u32x4 *>(g)[i];
+  __syncthreads();
+}
+
+// Eight sigmoids of the eight bf16 values of a 16-byte word; z holds their fp32 values.
+__device__ __forceinline__ void sigmoid8(const float *lut, u32x4 w, const float (&z)[8], float (&sg)[8]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  bool slow = false;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t h = (ws[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+    const uint32_t idx = (h & 0x7fffu) - (uint32_t)(kLutELo << 7);   // unsigned: below the range wraps high
+    const bool in = idx < (uint32_t)kLutHalf;
+    sg[i] = lut[in ? idx + ((h >> 15) ? kLutHalf : 0) : 0];
+    slow |= !in;
+  }
+  if (slow) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t h = (ws[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+      if ((h & 0x7fffu) - (uint32_t)(kLutELo << 7) >= (uint32_t)kLutHalf) sg[i] = sigmoid(z[i]);
+    }
+  }
+}
+
+__device__ __forceinline__ void unpack8(u32x4 w, float (&v)[8]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    v[2 * i] = bf16_lo(ws[i]);
+    v[2 * i + 1] = bf16_hi(ws[i]);
+  }
+}
+
+// a = bf16(bf16(z1 * sigmoid(z1)) * z2) for 8 pairs (fp8_native.py:55-58); returns exact bf16 values as fp32.
+__device__ __forceinline__ void swiglu8(const float *lut, u32x4 z1w, u32x4 z2w, float (&a)[8]) {
+  float z1[8], z2[8], sg[8];
+  unpack8(z1w, z1);
+  unpack8(z2w, z2);
+  sigmoid8(lut, z1w, z1, sg);
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = bf16_round(bf16_round(z1[i] * sg[i]) * z2[i]);
+}
+
+__device__ __forceinline__ uint32_t absbits_nonan(float v) {
+  const uint32_t a = __float_as_uint(v) & 0x7fffffffu;
+  return a > 0x7f800000u ? 0u : a;
 }
 
 // ------------------------------------------------------------------------------------------- pass 2: cast + transpose
 
 // Sources of the transposing cast: 8 consecutive elements (row r, columns c..c+7) as fp32.
 struct SrcBF16 {
+  static constexpr bool kLut = false;
   const uint16_t *x;
   int64_t ld;
-  __device__ __forceinline__ void load8(int64_t r, int64_t c, float (&v)[8]) const {
-    const u32x4 w = *reinterpret_cast<const u32x4 *>(x + r * ld + c);
-    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      v[2 * i] = bf16_lo(a[i]);
-      v[2 * i + 1] = bf16_hi(a[i]);
-    }
+  __device__ __forceinline__ void load8(int64_t r, int64_t c, float (&v)[8], const float *) const {
+    unpack8(*reinterpret_cast<const u32x4 *>(x + r * ld + c), v);
   }
 };
 
 struct SrcF32 {
+  static constexpr bool kLut = false;
   const float *x;
   int64_t ld;
-  __device__ __forceinline__ void load8(int64_t r, int64_t c, float (&v)[8]) const {
+  __device__ __forceinline__ void load8(int64_t r, int64_t c, float (&v)[8], const float *) const {
     const u32x4 w0 = *reinterpret_cast<const u32x4 *>(x + r * ld + c);
     const u32x4 w1 = *reinterpret_cast<const u32x4 *>(x + r * ld + c + 4);
     v[0] = __uint_as_float(w0.x), v[1] = __uint_as_float(w0.y), v[2] = __uint_as_float(w0.z);
@@ -140,102 +241,136 @@ struct SrcF32 {
   }
 };
 
-struct SrcSwiGLU;  // defined with the SwiGLU kernels below
+// The SwiGLU product a of z [M, 2H] (row stride sz), as a source of H columns.
+struct SrcSwiGLU {
+  static constexpr bool kLut = true;
+  const uint16_t *z;
+  int64_t sz, H;
+  const float *table;   // the sigmoid table the amax pass of this call wrote
+  __device__ __forceinline__ void load8(int64_t r, int64_t c, float (&v)[8], const float *lut) const {
+    const u32x4 z1 = *reinterpret_cast<const u32x4 *>(z + r * sz + c);
+    const u32x4 z2 = *reinterpret_cast<const u32x4 *>(z + r * sz + H + c);
+    swiglu8(lut, z1, z2, v);
+  }
+};
 
 // src [rows, cols] (cols % 8 == 0) -> q [rows, cols] (row stride ldq; skipped when q == nullptr) and the transposed
 // bytes qt [cols, ldt] (ldt % 16 == 0, ldt >= rows), whose columns rows..ldt-1 are written as zeros so a GEMM can
-// reduce over the padded length. Tile: 64 rows x 64 cols per workgroup of 256 threads; the transpose goes through
-// LDS. The scale comes from the partial maxima of the matching amax pass.
+// reduce over the padded length. Tile: 128 rows x 128 columns per workgroup of 256 threads, so both outputs are
+// stored as whole 128-byte lines (q: 16 lanes x 8 bytes per row; qt: 8 lanes x 16 bytes per row); the transpose goes
+// through LDS. Each thread has its 8 loads in flight at once. The scale comes from the partial maxima of the
+// matching amax pass.
+constexpr int kTT = 128;   // transposing tile side
+
 template <class Src>
 __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int64_t cols,
                                                       const uint32_t *__restrict__ partial, int nparts,
                                                       uint8_t *__restrict__ q, int64_t ldq, uint8_t *__restrict__ qt,
                                                       int64_t ldt, float *__restrict__ dequant) {
-  __shared__ uint32_t tile[64][64 / 4 + 1];  // [row][col / 4] e4m3 bytes; one word of padding per row
+  constexpr int kPitch = kTT / 4 + 1;          // words per LDS row (one word of padding)
+  __shared__ uint32_t tile[kTT * kPitch];      // [row][col / 4] e4m3 bytes
+  const float *lut = nullptr;
+  if constexpr (Src::kLut) {
+    __shared__ float table[kLutSize];
+    lut_load(table, src.table);
+    lut = table;
+  }
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *dequant = deq;
-  const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
+  constexpr int kPer = kTT * (kTT / 8) / 256;  // 8-element chunks per thread per tile: 8
+  const uint8_t *tb = reinterpret_cast<const uint8_t *>(tile);
+  // The SwiGLU source walks tiles (persistent workgroups); the others take exactly one tile each.
+  const int64_t tstep = Src::kLut ? (int64_t)gridDim.x : tiles;
+  for (int64_t t = blockIdx.x; t < tiles; t += tstep) {   // tiles walked column-block fastest
+    const int64_t c0 = (t % tiles_c) * kTT, r0 = (t / tiles_c) * kTT;
+    float v[kPer][8];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int ci = threadIdx.x + 256 * i;
-    const int r = ci >> 3, cc = ci & 7;
-    const int64_t gr = r0 + r, gc = c0 + cc * 8;
-    u32x2 o = {0u, 0u};
-    if (gr < rows && gc < cols) {
-      float v[8];
-      src.load8(gr, gc, v);
-      o.x = e4m3x4(sat(v[0] * scale), sat(v[1] * scale), sat(v[2] * scale), sat(v[3] * scale));
-      o.y = e4m3x4(sat(v[4] * scale), sat(v[5] * scale), sat(v[6] * scale), sat(v[7] * scale));
-      if (q) *reinterpret_cast<u32x2 *>(q + gr * ldq + gc) = o;
+    for (int i = 0; i < kPer; i++) {
+      const int id = threadIdx.x + 256 * i;
+      const int r = id >> 4, cc = id & 15;
+      const int64_t gr = r0 + r, gc = c0 + 8 * cc;
+      if (gr < rows && gc < cols) src.load8(gr, gc, v[i], lut);
     }
-    tile[r][cc * 2] = o.x;
-    tile[r][cc * 2 + 1] = o.y;
-  }
-  __syncthreads();
-  // qt row c0 + c gets bytes r0 + 16p .. r0 + 16p + 15: thread t -> c = t / 4, p = t % 4
-  const int c = threadIdx.x >> 2, p = threadIdx.x & 3;
-  const int64_t gc = c0 + c, gr = r0 + 16 * p;
-  if (gc < cols && gr < ldt) {
-    const uint8_t *tb = reinterpret_cast<const uint8_t *>(&tile[0][0]);
-    constexpr int kRowBytes = (64 / 4 + 1) * 4;
-    uint32_t o[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      uint32_t v = 0;
-#pragma unroll
-      for (int b = 0; b < 4; b++) v |= (uint32_t)tb[(16 * p + 4 * j + b) * kRowBytes + c] << (8 * b);
-      o[j] = v;
+    for (int i = 0; i < kPer; i++) {
+      const int id = threadIdx.x + 256 * i;
+      const int r = id >> 4, cc = id & 15;
+      const int64_t gr = r0 + r, gc = c0 + 8 * cc;
+      u32x2 o = {0u, 0u};
+      if (gr < rows && gc < cols) {
+        o.x = e4m3x4(sat(v[i][0] * scale), sat(v[i][1] * scale), sat(v[i][2] * scale), sat(v[i][3] * scale));
+        o.y = e4m3x4(sat(v[i][4] * scale), sat(v[i][5] * scale), sat(v[i][6] * scale), sat(v[i][7] * scale));
+        if (q) *reinterpret_cast<u32x2 *>(q + gr * ldq + gc) = o;
+      }
+      tile[r * kPitch + 2 * cc] = o.x;
+      tile[r * kPitch + 2 * cc + 1] = o.y;
     }
-    *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = u32x4{o[0], o[1], o[2], o[3]};
-  }
-}
-
-// ------------------------------------------------------------------------------------------- SwiGLU
-
-// a = bf16(bf16(z1 * sigmoid(z1)) * z2) for one z1 / z2 pair of bf16 (fp8_native.py:55-58).
-__device__ __forceinline__ float swiglu1(float z1, float z2) {
-  float sl = bf16_round(z1 * sigmoid(z1));
-  return bf16_round(sl * z2);
-}
-
-// Eight products from 16-byte words of z1 and z2; returns them as fp32 (exact bf16 values).
-__device__ __forceinline__ void swiglu8(u32x4 z1, u32x4 z2, float (&a)[8]) {
-  const uint32_t w1[4] = {z1.x, z1.y, z1.z, z1.w}, w2[4] = {z2.x, z2.y, z2.z, z2.w};
+    __syncthreads();
+    // qt row c0 + c gets bytes r0 + 16 p .. r0 + 16 p + 15 of its column
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    a[2 * i] = swiglu1(bf16_lo(w1[i]), bf16_lo(w2[i]));
-    a[2 * i + 1] = swiglu1(bf16_hi(w1[i]), bf16_hi(w2[i]));
+    for (int j = 0; j < kTT * (kTT / 16) / 256; j++) {
+      const int id = threadIdx.x + 256 * j;
+      const int c = id >> 3, p = id & 7;
+      const int64_t gc = c0 + c, gr = r0 + 16 * p;
+      if (gc < cols && gr < ldt) {
+        uint32_t o[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          uint32_t x = 0;
+#pragma unroll
+          for (int b = 0; b < 4; b++) x |= (uint32_t)tb[(16 * p + 4 * w + b) * (4 * kPitch) + c] << (8 * b);
+          o[w] = x;
+        }
+        *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+    if constexpr (!Src::kLut) break;
+    __syncthreads();   // the tile buffer is rewritten by the next tile
   }
 }
 
-struct SrcSwiGLU {
-  const uint16_t *z;
-  int64_t sz, H;
-  __device__ __forceinline__ void load8(int64_t r, int64_t c, float (&v)[8]) const {
-    const u32x4 z1 = *reinterpret_cast<const u32x4 *>(z + r * sz + c);
-    const u32x4 z2 = *reinterpret_cast<const u32x4 *>(z + r * sz + H + c);
-    swiglu8(z1, z2, v);
-  }
-};
+// ------------------------------------------------------------------------------------------- SwiGLU kernels
 
-__device__ __forceinline__ uint32_t absbits_nonan(float v) {
-  uint32_t a = __float_as_uint(v) & 0x7fffffffu;
-  return a > 0x7f800000u ? 0u : a;
-}
+// z [M, 2H] bf16 (row stride sz, H % 8 == 0): rows strided over workgroups (kRowsPer rows at a time, all their
+// loads issued first), 8-element units over threads. Workgroup 0 also publishes its sigmoid table to `table` for the
+// cast pass of the same call.
+constexpr int kRowsPer = 4;
 
-// z [M, 2H] bf16 (row stride sz, H % 8 == 0): rows strided over workgroups, 8-element units over threads.
 __global__ __launch_bounds__(kCastThreads) void swiglu_amax_kernel(const uint16_t *__restrict__ z, int64_t M, int64_t H,
-                                                                    int64_t sz, uint32_t *__restrict__ partial) {
+                                                                    int64_t sz, uint32_t *__restrict__ partial,
+                                                                    float *__restrict__ table) {
+  __shared__ float lut[kLutSize];
+  lut_build(lut);
+  if (blockIdx.x == 0 && table)
+    for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) table[i] = lut[i];
   const int64_t units = H / 8;
+  const int64_t rstride = gridDim.x;
   uint32_t m = 0;
-  for (int64_t r = blockIdx.x; r < M; r += gridDim.x) {
-    const uint16_t *zr = z + r * sz;
-    for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
-      u32x4 z1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
-      u32x4 z2 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
+  for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
+    int64_t r = blockIdx.x;
+    for (; r + (kRowsPer - 1) * rstride < M; r += kRowsPer * rstride) {
+      u32x4 z1[kRowsPer], z2[kRowsPer];
+#pragma unroll
+      for (int k = 0; k < kRowsPer; k++) {
+        const uint16_t *zr = z + (r + k * rstride) * sz;
+        z1[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
+        z2[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
+      }
+#pragma unroll
+      for (int k = 0; k < kRowsPer; k++) {
+        float a[8];
+        swiglu8(lut, z1[k], z2[k], a);
+#pragma unroll
+        for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(a[i]));
+      }
+    }
+    for (; r < M; r += rstride) {
+      const uint16_t *zr = z + r * sz;
       float a[8];
-      swiglu8(z1, z2, a);
+      swiglu8(lut, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u)),
+              __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u)), a);
 #pragma unroll
       for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(a[i]));
     }
@@ -247,7 +382,10 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_amax_kernel(const uint16_
 __global__ __launch_bounds__(kCastThreads) void swiglu_cast_kernel(const uint16_t *__restrict__ z, int64_t M, int64_t H,
                                                                     int64_t sz, const uint32_t *__restrict__ partial,
                                                                     int nparts, uint8_t *__restrict__ q, int64_t sq,
-                                                                    float *__restrict__ dequant) {
+                                                                    float *__restrict__ dequant,
+                                                                    const float *__restrict__ table) {
+  __shared__ float lut[kLutSize];
+  lut_load(lut, table);
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);
   if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
@@ -255,10 +393,10 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_cast_kernel(const uint16_
   for (int64_t r = blockIdx.x; r < M; r += gridDim.x) {
     const uint16_t *zr = z + r * sz;
     for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
-      u32x4 z1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
-      u32x4 z2 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
+      const u32x4 z1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
+      const u32x4 z2 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
       float a[8];
-      swiglu8(z1, z2, a);
+      swiglu8(lut, z1, z2, a);
       u32x2 o;
       o.x = e4m3x4(sat(a[0] * scale), sat(a[1] * scale), sat(a[2] * scale), sat(a[3] * scale));
       o.y = e4m3x4(sat(a[4] * scale), sat(a[5] * scale), sat(a[6] * scale), sat(a[7] * scale));
@@ -273,42 +411,39 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
                                                                    const uint16_t *__restrict__ da, int64_t M, int64_t H,
                                                                    int64_t sz, int64_t sda, uint16_t *__restrict__ dz,
                                                                    int64_t sdz, uint32_t *__restrict__ partial) {
+  __shared__ float lut[kLutSize];
+  lut_build(lut);
   const int64_t units = H / 8;
   uint32_t m = 0;
   for (int64_t r = blockIdx.x; r < M; r += gridDim.x) {
     const uint16_t *zr = z + r * sz;
     for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
-      u32x4 z1v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
-      u32x4 z2v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
-      u32x4 dav = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + r * sda + 8 * u));
-      const uint32_t w1[4] = {z1v.x, z1v.y, z1v.z, z1v.w}, w2[4] = {z2v.x, z2v.y, z2v.z, z2v.w},
-                     wd[4] = {dav.x, dav.y, dav.z, dav.w};
-      uint32_t o1[4], o2[4];
+      const u32x4 z1v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
+      const u32x4 z2v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
+      const u32x4 dav = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + r * sda + 8 * u));
+      float z1[8], z2[8], dv[8], sg[8];
+      unpack8(z1v, z1);
+      unpack8(z2v, z2);
+      unpack8(dav, dv);
+      sigmoid8(lut, z1v, z1, sg);
+      uint32_t h1[8], h2[8];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        uint32_t h1[2], h2[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const float z1 = j ? bf16_hi(w1[i]) : bf16_lo(w1[i]);
-          const float z2 = j ? bf16_hi(w2[i]) : bf16_lo(w2[i]);
-          const float dv = j ? bf16_hi(wd[i]) : bf16_lo(wd[i]);
-          const float sg = sigmoid(z1);
-          const float sl = bf16_round(z1 * sg);
-          const float t1 = 1.0f - sg;
-          const float t2 = z1 * t1;
-          const float t3 = 1.0f + t2;
-          const float g = sg * t3;
-          const float pr = dv * z2;
-          h1[j] = bf16_rne(pr * g);
-          h2[j] = bf16_rne(dv * sl);
-          m = max(m, absbits_nonan(__uint_as_float(h1[j] << 16)));
-          m = max(m, absbits_nonan(__uint_as_float(h2[j] << 16)));
-        }
-        o1[i] = h1[0] | (h1[1] << 16);
-        o2[i] = h2[0] | (h2[1] << 16);
+      for (int i = 0; i < 8; i++) {
+        const float sl = bf16_round(z1[i] * sg[i]);
+        const float t1 = 1.0f - sg[i];
+        const float t2 = z1[i] * t1;
+        const float t3 = 1.0f + t2;
+        const float g = sg[i] * t3;
+        const float pr = dv[i] * z2[i];
+        h1[i] = bf16_rne(pr * g);
+        h2[i] = bf16_rne(dv[i] * sl);
+        m = max(m, absbits_nonan(__uint_as_float(h1[i] << 16)));
+        m = max(m, absbits_nonan(__uint_as_float(h2[i] << 16)));
       }
-      *reinterpret_cast<u32x4 *>(dz + r * sdz + 8 * u) = u32x4{o1[0], o1[1], o1[2], o1[3]};
-      *reinterpret_cast<u32x4 *>(dz + r * sdz + H + 8 * u) = u32x4{o2[0], o2[1], o2[2], o2[3]};
+      *reinterpret_cast<u32x4 *>(dz + r * sdz + 8 * u) =
+          u32x4{h1[0] | (h1[1] << 16), h1[2] | (h1[3] << 16), h1[4] | (h1[5] << 16), h1[6] | (h1[7] << 16)};
+      *reinterpret_cast<u32x4 *>(dz + r * sdz + H + 8 * u) =
+          u32x4{h2[0] | (h2[1] << 16), h2[2] | (h2[3] << 16), h2[4] | (h2[5] << 16), h2[6] | (h2[7] << 16)};
     }
   }
   m = block_max_u32(m);
@@ -325,9 +460,9 @@ static inline int grid_for(int64_t units, int cap) {
 template <typename T>
 static int launch_tcast(const T *x, int64_t n, uint8_t *q, float *dequant, uint32_t *partial, hipStream_t st) {
   const int64_t units = n / 16;
-  const int ga = grid_for((units + 3) / 4, kMaxParts);
+  const int ga = grid_for((units + kUnroll - 1) / kUnroll, kAmaxBlocks);
   amax_kernel<T><<<ga, kCastThreads, 0, st>>>(x, n, partial);
-  const int gc = grid_for(units, kMaxCastBlocks);
+  const int gc = grid_for((units + kUnroll - 1) / kUnroll, kMaxCastBlocks);
   cast_kernel<T><<<gc, kCastThreads, 0, st>>>(x, n, partial, ga, q, dequant);
   return (int)hipGetLastError();
 }
@@ -335,11 +470,15 @@ static int launch_tcast(const T *x, int64_t n, uint8_t *q, float *dequant, uint3
 template <class Src>
 static void launch_cast_t(Src src, int64_t rows, int64_t cols, int nparts, uint8_t *q, int64_t ldq, uint8_t *qt,
                           int64_t ldt, float *dequant, const uint32_t *partial, hipStream_t st) {
-  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((ldt + 63) / 64));
+  // One tile per workgroup, except for the SwiGLU source: its workgroups copy the 24 KiB sigmoid table first, so
+  // they stay resident and walk the tiles.
+  const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
+  const int grid = (int)(!Src::kLut || tiles < kCastTBlocks ? tiles : kCastTBlocks);
   cast_t_kernel<Src><<<grid, 256, 0, st>>>(src, rows, cols, partial, nparts, q, ldq, qt, ldt, dequant);
 }
 
-static inline int swiglu_grid(int64_t M) { return (int)(M < 1 ? 1 : (M > kMaxParts ? kMaxParts : M)); }
+// SwiGLU kernels: rows strided over at most kSwigluBlocks workgroups (each builds its 24 KiB sigmoid table once).
+static inline int swiglu_grid(int64_t M) { return (int)(M < 1 ? 1 : (M > kSwigluBlocks ? kSwigluBlocks : M)); }
 
 }  // namespace gpic
 
@@ -369,7 +508,7 @@ int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int64_t n = rows * cols;
-  const int ga = grid_for((n / 16 + 3) / 4, kMaxParts);
+  const int ga = grid_for((n / 16 + kUnroll - 1) / kUnroll, kAmaxBlocks);
   if (dtype == GPIC_DTYPE_BF16)
     amax_kernel<uint16_t><<<ga, kCastThreads, 0, st>>>(static_cast<const uint16_t *>(x), n, partial);
   else
@@ -393,8 +532,8 @@ int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, u
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial);
-  swiglu_cast_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, g, q, sq, dequant);
+  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws));
+  swiglu_cast_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, g, q, sq, dequant, ws_table(ws));
   return (int)hipGetLastError();
 }
 
@@ -408,11 +547,11 @@ int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz,
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial);
+  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws));
   if (H == 0 || ldt == 0)
     cast_kernel<uint16_t><<<1, kCastThreads, 0, st>>>(nullptr, 0, partial, g, nullptr, dequant);
   else
-    launch_cast_t(SrcSwiGLU{z, sz, H}, M, H, g, q, sq, qt, ldt, dequant, partial, st);
+    launch_cast_t(SrcSwiGLU{z, sz, H, ws_table(ws)}, M, H, g, q, sq, qt, ldt, dequant, partial, st);
   return (int)hipGetLastError();
 }
 
@@ -426,7 +565,7 @@ static int swiglu_bwd_common(const uint16_t *z, const uint16_t *da, int64_t M, i
   if (dzqt && H > 0 && ldt > 0) {
     launch_cast_t(SrcBF16{dz, 2 * H}, M, 2 * H, g, dzq, 2 * H, dzqt, ldt, dequant, partial, st);
   } else {
-    const int gc = grid_for(n / 16, kMaxCastBlocks);
+    const int gc = grid_for((n / 16 + kUnroll - 1) / kUnroll, kMaxCastBlocks);
     cast_kernel<uint16_t><<<gc, kCastThreads, 0, st>>>(dz, n, partial, g, dzq, dequant);
   }
   return (int)hipGetLastError();

@@ -9,8 +9,11 @@ namespace gpic {
 
 constexpr int kCastThreads = 256;                     // threads per workgroup of the streaming cast kernels
 constexpr int kMaxParts = 1024;                       // at most this many partial maxima per amax pass
+constexpr int kAmaxBlocks = 512;                      // workgroups of a flat amax pass
+constexpr int kSwigluBlocks = 512;                    // workgroups of a SwiGLU pass
 constexpr int kMaxCastBlocks = 8192;                  // workgroups of a streaming cast pass
-constexpr size_t kCastWorkspaceBytes = kMaxParts * 4; // the partial maxima
+constexpr int kCastTBlocks = 1024;                    // workgroups of a (persistent) transposing cast pass
+constexpr size_t kCastWorkspaceBytes = 32 * 1024;     // partial maxima (4 KiB) + the SwiGLU sigmoid table (24 KiB)
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
