@@ -29,6 +29,11 @@
 namespace gpic {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+// The C staging block is written 8 bytes and read 16 bytes at a time: types that may alias each other, or
+// type-based alias analysis would treat the reads as independent of the writes.
+typedef uint32_t st8_t __attribute__((ext_vector_type(2), __may_alias__));
+typedef uint32_t st16_t __attribute__((ext_vector_type(4), __may_alias__));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 #define GPIC_LDS __attribute__((address_space(3)))
@@ -38,6 +43,7 @@ constexpr int kThreads = 512;                          // 8 waves: 2 groups x 4
 constexpr int kWTM = 64, kWTN = 128;                   // wave tile
 constexpr int kTM = kWTM / 32, kTN = kWTN / 32;        // 32 x 32 MFMA tiles per wave: 2 x 4
 constexpr int kStageBytes = (kBM + kBN) * kBK;         // 64 KiB
+constexpr int kCStageBytes = 32 * 128;                 // per wave: a 32 x 64 bf16 block of C on its way out
 constexpr int kLoaders = 4;                            // group 0 issues the global loads
 constexpr int kLoads = (kBM + kBN) / 8 / kLoaders;     // 16 wave-instructions per stage per loading wave
 constexpr int kGroupM = 4;
@@ -45,6 +51,35 @@ constexpr int kBufferFlags = 0x00020000;               // raw buffer descriptor 
 constexpr int kOOB = (int)0x80000000;                  // an offset past any descriptor's range: reads zeros
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+// Raw buffer descriptor (stride 0) over [base, base + bytes): offsets at or past `bytes` read as zero.
+__device__ __forceinline__ v4i buffer_rsrc(const void *base, int bytes) {
+  const uint64_t a = (uint64_t)base;
+  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff)),
+             __builtin_amdgcn_readfirstlane(bytes), kBufferFlags};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const GPIC_LDS void *)p;
+}
+
+// LDS DMA: lane j loads 16 bytes at buffer offset voffset + soffset (range-checked on voffset) and the wave writes
+// them to LDS [lds, lds + 1 KiB) in lane order. Written as asm so the compiler does not count it as an LDS store it
+// has to order against later LDS reads: it would otherwise wait for every load in flight before reading the other
+// stage. The waits these loads need are explicit at their uses (s_waitcnt vmcnt then a barrier).
+__device__ __forceinline__ void lds_dma16(v4i rsrc, int voffset, int soffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds)
+               : "memory", "m0");
+}
+
+// A uniform value the compiler must recompute where it is used: keeps it from hoisting the 16 per-load row offsets
+// out of the K loop as 16 live VGPRs (one v_add beside each load is free; the registers are not).
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
 
 // Logical tile id for workgroup `bid` out of G: XCD x (= bid % 8) gets the contiguous range of ids
 // [start_x, start_x + count_x).
@@ -60,6 +95,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
                                                             int64_t ldc, float *__restrict__ P, int M, int N, int K,
                                                             int ksplit, int tiles_m, int tiles_n, int splits) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t cstage[kThreads / 64 * kCStageBytes];
   // Declaring an AGPR clobber makes the compiler select the MFMA form that keeps accumulators in AGPRs.
   asm volatile("" ::: "a0");
 
@@ -85,10 +121,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 
   // ---- buffer descriptors over this tile's rows of A and B (rows past M / N read as zero)
   const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBN);
-  const __amdgpu_buffer_rsrc_t rA =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(A + (int64_t)m0 * lda), 0, rows_a * lda, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rB =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(B + (int64_t)n0 * ldb), 0, rows_b * ldb, kBufferFlags);
+  const v4i rA = buffer_rsrc(A + (int64_t)m0 * lda, rows_a * lda);
+  const v4i rB = buffer_rsrc(B + (int64_t)n0 * ldb, rows_b * ldb);
 
   // ---- loads (group 0). Wave instruction i fills stacked rows [R0, R0 + 8) of [A tile; B tile],
   // R0 = (i * 4 + wave) * 8; lane j writes slot j & 7 of row R0 + j / 8, i.e. K chunk (j & 7) ^ swz(row). swz(row)
@@ -98,15 +132,14 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int kchunk = 16 * ((lane & 7) ^ swz(lrow));
   const int baseA = lrow * lda + kchunk, baseB = lrow * ldb + kchunk;
   auto issue = [&](int stage, int k0) {
-    GPIC_LDS uint8_t *sbase = (GPIC_LDS uint8_t *)smem + stage * kStageBytes;
+    const uint32_t sbase = lds_addr(smem) + stage * kStageBytes;
     if (k0 + kBK <= kend) {
 #pragma unroll
       for (int i = 0; i < kLoads; i++) {
         const int R0 = (i * kLoaders + (wave & 3)) * 8;
         const bool isA = i < kLoads / 2;
-        const int vo = isA ? baseA + i * 32 * lda : baseB + (i - kLoads / 2) * 32 * ldb;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, (GPIC_LDS void *)(sbase + R0 * kBK), 16, vo, k0, 0,
-                                                 0);
+        const int vo = (isA ? baseA : baseB) + opaque(isA ? i * 32 * lda : (i - kLoads / 2) * 32 * ldb);
+        lds_dma16(isA ? rA : rB, vo, k0, sbase + R0 * kBK);
       }
     } else {  // the last, partial K tile: chunks at or past kend read zeros
       const bool kin = k0 + kchunk < kend;
@@ -114,9 +147,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       for (int i = 0; i < kLoads; i++) {
         const int R0 = (i * kLoaders + (wave & 3)) * 8;
         const bool isA = i < kLoads / 2;
-        const int vo = (isA ? baseA + i * 32 * lda : baseB + (i - kLoads / 2) * 32 * ldb) + k0;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, (GPIC_LDS void *)(sbase + R0 * kBK), 16,
-                                                 kin ? vo : kOOB, 0, 0, 0);
+        const int vo = (isA ? baseA : baseB) + opaque(isA ? i * 32 * lda : (i - kLoads / 2) * 32 * ldb) + k0;
+        lds_dma16(isA ? rA : rB, kin ? vo : kOOB, 0, sbase + R0 * kBK);
       }
     }
   };
@@ -177,7 +209,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     read(st);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stage before anyone overwrites it
     phase_barrier();
-    // MFMA phase
 #pragma unroll
     for (int step = 0; step < 2; step++)
 #pragma unroll
@@ -194,34 +225,66 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // ---- epilogue: acc[ni][mi] lane l holds D[n][m] for m = mi * 32 + (l & 31) and
   // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns
   const float s = sa[0] * sb[0];
+  if (P) {   // split-K fp32 partials: 16-byte stores straight from the accumulators
 #pragma unroll
-  for (int ni = 0; ni < kTN; ni++) {
+    for (int ni = 0; ni < kTN; ni++)
 #pragma unroll
-    for (int mi = 0; mi < kTM; mi++) {
-      const int m = m0 + wm * kWTM + mi * 32 + (lane & 31);
-      if (m >= M) continue;
+      for (int mi = 0; mi < kTM; mi++) {
+        const int m = m0 + wm * kWTM + mi * 32 + (lane & 31);
+        if (m >= M) continue;
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (lane >> 5);
-        if (n >= N) continue;
-        const v16f &v = acc[ni][mi];
-        if (P) {
+        for (int q = 0; q < 4; q++) {
+          const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (lane >> 5);
+          if (n >= N) continue;
+          const v16f &v = acc[ni][mi];
           *reinterpret_cast<v4f *>(P + ((int64_t)split * M + m) * N + n) =
               v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        } else {
-          uint32_t h[4];
-#pragma unroll
-          for (int j = 0; j < 4; j++) h[j] = bf16_rne(v[4 * q + j] * s);
-          if (bias) {
-            const u32x2 bw = *reinterpret_cast<const u32x2 *>(bias + n);
-            h[0] = bf16_rne(bf16_lo(h[0]) + bf16_lo(bw.x));
-            h[1] = bf16_rne(bf16_lo(h[1]) + bf16_hi(bw.x));
-            h[2] = bf16_rne(bf16_lo(h[2]) + bf16_lo(bw.y));
-            h[3] = bf16_rne(bf16_lo(h[3]) + bf16_hi(bw.y));
-          }
-          *reinterpret_cast<u32x2 *>(C + (int64_t)m * ldc + n) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
         }
       }
+    return;
+  }
+  // bf16 output through this wave's private 4 KiB of LDS: a 32 x 64 block of C (two ni tiles, 128 bytes a row) is
+  // written in the accumulator layout, then read back as 8 whole rows per instruction, so each global store
+  // instruction writes 8 complete 128-byte lines (the accumulator layout would give 32 rows x 16 bytes).
+  // Row r's 16-byte chunk c sits in slot c ^ swz(r). Only this wave touches the block: no workgroup barrier.
+  GPIC_LDS uint8_t *cst = (GPIC_LDS uint8_t *)cstage + wave * kCStageBytes;
+  const int wr = lane & 31, wh = 8 * (lane >> 5);
+  const int rr = lane >> 3, rc = lane & 7;
+#pragma unroll
+  for (int mi = 0; mi < kTM; mi++) {
+#pragma unroll
+    for (int pair = 0; pair < kTN / 2; pair++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int ni = 2 * pair + h;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const v16f &v = acc[ni][mi];
+          uint32_t o[4];
+#pragma unroll
+          for (int j = 0; j < 4; j++) o[j] = bf16_rne(v[4 * q + j] * s);
+          if (bias) {
+            const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (lane >> 5);
+            const u32x2 bw = n < N ? *reinterpret_cast<const u32x2 *>(bias + n) : u32x2{0, 0};
+            o[0] = bf16_rne(bf16_lo(o[0]) + bf16_lo(bw.x));
+            o[1] = bf16_rne(bf16_lo(o[1]) + bf16_hi(bw.x));
+            o[2] = bf16_rne(bf16_lo(o[2]) + bf16_lo(bw.y));
+            o[3] = bf16_rne(bf16_lo(o[3]) + bf16_hi(bw.y));
+          }
+          *(GPIC_LDS st8_t *)(cst + wr * 128 + 16 * ((4 * h + q) ^ swz(wr)) + wh) =
+              st8_t{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int r = 8 * j + rr;
+        const st16_t w = *(const GPIC_LDS st16_t *)(cst + r * 128 + 16 * (rc ^ swz(r)));
+        const int m = m0 + wm * kWTM + mi * 32 + r;
+        const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
+        if (m < M && n < N) *reinterpret_cast<st16_t *>(C + (int64_t)m * ldc + n) = w;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
     }
   }
 }
