@@ -30,9 +30,9 @@ namespace gpic {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
-// The C staging block is written 8 bytes and read 16 bytes at a time: types that may alias each other, or
-// type-based alias analysis would treat the reads as independent of the writes.
-typedef uint32_t st8_t __attribute__((ext_vector_type(2), __may_alias__));
+// Types for the C staging block in LDS and the bf16 stores: may_alias, since LDS holding fragments of A and B as
+// one type is reused for C as another, and type-based alias analysis must not separate the two.
+typedef float f4a_t __attribute__((ext_vector_type(4), __may_alias__));
 typedef uint32_t st16_t __attribute__((ext_vector_type(4), __may_alias__));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -43,7 +43,8 @@ constexpr int kThreads = 512;                          // 8 waves: 2 groups x 4
 constexpr int kWTM = 64, kWTN = 128;                   // wave tile
 constexpr int kTM = kWTM / 32, kTN = kWTN / 32;        // 32 x 32 MFMA tiles per wave: 2 x 4
 constexpr int kStageBytes = (kBM + kBN) * kBK;         // 64 KiB
-constexpr int kCStageBytes = 32 * 128;                 // per wave: a 32 x 64 bf16 block of C on its way out
+constexpr int kCStageBytes = 32 * 256;                 // per wave: a 32 x 64 fp32 block of C on its way out
+static_assert(kThreads / 64 * kCStageBytes <= kStageBytes, "the C blocks of all waves fit in one stage");
 constexpr int kLoaders = 4;                            // group 0 issues the global loads
 constexpr int kLoads = (kBM + kBN) / 8 / kLoaders;     // 16 wave-instructions per stage per loading wave
 constexpr int kGroupM = 4;
@@ -75,9 +76,16 @@ __device__ __forceinline__ void lds_dma16(v4i rsrc, int voffset, int soffset, ui
 }
 
 // A uniform value the compiler must recompute where it is used: keeps it from hoisting the 16 per-load row offsets
-// out of the K loop as 16 live VGPRs (one v_add beside each load is free; the registers are not).
+// out of the K loop as 16 live registers (a scalar multiply and a v_add beside each load are free; registers are not).
 __device__ __forceinline__ int opaque(int v) {
   asm volatile("" : "+s"(v));
+  return v;
+}
+
+// The same for a per-lane value: the epilogue derives its addresses from an opaque copy of the lane index, so they
+// are computed in the epilogue instead of being hoisted out of the tile loop and spilled across it.
+__device__ __forceinline__ int opaque_v(int v) {
+  asm volatile("" : "+v"(v));
   return v;
 }
 
@@ -88,6 +96,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
+template <bool kTail>
 __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
                                                             const uint8_t *__restrict__ B, int ldb,
                                                             const float *__restrict__ sa, const float *__restrict__ sb,
@@ -95,7 +104,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
                                                             int64_t ldc, float *__restrict__ P, int M, int N, int K,
                                                             int ksplit, int tiles_m, int tiles_n, int splits) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t cstage[kThreads / 64 * kCStageBytes];
   // Declaring an AGPR clobber makes the compiler select the MFMA form that keeps accumulators in AGPRs.
   asm volatile("" ::: "a0");
 
@@ -104,26 +112,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int group = wave >> 2;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- which tile / split this workgroup owns
-  const int tiles = tiles_m * tiles_n;
-  const int lid = xcd_remap(blockIdx.x, tiles * splits);
-  const int split = lid / tiles;
-  const int tile = lid % tiles;
-  const int per_group = kGroupM * tiles_n;
-  const int first_m = (tile / per_group) * kGroupM;
-  const int gsz = min(tiles_m - first_m, kGroupM);
-  const int tm = first_m + (tile % per_group) % gsz;
-  const int tn = (tile % per_group) / gsz;
-  const int m0 = tm * kBM, n0 = tn * kBN;
-  const int kbeg = split * ksplit;
-  const int kend = min(K, kbeg + ksplit);
-  const int nk = (kend - kbeg + kBK - 1) / kBK;
-
-  // ---- buffer descriptors over this tile's rows of A and B (rows past M / N read as zero)
-  const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBN);
-  const v4i rA = buffer_rsrc(A + (int64_t)m0 * lda, rows_a * lda);
-  const v4i rB = buffer_rsrc(B + (int64_t)n0 * ldb, rows_b * ldb);
-
   // ---- loads (group 0). Wave instruction i fills stacked rows [R0, R0 + 8) of [A tile; B tile],
   // R0 = (i * 4 + wave) * 8; lane j writes slot j & 7 of row R0 + j / 8, i.e. K chunk (j & 7) ^ swz(row). swz(row)
   // does not depend on i, so every instruction's offset is a per-lane base plus i * 32 rows. Row offsets stay in
@@ -131,162 +119,206 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int lrow = (wave & 3) * 8 + (lane >> 3);
   const int kchunk = 16 * ((lane & 7) ^ swz(lrow));
   const int baseA = lrow * lda + kchunk, baseB = lrow * ldb + kchunk;
-  auto issue = [&](int stage, int k0) {
-    const uint32_t sbase = lds_addr(smem) + stage * kStageBytes;
-    if (k0 + kBK <= kend) {
-#pragma unroll
-      for (int i = 0; i < kLoads; i++) {
-        const int R0 = (i * kLoaders + (wave & 3)) * 8;
-        const bool isA = i < kLoads / 2;
-        const int vo = (isA ? baseA : baseB) + opaque(isA ? i * 32 * lda : (i - kLoads / 2) * 32 * ldb);
-        lds_dma16(isA ? rA : rB, vo, k0, sbase + R0 * kBK);
-      }
-    } else {  // the last, partial K tile: chunks at or past kend read zeros
-      const bool kin = k0 + kchunk < kend;
-#pragma unroll
-      for (int i = 0; i < kLoads; i++) {
-        const int R0 = (i * kLoaders + (wave & 3)) * 8;
-        const bool isA = i < kLoads / 2;
-        const int vo = (isA ? baseA : baseB) + opaque(isA ? i * 32 * lda : (i - kLoads / 2) * 32 * ldb) + k0;
-        lds_dma16(isA ? rA : rB, kin ? vo : kOOB, 0, sbase + R0 * kBK);
-      }
-    }
-  };
+  const float s = sa[0] * sb[0];
 
-  // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5)
-  v8i fa[2][kTM], fb[2][kTN];
-  const int frow = lane & 31;
-  const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
-  const int c0 = 2 * (lane >> 5);
-  auto read = [&](int stage) {
-    const GPIC_LDS uint8_t *sA = (const GPIC_LDS uint8_t *)smem + stage * kStageBytes;
-    const GPIC_LDS uint8_t *sB = sA + kBM * kBK;
+  // ---- persistent: work item `it` (a tile and a K split) goes to workgroup it % gridDim.x. The grid is a multiple
+  // of 8 (or covers every item in one pass), so it & 7 is the XCD the workgroup runs on and xcd_remap gives each
+  // XCD a contiguous range of tiles. A workgroup's stores of one tile drain while it loads and multiplies the next.
+  const int tiles = tiles_m * tiles_n;
+  const int work = tiles * splits;
+  for (int it = blockIdx.x; it < work; it += gridDim.x) {
+    const int lid = xcd_remap(it, work);
+    const int split = lid / tiles;
+    const int tile = lid % tiles;
+    const int per_group = kGroupM * tiles_n;
+    const int first_m = (tile / per_group) * kGroupM;
+    const int gsz = min(tiles_m - first_m, kGroupM);
+    const int tm = first_m + (tile % per_group) % gsz;
+    const int tn = (tile % per_group) / gsz;
+    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int kbeg = split * ksplit;
+    const int kend = min(K, kbeg + ksplit);
+    const int nk = (kend - kbeg + kBK - 1) / kBK;
+
+    // ---- buffer descriptors over this tile's rows of A and B (rows past M / N read as zero)
+    const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBN);
+    const v4i rA = buffer_rsrc(A + (int64_t)m0 * lda, rows_a * lda);
+    const v4i rB = buffer_rsrc(B + (int64_t)n0 * ldb, rows_b * ldb);
+
+    auto issue = [&](int stage, int k0) {
+      const uint32_t sbase = lds_addr(smem) + stage * kStageBytes;
+      // 32 rows of A / B; opaque, so each load's offset is one scalar multiply here rather than a register held
+      // across the loop for each of the 16 loads
+      const int a32 = opaque(32 * lda), b32 = opaque(32 * ldb);
+      if (!kTail || k0 + kBK <= kend) {
 #pragma unroll
-    for (int step = 0; step < 2; step++) {
-      const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
+        for (int i = 0; i < kLoads; i++) {
+          const int R0 = (i * kLoaders + (wave & 3)) * 8;
+          const bool isA = i < kLoads / 2;
+          const int vo = isA ? baseA + i * a32 : baseB + (i - kLoads / 2) * b32;
+          lds_dma16(isA ? rA : rB, vo, k0, sbase + R0 * kBK);
+        }
+      } else {  // the last, partial K tile: chunks at or past kend read zeros
+        const bool kin = k0 + kchunk < kend;
 #pragma unroll
-      for (int t = 0; t < kTM; t++) {
-        const GPIC_LDS uint8_t *pa = sA + (wm * kWTM + t * 32 + frow) * kBK;
-        const u32x4 a0 = *(const GPIC_LDS u32x4 *)(pa + lo), a1 = *(const GPIC_LDS u32x4 *)(pa + hi);
-        fa[step][t] = v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        for (int i = 0; i < kLoads; i++) {
+          const int R0 = (i * kLoaders + (wave & 3)) * 8;
+          const bool isA = i < kLoads / 2;
+          const int vo = (isA ? baseA + i * a32 : baseB + (i - kLoads / 2) * b32) + k0;
+          lds_dma16(isA ? rA : rB, kin ? vo : kOOB, 0, sbase + R0 * kBK);
+        }
       }
+    };
+
+    // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5)
+    v8i fa[2][kTM], fb[2][kTN];
+    const int frow = lane & 31;
+    const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
+    const int c0 = 2 * (lane >> 5);
+    auto read = [&](int stage) {
+      const GPIC_LDS uint8_t *sA = (const GPIC_LDS uint8_t *)smem + stage * kStageBytes;
+      const GPIC_LDS uint8_t *sB = sA + kBM * kBK;
 #pragma unroll
-      for (int t = 0; t < kTN; t++) {
-        const GPIC_LDS uint8_t *pb = sB + (wn * kWTN + t * 32 + frow) * kBK;
-        const u32x4 b0 = *(const GPIC_LDS u32x4 *)(pb + lo), b1 = *(const GPIC_LDS u32x4 *)(pb + hi);
-        fb[step][t] = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+      for (int step = 0; step < 2; step++) {
+        const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
+#pragma unroll
+        for (int t = 0; t < kTM; t++) {
+          const GPIC_LDS uint8_t *pa = sA + (wm * kWTM + t * 32 + frow) * kBK;
+          const u32x4 a0 = *(const GPIC_LDS u32x4 *)(pa + lo), a1 = *(const GPIC_LDS u32x4 *)(pa + hi);
+          fa[step][t] = v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        }
+#pragma unroll
+        for (int t = 0; t < kTN; t++) {
+          const GPIC_LDS uint8_t *pb = sB + (wn * kWTN + t * 32 + frow) * kBK;
+          const u32x4 b0 = *(const GPIC_LDS u32x4 *)(pb + lo), b1 = *(const GPIC_LDS u32x4 *)(pb + hi);
+          fb[step][t] = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        }
       }
-    }
-  };
+    };
 
-  v16f acc[kTN][kTM];
+    v16f acc[kTN][kTM];
 #pragma unroll
-  for (int i = 0; i < kTN; i++)
+    for (int i = 0; i < kTN; i++)
 #pragma unroll
-    for (int j = 0; j < kTM; j++) acc[i][j] = v16f{};
+      for (int j = 0; j < kTM; j++) acc[i][j] = v16f{};
 
-  // Phase boundary: a bare s_barrier (no fence: the waits each side needs are explicit, so the loads group 0 issued
-  // in its memory phase stay in flight through it), pinned with sched_barrier so the compiler cannot move MFMAs
-  // (register-only instructions) across it into the other group's phase.
-  auto phase_barrier = [&]() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
+    // Phase boundary: a bare s_barrier (no fence: the waits each side needs are explicit, so the loads group 0 issued
+    // in its memory phase stay in flight through it), pinned with sched_barrier so the compiler cannot move MFMAs
+    // (register-only instructions) across it into the other group's phase.
+    auto phase_barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
 
-  // Prologue: group 0 sends tile 0; every wave waits for its own loads, then all meet, so tile 0 is complete in LDS
-  // before anyone reads it. Group 1 then passes one extra barrier to run one phase behind group 0.
-  if (group == 0 && nk > 0) issue(0, kbeg);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  phase_barrier();
-  if (group == 1) phase_barrier();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
-    // memory phase: send tile kt + 1 (group 0), read this wave's fragments of tile kt
-    if (group == 0 && kt + 1 < nk) issue(st ^ 1, kbeg + (kt + 1) * kBK);
-    read(st);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stage before anyone overwrites it
+    // Prologue: group 0 sends K tile 0 and waits for it, then all meet, so it is complete in LDS before anyone reads
+    // it (the previous work item's last barrier ended every read of both stages). Group 1 then passes one extra
+    // barrier to run one phase behind group 0. Group 1 issues no loads, so its stores of the previous tile drain
+    // without anyone waiting for them.
+    if (group == 0 && nk > 0) issue(0, kbeg);
+    if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     phase_barrier();
+    if (group == 1) phase_barrier();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int st = kt & 1;
+      // memory phase: send tile kt + 1 (group 0), read this wave's fragments of tile kt
+      if (group == 0 && kt + 1 < nk) issue(st ^ 1, kbeg + (kt + 1) * kBK);
+      read(st);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stage before anyone overwrites it
+      phase_barrier();
 #pragma unroll
-    for (int step = 0; step < 2; step++)
+      for (int step = 0; step < 2; step++)
+#pragma unroll
+        for (int ni = 0; ni < kTN; ni++)
+#pragma unroll
+          for (int mi = 0; mi < kTM; mi++)
+            acc[ni][mi] =
+                __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[step][ni], fa[step][mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
+      if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kt + 1 has landed in LDS
+      phase_barrier();
+    }
+    if (group == 0) phase_barrier();
+
+    // ---- epilogue: acc[ni][mi] lane l holds D[n][m] for m = mi * 32 + (l & 31) and
+    // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns
+    const int el = opaque_v(lane);
+    if (P) {   // split-K fp32 partials: 16-byte stores straight from the accumulators
 #pragma unroll
       for (int ni = 0; ni < kTN; ni++)
 #pragma unroll
-        for (int mi = 0; mi < kTM; mi++)
-          acc[ni][mi] =
-              __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[step][ni], fa[step][mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
-    if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kt + 1 has landed in LDS
-    phase_barrier();
-  }
-  if (group == 0) phase_barrier();
-
-  // ---- epilogue: acc[ni][mi] lane l holds D[n][m] for m = mi * 32 + (l & 31) and
-  // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns
-  const float s = sa[0] * sb[0];
-  if (P) {   // split-K fp32 partials: 16-byte stores straight from the accumulators
+        for (int mi = 0; mi < kTM; mi++) {
+          const int m = m0 + wm * kWTM + mi * 32 + (el & 31);
+          if (m >= M) continue;
 #pragma unroll
-    for (int ni = 0; ni < kTN; ni++)
-#pragma unroll
-      for (int mi = 0; mi < kTM; mi++) {
-        const int m = m0 + wm * kWTM + mi * 32 + (lane & 31);
-        if (m >= M) continue;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (lane >> 5);
-          if (n >= N) continue;
-          const v16f &v = acc[ni][mi];
-          *reinterpret_cast<v4f *>(P + ((int64_t)split * M + m) * N + n) =
-              v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        }
-      }
-    return;
-  }
-  // bf16 output through this wave's private 4 KiB of LDS: a 32 x 64 block of C (two ni tiles, 128 bytes a row) is
-  // written in the accumulator layout, then read back as 8 whole rows per instruction, so each global store
-  // instruction writes 8 complete 128-byte lines (the accumulator layout would give 32 rows x 16 bytes).
-  // Row r's 16-byte chunk c sits in slot c ^ swz(r). Only this wave touches the block: no workgroup barrier.
-  GPIC_LDS uint8_t *cst = (GPIC_LDS uint8_t *)cstage + wave * kCStageBytes;
-  const int wr = lane & 31, wh = 8 * (lane >> 5);
-  const int rr = lane >> 3, rc = lane & 7;
-#pragma unroll
-  for (int mi = 0; mi < kTM; mi++) {
-#pragma unroll
-    for (int pair = 0; pair < kTN / 2; pair++) {
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int ni = 2 * pair + h;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const v16f &v = acc[ni][mi];
-          uint32_t o[4];
-#pragma unroll
-          for (int j = 0; j < 4; j++) o[j] = bf16_rne(v[4 * q + j] * s);
-          if (bias) {
-            const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (lane >> 5);
-            const u32x2 bw = n < N ? *reinterpret_cast<const u32x2 *>(bias + n) : u32x2{0, 0};
-            o[0] = bf16_rne(bf16_lo(o[0]) + bf16_lo(bw.x));
-            o[1] = bf16_rne(bf16_lo(o[1]) + bf16_hi(bw.x));
-            o[2] = bf16_rne(bf16_lo(o[2]) + bf16_lo(bw.y));
-            o[3] = bf16_rne(bf16_lo(o[3]) + bf16_hi(bw.y));
+          for (int q = 0; q < 4; q++) {
+            const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (el >> 5);
+            if (n >= N) continue;
+            const v16f &v = acc[ni][mi];
+            *reinterpret_cast<v4f *>(P + ((int64_t)split * M + m) * N + n) =
+                v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
           }
-          *(GPIC_LDS st8_t *)(cst + wr * 128 + 16 * ((4 * h + q) ^ swz(wr)) + wh) =
-              st8_t{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        }
+      continue;
+    }
+    // bf16 output through LDS. The accumulators go to LDS as fp32 straight from AGPRs (VALU work on them would need
+    // VGPR copies of all 128), one 32 x 64 block (two ni tiles) at a time; each lane then reads back 8 consecutive
+    // columns of one row, scales, rounds, adds the bias and stores 16 bytes, 8 lanes to a 128-byte line of C.
+    // A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free both ways).
+    // Each wave uses its own 8 KiB of stage 1: nothing else touches stage 1 between this work item's last barrier
+    // and the next one's first barrier, and group 0 sends a K tile there only after that barrier, which group 1
+    // reaches only when its epilogue is done.
+    GPIC_LDS uint8_t *cst = (GPIC_LDS uint8_t *)smem + kStageBytes + wave * kCStageBytes;
+    const int wr = el & 31, wh = el >> 5;
+    const int rr = el >> 3, rc = el & 7;
+    u32x2 bw[kTN / 2][2] = {};
+    if (bias) {
+#pragma unroll
+      for (int pair = 0; pair < kTN / 2; pair++) {
+        const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
+        if (n < N) {
+          bw[pair][0] = *reinterpret_cast<const u32x2 *>(bias + n);
+          bw[pair][1] = *reinterpret_cast<const u32x2 *>(bias + n + 4);
         }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int r = 8 * j + rr;
-        const st16_t w = *(const GPIC_LDS st16_t *)(cst + r * 128 + 16 * (rc ^ swz(r)));
-        const int m = m0 + wm * kWTM + mi * 32 + r;
-        const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
-        if (m < M && n < N) *reinterpret_cast<st16_t *>(C + (int64_t)m * ldc + n) = w;
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
     }
-  }
+#pragma unroll
+    for (int mi = 0; mi < kTM; mi++) {
+#pragma unroll
+      for (int pair = 0; pair < kTN / 2; pair++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const v16f &v = acc[2 * pair + h][mi];
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            *(GPIC_LDS f4a_t *)(cst + wr * 256 + 16 * ((8 * h + 2 * q + wh) ^ (wr & 15))) =
+                f4a_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int r = 8 * j + rr;
+          const f4a_t x0 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc) ^ (r & 15)));
+          const f4a_t x1 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc + 1) ^ (r & 15)));
+          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          st16_t w;
+#pragma unroll
+          for (int e = 0; e < 4; e++) w[e] = bf16_rne(x[2 * e] * s) | (bf16_rne(x[2 * e + 1] * s) << 16);
+          if (bias) {   // bf16(bf16(acc * s) + bias): the output is rounded, then the bias add is rounded again
+            const uint32_t b[4] = {bw[pair][0].x, bw[pair][0].y, bw[pair][1].x, bw[pair][1].y};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              w[e] = bf16_rne(bf16_lo(w[e]) + bf16_lo(b[e])) | (bf16_rne(bf16_hi(w[e]) + bf16_hi(b[e])) << 16);
+          }
+          const int m = m0 + wm * kWTM + mi * 32 + r;
+          const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
+          if (m < M && n < N) *reinterpret_cast<st16_t *>(C + (int64_t)m * ldc + n) = w;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
+      }
+    }
+  }  // work items
 }
 
 // Sum of the split-K partials in split order, then the same epilogue as the single-pass kernel.
@@ -379,8 +411,13 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
     if (!aligned16(ws)) return GPIC_EALIGN;
     P = static_cast<float *>(ws);
   }
-  const int grid = p.tiles_m * p.tiles_n * p.splits;
-  gemm_tn_kernel<<<grid, kThreads, 0, st>>>(
+  // One workgroup per CU at most (160 KiB of LDS each); a persistent grid is a multiple of 8, one per XCD.
+  const int work = p.tiles_m * p.tiles_n * p.splits;
+  const int slots = num_cus() & ~7;
+  const int grid = work <= slots || slots < 8 ? work : slots;
+  // the partial-K-tile load path is compiled only into the instance that needs it
+  auto *kernel = K % kBK ? gemm_tn_kernel<true> : gemm_tn_kernel<false>;
+  kernel<<<grid, kThreads, 0, st>>>(
       A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
       p.splits);
   if (P) {
