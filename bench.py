@@ -54,6 +54,8 @@ def parse():
     p.add_argument("--no-compare", action="store_true")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB buffer (the known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--traffic", action="store_true",
+                   help="only run each of the 12 GEMM shapes once, in the printed order (one counter row per shape)")
     return p.parse_args()
 
 
@@ -194,6 +196,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4, "launches": 3}), flush=True)
+        return
+
+    if args.traffic:
+        shapes = gemm_shapes()
+        ops = gemm_operands(G, dev, shapes)
+        for aq, sa, bq, sb in ops:
+            G.fp8_gemm(aq, sa, bq, sb, None, False)
+            torch.cuda.synchronize()
+        print(json.dumps({"gemm_order": [name for name, *_ in shapes]}), flush=True)
         return
 
     # ---- the step: the whole FP8 linear path of a d12 block, fwd + bwd

@@ -426,7 +426,7 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
       unpack8(z2v, z2);
       unpack8(dav, dv);
       sigmoid8(lut, z1v, z1, sg);
-      uint32_t h1[8], h2[8];
+      float d1[8], d2[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const float sl = bf16_round(z1[i] * sg[i]);
@@ -435,15 +435,19 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
         const float t3 = 1.0f + t2;
         const float g = sg[i] * t3;
         const float pr = dv[i] * z2[i];
-        h1[i] = bf16_rne(pr * g);
-        h2[i] = bf16_rne(dv[i] * sl);
-        m = max(m, absbits_nonan(__uint_as_float(h1[i] << 16)));
-        m = max(m, absbits_nonan(__uint_as_float(h2[i] << 16)));
+        d1[i] = pr * g;
+        d2[i] = dv[i] * sl;
       }
-      *reinterpret_cast<u32x4 *>(dz + r * sdz + 8 * u) =
-          u32x4{h1[0] | (h1[1] << 16), h1[2] | (h1[3] << 16), h1[4] | (h1[5] << 16), h1[6] | (h1[7] << 16)};
-      *reinterpret_cast<u32x4 *>(dz + r * sdz + H + 8 * u) =
-          u32x4{h2[0] | (h2[1] << 16), h2[2] | (h2[3] << 16), h2[4] | (h2[5] << 16), h2[6] | (h2[7] << 16)};
+      u32x4 h1, h2;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        h1[j] = pack_bf16(d1[2 * j], d1[2 * j + 1]);
+        h2[j] = pack_bf16(d2[2 * j], d2[2 * j + 1]);
+        m = max(m, max(absbits_nonan(bf16_lo(h1[j])), absbits_nonan(bf16_hi(h1[j]))));
+        m = max(m, max(absbits_nonan(bf16_lo(h2[j])), absbits_nonan(bf16_hi(h2[j]))));
+      }
+      *reinterpret_cast<u32x4 *>(dz + r * sdz + 8 * u) = h1;
+      *reinterpret_cast<u32x4 *>(dz + r * sdz + H + 8 * u) = h2;
     }
   }
   m = block_max_u32(m);

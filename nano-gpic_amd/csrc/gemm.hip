@@ -304,12 +304,12 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
           const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
           st16_t w;
 #pragma unroll
-          for (int e = 0; e < 4; e++) w[e] = bf16_rne(x[2 * e] * s) | (bf16_rne(x[2 * e + 1] * s) << 16);
+          for (int e = 0; e < 4; e++) w[e] = pack_bf16(x[2 * e] * s, x[2 * e + 1] * s);
           if (bias) {   // bf16(bf16(acc * s) + bias): the output is rounded, then the bias add is rounded again
             const uint32_t b[4] = {bw[pair][0].x, bw[pair][0].y, bw[pair][1].x, bw[pair][1].y};
 #pragma unroll
             for (int e = 0; e < 4; e++)
-              w[e] = bf16_rne(bf16_lo(w[e]) + bf16_lo(b[e])) | (bf16_rne(bf16_hi(w[e]) + bf16_hi(b[e])) << 16);
+              w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
           }
           const int m = m0 + wm * kWTM + mi * 32 + r;
           const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
@@ -333,17 +333,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
     const int n = (int)(i % (N / 4)) * 4;
     v4f sum = *reinterpret_cast<const v4f *>(P + m * N + n);
     for (int z = 1; z < splits; z++) sum += *reinterpret_cast<const v4f *>(P + ((int64_t)z * M + m) * N + n);
-    uint32_t h[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) h[j] = bf16_rne(sum[j] * s);
-    if (bias) {
+    u32x2 w{pack_bf16(sum[0] * s, sum[1] * s), pack_bf16(sum[2] * s, sum[3] * s)};
+    if (bias) {   // the output is rounded, then the bias add is rounded again
       const u32x2 bw = *reinterpret_cast<const u32x2 *>(bias + n);
-      h[0] = bf16_rne(bf16_lo(h[0]) + bf16_lo(bw.x));
-      h[1] = bf16_rne(bf16_lo(h[1]) + bf16_hi(bw.x));
-      h[2] = bf16_rne(bf16_lo(h[2]) + bf16_lo(bw.y));
-      h[3] = bf16_rne(bf16_lo(h[3]) + bf16_hi(bw.y));
+      w.x = pack_bf16(bf16_lo(w.x) + bf16_lo(bw.x), bf16_hi(w.x) + bf16_hi(bw.x));
+      w.y = pack_bf16(bf16_lo(w.y) + bf16_lo(bw.y), bf16_hi(w.y) + bf16_hi(bw.y));
     }
-    *reinterpret_cast<u32x2 *>(C + m * ldc + n) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    *reinterpret_cast<u32x2 *>(C + m * ldc + n) = w;
   }
 }
 
