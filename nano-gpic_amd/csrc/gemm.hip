@@ -145,20 +145,21 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const v4i rA = buffer_rsrc(A + (int64_t)m0 * lda, rows_a * lda);
     const v4i rB = buffer_rsrc(B + (int64_t)n0 * ldb, rows_b * ldb);
 
+    // Load i of the 16 this wave issues for a whole K tile at k0 into `stage`. The stride of 32 rows is opaque, so
+    // each load's offset is a scalar multiply here rather than a register held across the loop for each load.
+    auto load_full = [&](int stage, int k0, int i) {
+      const int R0 = (i * kLoaders + (wave & 3)) * 8;
+      const bool isA = i < kLoads / 2;
+      const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + (i - kLoads / 2) * opaque(32 * ldb);
+      lds_dma16(isA ? rA : rB, vo, k0, lds_addr(smem) + stage * kStageBytes + R0 * kBK);
+    };
     auto issue = [&](int stage, int k0) {
-      const uint32_t sbase = lds_addr(smem) + stage * kStageBytes;
-      // 32 rows of A / B; opaque, so each load's offset is one scalar multiply here rather than a register held
-      // across the loop for each of the 16 loads
-      const int a32 = opaque(32 * lda), b32 = opaque(32 * ldb);
       if (!kTail || k0 + kBK <= kend) {
 #pragma unroll
-        for (int i = 0; i < kLoads; i++) {
-          const int R0 = (i * kLoaders + (wave & 3)) * 8;
-          const bool isA = i < kLoads / 2;
-          const int vo = isA ? baseA + i * a32 : baseB + (i - kLoads / 2) * b32;
-          lds_dma16(isA ? rA : rB, vo, k0, sbase + R0 * kBK);
-        }
+        for (int i = 0; i < kLoads; i++) load_full(stage, k0, i);
       } else {  // the last, partial K tile: chunks at or past kend read zeros
+        const uint32_t sbase = lds_addr(smem) + stage * kStageBytes;
+        const int a32 = opaque(32 * lda), b32 = opaque(32 * ldb);
         const bool kin = k0 + kchunk < kend;
 #pragma unroll
         for (int i = 0; i < kLoads; i++) {
@@ -170,29 +171,41 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       }
     };
 
-    // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5)
+    // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5).
+    // Fragment j = 6 * step + f: f < kTM is A fragment f, otherwise B fragment f - kTM; two ds_read_b128 each.
     v8i fa[2][kTM], fb[2][kTN];
     const int frow = lane & 31;
     const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
     const int c0 = 2 * (lane >> 5);
-    auto read = [&](int stage) {
+    auto read_frag = [&](int stage, int j) {
+      const int step = j / (kTM + kTN), f = j % (kTM + kTN);
+      const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
       const GPIC_LDS uint8_t *sA = (const GPIC_LDS uint8_t *)smem + stage * kStageBytes;
-      const GPIC_LDS uint8_t *sB = sA + kBM * kBK;
+      const GPIC_LDS uint8_t *p = f < kTM ? sA + (wm * kWTM + f * 32 + frow) * kBK
+                                          : sA + kBM * kBK + (wn * kWTN + (f - kTM) * 32 + frow) * kBK;
+      const u32x4 x0 = *(const GPIC_LDS u32x4 *)(p + lo), x1 = *(const GPIC_LDS u32x4 *)(p + hi);
+      const v8i v{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+      if (f < kTM) fa[step][f] = v;
+      else fb[step][f - kTM] = v;
+    };
+    auto read = [&](int stage) {
 #pragma unroll
-      for (int step = 0; step < 2; step++) {
-        const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
+      for (int j = 0; j < 2 * (kTM + kTN); j++) read_frag(stage, j);
+    };
+    // Group 0's memory phase with a whole next K tile: its 12 fragment reads interleaved with its 16 loads. A load
+    // issue waits while the texture unit's queue is full; with the reads between the loads, the LDS works through
+    // the reads during those waits instead of after the last load.
+    static_assert(2 * (kTM + kTN) == 12 && kLoads == 16, "interleave pattern: 3 fragments per 4 loads");
+    auto issue_and_read = [&](int rstage, int istage, int k0) {
 #pragma unroll
-        for (int t = 0; t < kTM; t++) {
-          const GPIC_LDS uint8_t *pa = sA + (wm * kWTM + t * 32 + frow) * kBK;
-          const u32x4 a0 = *(const GPIC_LDS u32x4 *)(pa + lo), a1 = *(const GPIC_LDS u32x4 *)(pa + hi);
-          fa[step][t] = v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        }
-#pragma unroll
-        for (int t = 0; t < kTN; t++) {
-          const GPIC_LDS uint8_t *pb = sB + (wn * kWTN + t * 32 + frow) * kBK;
-          const u32x4 b0 = *(const GPIC_LDS u32x4 *)(pb + lo), b1 = *(const GPIC_LDS u32x4 *)(pb + hi);
-          fb[step][t] = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        }
+      for (int j = 0; j < 4; j++) {
+        read_frag(rstage, 3 * j);
+        load_full(istage, k0, 4 * j);
+        read_frag(rstage, 3 * j + 1);
+        load_full(istage, k0, 4 * j + 1);
+        load_full(istage, k0, 4 * j + 2);
+        read_frag(rstage, 3 * j + 2);
+        load_full(istage, k0, 4 * j + 3);
       }
     };
 
@@ -224,8 +237,13 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     for (int kt = 0; kt < nk; ++kt) {
       const int st = kt & 1;
       // memory phase: send tile kt + 1 (group 0), read this wave's fragments of tile kt
-      if (group == 0 && kt + 1 < nk) issue(st ^ 1, kbeg + (kt + 1) * kBK);
-      read(st);
+      const int k1 = kbeg + (kt + 1) * kBK;
+      if (group == 0 && kt + 1 < nk && (!kTail || k1 + kBK <= kend)) {
+        issue_and_read(st, st ^ 1, k1);
+      } else {
+        if (group == 0 && kt + 1 < nk) issue(st ^ 1, k1);
+        read(st);
+      }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stage before anyone overwrites it
       phase_barrier();
 #pragma unroll
