@@ -42,11 +42,15 @@ constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kThreads = 512;                          // 8 waves: 2 groups x 4
 constexpr int kWTM = 64, kWTN = 128;                   // wave tile
 constexpr int kTM = kWTM / 32, kTN = kWTN / 32;        // 32 x 32 MFMA tiles per wave: 2 x 4
-constexpr int kStageBytes = (kBM + kBN) * kBK;         // 64 KiB
+constexpr int kHalfBytes = kBM * kBK;                  // 32 KiB: one operand's K tile (kBM == kBN)
+constexpr int kAStages = 3, kBStages = 2;              // A is sent two K tiles ahead, B one
+constexpr int kBBase = kAStages * kHalfBytes;          // B stages follow the A stages
+constexpr int kLdsBytes = (kAStages + kBStages) * kHalfBytes;   // 160 KiB, all of gfx950's LDS
+static_assert(kBM == kBN, "A and B K tiles have the same size");
 constexpr int kCStageBytes = 32 * 256;                 // per wave: a 32 x 64 fp32 block of C on its way out
-static_assert(kThreads / 64 * kCStageBytes <= kStageBytes, "the C blocks of all waves fit in one stage");
-constexpr int kLoaders = 4;                            // group 0 issues the global loads
-constexpr int kLoads = (kBM + kBN) / 8 / kLoaders;     // 16 wave-instructions per stage per loading wave
+static_assert(kThreads / 2 / 64 * kCStageBytes == kHalfBytes, "each group's C blocks fill one half stage");
+constexpr int kLoaders = 4;                            // waves of a group
+constexpr int kLoads = kBM / 8 / kLoaders;             // 8 wave-instructions (1 KiB each) per operand K tile per wave
 constexpr int kGroupM = 4;
 constexpr int kBufferFlags = 0x00020000;               // raw buffer descriptor word 3 for gfx9-family targets
 constexpr int kOOB = (int)0x80000000;                  // an offset past any descriptor's range: reads zeros
@@ -103,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
                                                             const uint16_t *__restrict__ bias, uint16_t *__restrict__ C,
                                                             int64_t ldc, float *__restrict__ P, int M, int N, int K,
                                                             int ksplit, int tiles_m, int tiles_n, int splits) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
   // Declaring an AGPR clobber makes the compiler select the MFMA form that keeps accumulators in AGPRs.
   asm volatile("" ::: "a0");
 
@@ -112,10 +116,11 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int group = wave >> 2;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- loads (group 0). Wave instruction i fills stacked rows [R0, R0 + 8) of [A tile; B tile],
-  // R0 = (i * 4 + wave) * 8; lane j writes slot j & 7 of row R0 + j / 8, i.e. K chunk (j & 7) ^ swz(row). swz(row)
-  // does not depend on i, so every instruction's offset is a per-lane base plus i * 32 rows. Row offsets stay in
-  // the VGPR offset (the part the descriptor range-checks); only the K position goes to the scalar offset.
+  // ---- loads. A K tile of one operand is 256 rows x 128 bytes = 32 wave-instructions of 1 KiB, 8 per wave of a
+  // group. Instruction i of a wave fills rows [R0, R0 + 8), R0 = (i * 4 + wave % 4) * 8; lane j writes slot j & 7
+  // of row R0 + j / 8, i.e. K chunk (j & 7) ^ swz(row). swz(row) does not depend on i, so every instruction's offset
+  // is a per-lane base plus i * 32 rows. Row offsets stay in the VGPR offset (the part the descriptor
+  // range-checks); only the K position goes to the scalar offset.
   const int lrow = (wave & 3) * 8 + (lane >> 3);
   const int kchunk = 16 * ((lane & 7) ^ swz(lrow));
   const int baseA = lrow * lda + kchunk, baseB = lrow * ldb + kchunk;
@@ -145,31 +150,19 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const v4i rA = buffer_rsrc(A + (int64_t)m0 * lda, rows_a * lda);
     const v4i rB = buffer_rsrc(B + (int64_t)n0 * ldb, rows_b * ldb);
 
-    // Load i of the 16 this wave issues for a whole K tile at k0 into `stage`. The stride of 32 rows is opaque, so
-    // each load's offset is a scalar multiply here rather than a register held across the loop for each load.
-    auto load_full = [&](int stage, int k0, int i) {
+    // Load i (of 8) of this wave's share of operand `isA ? A : B`'s K tile at k0, into the LDS half stage at
+    // byte offset `dst`. The stride of 32 rows is opaque, so each load's offset is a scalar multiply here rather
+    // than a register held across the loop for each load. In the last, partial K tile (kTail instance only),
+    // chunks at or past kend read zeros.
+    auto load = [&](bool isA, int dst, int k0, int i) {
       const int R0 = (i * kLoaders + (wave & 3)) * 8;
-      const bool isA = i < kLoads / 2;
-      const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + (i - kLoads / 2) * opaque(32 * ldb);
-      lds_dma16(isA ? rA : rB, vo, k0, lds_addr(smem) + stage * kStageBytes + R0 * kBK);
+      const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + i * opaque(32 * ldb);
+      const uint32_t to = lds_addr(smem) + dst + R0 * kBK;
+      if (!kTail || k0 + kBK <= kend) lds_dma16(isA ? rA : rB, vo, k0, to);
+      else lds_dma16(isA ? rA : rB, k0 + kchunk < kend ? vo + k0 : kOOB, 0, to);
     };
-    auto issue = [&](int stage, int k0) {
-      if (!kTail || k0 + kBK <= kend) {
-#pragma unroll
-        for (int i = 0; i < kLoads; i++) load_full(stage, k0, i);
-      } else {  // the last, partial K tile: chunks at or past kend read zeros
-        const uint32_t sbase = lds_addr(smem) + stage * kStageBytes;
-        const int a32 = opaque(32 * lda), b32 = opaque(32 * ldb);
-        const bool kin = k0 + kchunk < kend;
-#pragma unroll
-        for (int i = 0; i < kLoads; i++) {
-          const int R0 = (i * kLoaders + (wave & 3)) * 8;
-          const bool isA = i < kLoads / 2;
-          const int vo = (isA ? baseA + i * a32 : baseB + (i - kLoads / 2) * b32) + k0;
-          lds_dma16(isA ? rA : rB, kin ? vo : kOOB, 0, sbase + R0 * kBK);
-        }
-      }
-    };
+    auto a_half = [](int stage) { return stage * kHalfBytes; };
+    auto b_half = [](int stage) { return kBBase + stage * kHalfBytes; };
 
     // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5).
     // Fragment j = 6 * step + f: f < kTM is A fragment f, otherwise B fragment f - kTM; two ds_read_b128 each.
@@ -177,35 +170,29 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const int frow = lane & 31;
     const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
     const int c0 = 2 * (lane >> 5);
-    auto read_frag = [&](int stage, int j) {
+    auto read_frag = [&](int ast, int bst, int j) {
       const int step = j / (kTM + kTN), f = j % (kTM + kTN);
       const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
-      const GPIC_LDS uint8_t *sA = (const GPIC_LDS uint8_t *)smem + stage * kStageBytes;
-      const GPIC_LDS uint8_t *p = f < kTM ? sA + (wm * kWTM + f * 32 + frow) * kBK
-                                          : sA + kBM * kBK + (wn * kWTN + (f - kTM) * 32 + frow) * kBK;
+      const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem +
+                                  (f < kTM ? a_half(ast) + (wm * kWTM + f * 32 + frow) * kBK
+                                           : b_half(bst) + (wn * kWTN + (f - kTM) * 32 + frow) * kBK);
       const u32x4 x0 = *(const GPIC_LDS u32x4 *)(p + lo), x1 = *(const GPIC_LDS u32x4 *)(p + hi);
       const v8i v{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
       if (f < kTM) fa[step][f] = v;
       else fb[step][f - kTM] = v;
     };
-    auto read = [&](int stage) {
-#pragma unroll
-      for (int j = 0; j < 2 * (kTM + kTN); j++) read_frag(stage, j);
-    };
-    // Group 0's memory phase with a whole next K tile: its 12 fragment reads interleaved with its 16 loads. A load
-    // issue waits while the texture unit's queue is full; with the reads between the loads, the LDS works through
-    // the reads during those waits instead of after the last load.
-    static_assert(2 * (kTM + kTN) == 12 && kLoads == 16, "interleave pattern: 3 fragments per 4 loads");
-    auto issue_and_read = [&](int rstage, int istage, int k0) {
+    // A memory phase: the wave's 12 fragment reads of K tile (ast, bst), with its 8 loads of one operand's later K
+    // tile between them when `send`. A load issue waits while the texture unit's queue is full; with the reads in
+    // between, the LDS works through the reads during those waits.
+    static_assert(2 * (kTM + kTN) == 12 && kLoads == 8, "interleave pattern: 3 fragments per 2 loads");
+    auto mem_phase = [&](int ast, int bst, bool send, bool isA, int dst, int k0) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        read_frag(rstage, 3 * j);
-        load_full(istage, k0, 4 * j);
-        read_frag(rstage, 3 * j + 1);
-        load_full(istage, k0, 4 * j + 1);
-        load_full(istage, k0, 4 * j + 2);
-        read_frag(rstage, 3 * j + 2);
-        load_full(istage, k0, 4 * j + 3);
+        read_frag(ast, bst, 3 * j);
+        if (send) load(isA, dst, k0, 2 * j);
+        read_frag(ast, bst, 3 * j + 1);
+        read_frag(ast, bst, 3 * j + 2);
+        if (send) load(isA, dst, k0, 2 * j + 1);
       }
     };
 
@@ -226,26 +213,47 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       __builtin_amdgcn_sched_barrier(0);
     };
 
-    // Prologue: group 0 sends K tile 0 and waits for it, then all meet, so it is complete in LDS before anyone reads
-    // it (the previous work item's last barrier ended every read of both stages). Group 1 then passes one extra
-    // barrier to run one phase behind group 0. Group 1 issues no loads, so its stores of the previous tile drain
-    // without anyone waiting for them.
-    if (group == 0 && nk > 0) issue(0, kbeg);
-    if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // K tile t: A half in A stage t % 3, B half in B stage t % 2. Group 0 reads tile kt in phase 2 kt and multiplies
+    // in 2 kt + 1; group 1 reads it in 2 kt + 1 and multiplies in 2 kt + 2. The loads are spread over both kinds of
+    // phase, each side's between its own fragment reads: group 0 sends B(kt + 1) in phase 2 kt and waits for it at
+    // the end of 2 kt + 1; group 1 sends A(kt + 2) in phase 2 kt + 1 and waits for it at the end of 2 kt + 3 (after
+    // sending A(kt + 3): vmcnt(8) leaves only those 8 in flight). Every stage written in a phase was last read two
+    // phases before: B stage (kt + 1) % 2 held tile kt - 1 (read in 2 kt - 2, 2 kt - 1); A stage (kt + 2) % 3 held
+    // tile kt - 1 as well.
+    // Prologue: group 0 sends A(0), B(0) and A(1) and waits for the first two (the previous work item's last barrier
+    // ended every read; its epilogue used only A stage 2 and B stage 1); all meet; group 1 then passes one extra
+    // barrier to run one phase behind group 0. Group 0 waits for A(1) with B(1), at the end of phase 1.
+    if (group == 0 && nk > 0) {
+#pragma unroll
+      for (int i = 0; i < kLoads; i++) load(true, a_half(0), kbeg, i);
+#pragma unroll
+      for (int i = 0; i < kLoads; i++) load(false, b_half(0), kbeg, i);
+      if (nk > 1) {
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) load(true, a_half(1), kbeg + kBK, i);
+      }
+    }
+    if (group == 0) {
+      if (nk > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     phase_barrier();
     if (group == 1) phase_barrier();
+    int ast = 0;   // A stage of K tile kt
     for (int kt = 0; kt < nk; ++kt) {
-      const int st = kt & 1;
-      // memory phase: send tile kt + 1 (group 0), read this wave's fragments of tile kt
-      const int k1 = kbeg + (kt + 1) * kBK;
-      if (group == 0 && kt + 1 < nk && (!kTail || k1 + kBK <= kend)) {
-        issue_and_read(st, st ^ 1, k1);
+      const int bst = kt & 1;
+      // memory phase
+      if (group == 0) {
+        mem_phase(ast, bst, kt + 1 < nk, false, b_half(bst ^ 1), kbeg + (kt + 1) * kBK);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stages before anyone overwrites them
       } else {
-        if (group == 0 && kt + 1 < nk) issue(st ^ 1, k1);
-        read(st);
+        mem_phase(ast, bst, kt + 2 < nk, true, a_half(ast == 0 ? 2 : ast - 1), kbeg + (kt + 2) * kBK);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (kt + 2 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");   // A(kt + 1) has landed
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stage before anyone overwrites it
       phase_barrier();
+      // MFMA phase
 #pragma unroll
       for (int step = 0; step < 2; step++)
 #pragma unroll
@@ -254,8 +262,9 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
           for (int mi = 0; mi < kTM; mi++)
             acc[ni][mi] =
                 __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[step][ni], fa[step][mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
-      if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kt + 1 has landed in LDS
+      if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // B(kt + 1) (and A(1)) have landed
       phase_barrier();
+      ast = ast == 2 ? 0 : ast + 1;
     }
     if (group == 0) phase_barrier();
 
@@ -284,10 +293,11 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     // VGPR copies of all 128), one 32 x 64 block (two ni tiles) at a time; each lane then reads back 8 consecutive
     // columns of one row, scales, rounds, adds the bias and stores 16 bytes, 8 lanes to a 128-byte line of C.
     // A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free both ways).
-    // Each wave uses its own 8 KiB of stage 1: nothing else touches stage 1 between this work item's last barrier
-    // and the next one's first barrier, and group 0 sends a K tile there only after that barrier, which group 1
-    // reaches only when its epilogue is done.
-    GPIC_LDS uint8_t *cst = (GPIC_LDS uint8_t *)smem + kStageBytes + wave * kCStageBytes;
+    // Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. Nothing reads or writes those between
+    // this work item's last barrier and the next one's first (the next prologue sends A(0), B(0), A(1)); the first
+    // loads into them come after that barrier, which group 1 reaches only when its epilogue is done.
+    GPIC_LDS uint8_t *cst =
+        (GPIC_LDS uint8_t *)smem + (group == 0 ? a_half(2) : b_half(1)) + (wave & 3) * kCStageBytes;
     const int wr = el & 31, wh = el >> 5;
     const int rr = el >> 3, rc = el & 7;
     u32x2 bw[kTN / 2][2] = {};
