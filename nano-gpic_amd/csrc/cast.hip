@@ -253,6 +253,18 @@ struct SrcSwiGLU {
     swiglu8(lut, z1, z2, v);
   }
 };
+// dz of one element (fp8_native.py:83-98), before its bf16 rounding: the z1 half da * z2 * sg * (1 + z1 * (1 - sg)),
+// the z2 half da * bf16(z1 * sg).
+__device__ __forceinline__ float dz1_of(float z1, float z2, float dv, float sg) {
+  const float t1 = 1.0f - sg;
+  const float t2 = z1 * t1;
+  const float t3 = 1.0f + t2;
+  const float g = sg * t3;
+  const float pr = dv * z2;
+  return pr * g;
+}
+__device__ __forceinline__ float dz2_of(float z1, float dv, float sg) { return dv * bf16_round(z1 * sg); }
+
 
 // src [rows, cols] (cols % 8 == 0) -> q [rows, cols] (row stride ldq; skipped when q == nullptr) and the transposed
 // bytes qt [cols, ldt] (ldt % 16 == 0, ldt >= rows), whose columns rows..ldt-1 are written as zeros so a GEMM can
@@ -275,12 +287,12 @@ __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int6
     lut_load(table, src.table);
     lut = table;
   }
-  float scale, deq;
-  scales_from_amax(fold_partials(partial, nparts), scale, deq);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  // The persistent (SwiGLU) workgroups fold the partial maxima once; the one-tile workgroups fold them after
+  // issuing their tile's loads, so the two latencies overlap (the fold's barriers wait for LDS only).
+  float scale = 0.0f, deq = 0.0f;
+  if constexpr (Src::kLut) scales_from_amax(fold_partials(partial, nparts), scale, deq);
   const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
   constexpr int kPer = kTT * (kTT / 8) / 256;  // 8-element chunks per thread per tile: 8
-  const uint8_t *tb = reinterpret_cast<const uint8_t *>(tile);
   // The SwiGLU source walks tiles (persistent workgroups); the others take exactly one tile each.
   const int64_t tstep = Src::kLut ? (int64_t)gridDim.x : tiles;
   for (int64_t t = blockIdx.x; t < tiles; t += tstep) {   // tiles walked column-block fastest
@@ -293,6 +305,7 @@ __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int6
       const int64_t gr = r0 + r, gc = c0 + 8 * cc;
       if (gr < rows && gc < cols) src.load8(gr, gc, v[i], lut);
     }
+    if constexpr (!Src::kLut) scales_from_amax(fold_partials(partial, nparts), scale, deq);
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
       const int id = threadIdx.x + 256 * i;
@@ -307,27 +320,36 @@ __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int6
       tile[r * kPitch + 2 * cc] = o.x;
       tile[r * kPitch + 2 * cc + 1] = o.y;
     }
-    __syncthreads();
-    // qt row c0 + c gets bytes r0 + 16 p .. r0 + 16 p + 15 of its column
+    lds_barrier();
+    // qt rows c0 + 4k .. c0 + 4k + 3 get bytes r0 + 16p .. r0 + 16p + 15 of their columns, k = tid / 8, p = tid % 8:
+    // four 4 x 4 byte blocks (rows 16p + 4g .. + 3, word k of the tile) transposed with v_perm_b32. Eight lanes
+    // write the 128 bytes of one qt row chunk.
+    {
+      const int k = threadIdx.x >> 3, p = threadIdx.x & 7;
+      u32x4 out[4];
 #pragma unroll
-    for (int j = 0; j < kTT * (kTT / 16) / 256; j++) {
-      const int id = threadIdx.x + 256 * j;
-      const int c = id >> 3, p = id & 7;
-      const int64_t gc = c0 + c, gr = r0 + 16 * p;
-      if (gc < cols && gr < ldt) {
-        uint32_t o[4];
+      for (int g = 0; g < 4; g++) {
+        const uint32_t *w = tile + (16 * p + 4 * g) * kPitch + k;
+        const uint32_t w0 = w[0], w1 = w[kPitch], w2 = w[2 * kPitch], w3 = w[3 * kPitch];
+        const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);   // w0.b0 w1.b0 w0.b1 w1.b1
+        const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);   // w0.b2 w1.b2 w0.b3 w1.b3
+        const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+        out[0][g] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);         // byte 0 of w0..w3
+        out[1][g] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);         // byte 1
+        out[2][g] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);         // byte 2
+        out[3][g] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);         // byte 3
+      }
+      const int64_t gr = r0 + 16 * p;
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-          uint32_t x = 0;
-#pragma unroll
-          for (int b = 0; b < 4; b++) x |= (uint32_t)tb[(16 * p + 4 * w + b) * (4 * kPitch) + c] << (8 * b);
-          o[w] = x;
-        }
-        *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = u32x4{o[0], o[1], o[2], o[3]};
+      for (int j = 0; j < 4; j++) {
+        const int64_t gc = c0 + 4 * k + j;
+        if (gc < cols && gr < ldt) *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = out[j];
       }
     }
+    if (blockIdx.x == 0 && threadIdx.x == 0 && t == 0) *dequant = deq;
     if constexpr (!Src::kLut) break;
-    __syncthreads();   // the tile buffer is rewritten by the next tile
+    lds_barrier();   // the tile buffer is rewritten by the next tile
   }
 }
 
@@ -407,6 +429,7 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_cast_kernel(const uint16_
 
 // dz = [d1 | d2] (fp8_native.py:88-96), each operation rounded on its own, left to right:
 //   sg = sigmoid(z1); sl = bf16(z1 * sg); d1 = bf16((da * z2) * (sg * (1 + z1 * (1 - sg)))); d2 = bf16(da * sl)
+// dz = [dz1 | dz2] and the partial maxima of its bf16 values.
 __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t *__restrict__ z,
                                                                    const uint16_t *__restrict__ da, int64_t M, int64_t H,
                                                                    int64_t sz, int64_t sda, uint16_t *__restrict__ dz,
@@ -429,14 +452,8 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
       float d1[8], d2[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const float sl = bf16_round(z1[i] * sg[i]);
-        const float t1 = 1.0f - sg[i];
-        const float t2 = z1[i] * t1;
-        const float t3 = 1.0f + t2;
-        const float g = sg[i] * t3;
-        const float pr = dv[i] * z2[i];
-        d1[i] = pr * g;
-        d2[i] = dv[i] * sl;
+        d1[i] = dz1_of(z1[i], z2[i], dv[i], sg[i]);
+        d2[i] = dz2_of(z1[i], dv[i], sg[i]);
       }
       u32x4 h1, h2;
 #pragma unroll

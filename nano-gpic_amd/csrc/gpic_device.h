@@ -123,13 +123,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 
 // Block-wide maximum (blockDim.x a multiple of 64, at most 1024); every thread gets the result.
+// Workgroup barrier for LDS communication only: waits for this wave's LDS operations, not for its global loads, so
+// loads issued before it stay in flight (__syncthreads' fence would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v) {
   __shared__ uint32_t red[16];
   v = wave_max_u32(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();  // red[] may still be read by a previous call
+  lds_barrier();  // red[] may still be read by a previous call
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  lds_barrier();
   uint32_t m = 0;
   for (int i = 0; i < nw; i++) m = red[i] > m ? red[i] : m;
   return m;
