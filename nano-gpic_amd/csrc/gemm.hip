@@ -128,90 +128,130 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 
   // ---- persistent: work item `it` (a tile and a K split) goes to workgroup it % gridDim.x. The grid is a multiple
   // of 8 (or covers every item in one pass), so it & 7 is the XCD the workgroup runs on and xcd_remap gives each
-  // XCD a contiguous range of tiles. A workgroup's stores of one tile drain while it loads and multiplies the next.
+  // XCD a contiguous range of tiles.
   const int tiles = tiles_m * tiles_n;
   const int work = tiles * splits;
-  for (int it = blockIdx.x; it < work; it += gridDim.x) {
+  struct Item {
+    int m0, n0, split, kbeg, kend, nk;
+    v4i rA, rB;   // buffer descriptors over the item's rows of A and B (rows past M / N read as zero)
+  };
+  auto item = [&](int it) {
+    Item w;
     const int lid = xcd_remap(it, work);
-    const int split = lid / tiles;
+    w.split = lid / tiles;
     const int tile = lid % tiles;
     const int per_group = kGroupM * tiles_n;
     const int first_m = (tile / per_group) * kGroupM;
     const int gsz = min(tiles_m - first_m, kGroupM);
-    const int tm = first_m + (tile % per_group) % gsz;
-    const int tn = (tile % per_group) / gsz;
-    const int m0 = tm * kBM, n0 = tn * kBN;
-    const int kbeg = split * ksplit;
-    const int kend = min(K, kbeg + ksplit);
-    const int nk = (kend - kbeg + kBK - 1) / kBK;
+    w.m0 = (first_m + (tile % per_group) % gsz) * kBM;
+    w.n0 = ((tile % per_group) / gsz) * kBN;
+    w.kbeg = w.split * ksplit;
+    w.kend = min(K, w.kbeg + ksplit);
+    w.nk = (w.kend - w.kbeg + kBK - 1) / kBK;
+    w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
+    w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBN) * ldb);
+    return w;
+  };
 
-    // ---- buffer descriptors over this tile's rows of A and B (rows past M / N read as zero)
-    const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBN);
-    const v4i rA = buffer_rsrc(A + (int64_t)m0 * lda, rows_a * lda);
-    const v4i rB = buffer_rsrc(B + (int64_t)n0 * ldb, rows_b * ldb);
-
-    // Load i (of 8) of this wave's share of operand `isA ? A : B`'s K tile at k0, into the LDS half stage at
-    // byte offset `dst`. The stride of 32 rows is opaque, so each load's offset is a scalar multiply here rather
-    // than a register held across the loop for each load. In the last, partial K tile (kTail instance only),
-    // chunks at or past kend read zeros.
-    auto load = [&](bool isA, int dst, int k0, int i) {
-      const int R0 = (i * kLoaders + (wave & 3)) * 8;
-      const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + i * opaque(32 * ldb);
-      const uint32_t to = lds_addr(smem) + dst + R0 * kBK;
-      if (!kTail || k0 + kBK <= kend) lds_dma16(isA ? rA : rB, vo, k0, to);
-      else lds_dma16(isA ? rA : rB, k0 + kchunk < kend ? vo + k0 : kOOB, 0, to);
-    };
-    auto a_half = [](int stage) { return stage * kHalfBytes; };
-    auto b_half = [](int stage) { return kBBase + stage * kHalfBytes; };
-
-    // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5).
-    // Fragment j = 6 * step + f: f < kTM is A fragment f, otherwise B fragment f - kTM; two ds_read_b128 each.
-    v8i fa[2][kTM], fb[2][kTN];
-    const int frow = lane & 31;
-    const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
-    const int c0 = 2 * (lane >> 5);
-    auto read_frag = [&](int ast, int bst, int j) {
-      const int step = j / (kTM + kTN), f = j % (kTM + kTN);
-      const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
-      const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem +
-                                  (f < kTM ? a_half(ast) + (wm * kWTM + f * 32 + frow) * kBK
-                                           : b_half(bst) + (wn * kWTN + (f - kTM) * 32 + frow) * kBK);
-      const u32x4 x0 = *(const GPIC_LDS u32x4 *)(p + lo), x1 = *(const GPIC_LDS u32x4 *)(p + hi);
-      const v8i v{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-      if (f < kTM) fa[step][f] = v;
-      else fb[step][f - kTM] = v;
-    };
-    // A memory phase: the wave's 12 fragment reads of K tile (ast, bst), with its 8 loads of one operand's later K
-    // tile between them when `send`. A load issue waits while the texture unit's queue is full; with the reads in
-    // between, the LDS works through the reads during those waits.
-    static_assert(2 * (kTM + kTN) == 12 && kLoads == 8, "interleave pattern: 3 fragments per 2 loads");
-    auto mem_phase = [&](int ast, int bst, bool send, bool isA, int dst, int k0) {
+  // Load i (of 8) of this wave's share of operand `isA ? A : B`'s K tile at k0 of item w, into the LDS half stage at
+  // byte offset `dst`. The stride of 32 rows is opaque, so each load's offset is a scalar multiply here rather than a
+  // register held across the loop for each load. In the last, partial K tile (kTail instance only), chunks at or past
+  // kend read zeros.
+  auto load = [&](const Item &w, bool isA, int dst, int k0, int i) {
+    const int R0 = (i * kLoaders + (wave & 3)) * 8;
+    const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + i * opaque(32 * ldb);
+    const uint32_t to = lds_addr(smem) + dst + R0 * kBK;
+    if (!kTail || k0 + kBK <= w.kend) lds_dma16(isA ? w.rA : w.rB, vo, k0, to);
+    else lds_dma16(isA ? w.rA : w.rB, k0 + kchunk < w.kend ? vo + k0 : kOOB, 0, to);
+  };
+  auto a_half = [](int stage) { return stage * kHalfBytes; };
+  auto b_half = [](int stage) { return kBBase + stage * kHalfBytes; };
+  // Group 0 sends an item's first loads: A(0), B(0) and, with a second K tile, A(1) (16 + 8 per wave).
+  auto send_prologue = [&](const Item &w) {
+    if (w.nk > 0) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        read_frag(ast, bst, 3 * j);
-        if (send) load(isA, dst, k0, 2 * j);
-        read_frag(ast, bst, 3 * j + 1);
-        read_frag(ast, bst, 3 * j + 2);
-        if (send) load(isA, dst, k0, 2 * j + 1);
-      }
-    };
+      for (int i = 0; i < kLoads; i++) load(w, true, a_half(0), w.kbeg, i);
+#pragma unroll
+      for (int i = 0; i < kLoads; i++) load(w, false, b_half(0), w.kbeg, i);
+    }
+    if (w.nk > 1) {
+#pragma unroll
+      for (int i = 0; i < kLoads; i++) load(w, true, a_half(1), w.kbeg + kBK, i);
+    }
+  };
 
+  // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5).
+  // Fragment j = 6 * step + f: f < kTM is A fragment f, otherwise B fragment f - kTM; two ds_read_b128 each.
+  v8i fa[2][kTM], fb[2][kTN];
+  const int frow = lane & 31;
+  const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
+  const int c0 = 2 * (lane >> 5);
+  auto read_frag = [&](int ast, int bst, int j) {
+    const int step = j / (kTM + kTN), f = j % (kTM + kTN);
+    const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
+    const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem +
+                                (f < kTM ? a_half(ast) + (wm * kWTM + f * 32 + frow) * kBK
+                                         : b_half(bst) + (wn * kWTN + (f - kTM) * 32 + frow) * kBK);
+    const u32x4 x0 = *(const GPIC_LDS u32x4 *)(p + lo), x1 = *(const GPIC_LDS u32x4 *)(p + hi);
+    const v8i v{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+    if (f < kTM) fa[step][f] = v;
+    else fb[step][f - kTM] = v;
+  };
+  // A memory phase: the wave's 12 fragment reads of K tile (ast, bst), with its 8 loads of one operand's later K
+  // tile between them when `send`. A load issue waits while the texture unit's queue is full; with the reads in
+  // between, the LDS works through the reads during those waits.
+  static_assert(2 * (kTM + kTN) == 12 && kLoads == 8, "interleave pattern: 3 fragments per 2 loads");
+  auto mem_phase = [&](const Item &w, int ast, int bst, bool send, bool isA, int dst, int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      read_frag(ast, bst, 3 * j);
+      if (send) load(w, isA, dst, k0, 2 * j);
+      read_frag(ast, bst, 3 * j + 1);
+      read_frag(ast, bst, 3 * j + 2);
+      if (send) load(w, isA, dst, k0, 2 * j + 1);
+    }
+  };
+
+  // Phase boundary: a bare s_barrier (no fence: the waits each side needs are explicit, so the loads issued in a
+  // memory phase stay in flight through it), pinned with sched_barrier so the compiler cannot move MFMAs
+  // (register-only instructions) across it into the other group's phase.
+  auto phase_barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // The waits below count vector-memory operations: on this target (no separate store counter) loads, LDS-DMA
+  // loads and stores all retire in issue order through one vmcnt, as the compiler itself assumes for gfx9 targets.
+  // Group 0's prologue wait: its A(0) and B(0) have landed once at most the 8 loads of A(1) (when sent) and the
+  // `pend` stores it issued after them are still in flight; the stores of the previous item drain meanwhile.
+  auto wait_prologue = [](bool two, int pend) {
+    if (pend == 0) {
+      if (two) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (pend == 16) {
+      if (two) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    } else {
+      if (two) asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+    }
+  };
+  constexpr int kStoresBF16 = kTM * (kTN / 2) * 4;   // bf16 epilogue: 16 buffer stores per wave, always issued
+  constexpr int kStoresF32 = kTN * kTM * 4;          // split-K partials: 32
+
+  int it = blockIdx.x;
+  Item cur = item(it);
+  if (group == 0) send_prologue(cur);
+  int pend = 0;   // stores group 0 issued after the current item's prologue loads
+  for (;;) {
     v16f acc[kTN][kTM];
 #pragma unroll
     for (int i = 0; i < kTN; i++)
 #pragma unroll
       for (int j = 0; j < kTM; j++) acc[i][j] = v16f{};
-
-    // Phase boundary: a bare s_barrier (no fence: the waits each side needs are explicit, so the loads group 0 issued
-    // in its memory phase stay in flight through it), pinned with sched_barrier so the compiler cannot move MFMAs
-    // (register-only instructions) across it into the other group's phase.
-    auto phase_barrier = [&]() {
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-    };
 
     // K tile t: A half in A stage t % 3, B half in B stage t % 2. Group 0 reads tile kt in phase 2 kt and multiplies
     // in 2 kt + 1; group 1 reads it in 2 kt + 1 and multiplies in 2 kt + 2. The loads are spread over both kinds of
@@ -220,37 +260,26 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     // sending A(kt + 3): vmcnt(8) leaves only those 8 in flight). Every stage written in a phase was last read two
     // phases before: B stage (kt + 1) % 2 held tile kt - 1 (read in 2 kt - 2, 2 kt - 1); A stage (kt + 2) % 3 held
     // tile kt - 1 as well.
-    // Prologue: group 0 sends A(0), B(0) and A(1) and waits for the first two (the previous work item's last barrier
-    // ended every read; its epilogue used only A stage 2 and B stage 1); all meet; group 1 then passes one extra
-    // barrier to run one phase behind group 0. Group 0 waits for A(1) with B(1), at the end of phase 1.
-    if (group == 0 && nk > 0) {
-#pragma unroll
-      for (int i = 0; i < kLoads; i++) load(true, a_half(0), kbeg, i);
-#pragma unroll
-      for (int i = 0; i < kLoads; i++) load(false, b_half(0), kbeg, i);
-      if (nk > 1) {
-#pragma unroll
-        for (int i = 0; i < kLoads; i++) load(true, a_half(1), kbeg + kBK, i);
-      }
-    }
-    if (group == 0) {
-      if (nk > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
+    // Prologue: group 0 sent A(0), B(0) and A(1) (before the previous item's epilogue, or above for the first) and
+    // waits for the first two; all meet; group 1 then passes one extra barrier to run one phase behind group 0. A(1)
+    // is waited for by group 0 with B(1), at the end of phase 1.
+    if (group == 0) wait_prologue(cur.nk > 1, pend);
     phase_barrier();
     if (group == 1) phase_barrier();
     int ast = 0;   // A stage of K tile kt
-    for (int kt = 0; kt < nk; ++kt) {
+    for (int kt = 0; kt < cur.nk; ++kt) {
       const int bst = kt & 1;
       // memory phase
       if (group == 0) {
-        mem_phase(ast, bst, kt + 1 < nk, false, b_half(bst ^ 1), kbeg + (kt + 1) * kBK);
+        mem_phase(cur, ast, bst, kt + 1 < cur.nk, false, b_half(bst ^ 1), cur.kbeg + (kt + 1) * kBK);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // done reading the stages before anyone overwrites them
       } else {
-        mem_phase(ast, bst, kt + 2 < nk, true, a_half(ast == 0 ? 2 : ast - 1), kbeg + (kt + 2) * kBK);
+        mem_phase(cur, ast, bst, kt + 2 < cur.nk, true, a_half(ast == 0 ? 2 : ast - 1), cur.kbeg + (kt + 2) * kBK);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (kt + 2 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");   // A(kt + 1) has landed
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (opaque(kt) > 0) {   // A(kt + 1) has landed (A(1) is group 0's, waited for by group 0); opaque: no peeled copy of the first iteration
+          if (kt + 2 < cur.nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
       }
       phase_barrier();
       // MFMA phase
@@ -268,85 +297,102 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     }
     if (group == 0) phase_barrier();
 
+    // ---- the next item's first loads go out now (into A stages 0, 1 and B stage 0: nothing reads them any more),
+    // so their latency passes during this item's epilogue
+    const int nit = it + gridDim.x;
+    const bool more = nit < work;
+    if (more && group == 0) send_prologue(item(nit));
+
     // ---- epilogue: acc[ni][mi] lane l holds D[n][m] for m = mi * 32 + (l & 31) and
-    // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns
+    // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns. Every store is a
+    // buffer store issued by every wave (lanes outside M x N get an offset past the descriptor's range and write
+    // nothing), so group 0 knows exactly how many stores follow its prologue loads.
     const int el = opaque_v(lane);
+    const int rows_c = min(M - cur.m0, kBM);
     if (P) {   // split-K fp32 partials: 16-byte stores straight from the accumulators
+      const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(P + ((int64_t)cur.split * M + cur.m0) * N), 0, rows_c * N * 4, kBufferFlags);
 #pragma unroll
       for (int ni = 0; ni < kTN; ni++)
 #pragma unroll
-        for (int mi = 0; mi < kTM; mi++) {
-          const int m = m0 + wm * kWTM + mi * 32 + (el & 31);
-          if (m >= M) continue;
+        for (int mi = 0; mi < kTM; mi++)
 #pragma unroll
           for (int q = 0; q < 4; q++) {
-            const int n = n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (el >> 5);
-            if (n >= N) continue;
+            const int r = wm * kWTM + mi * 32 + (el & 31);
+            const int n = cur.n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (el >> 5);
             const v16f &v = acc[ni][mi];
-            *reinterpret_cast<v4f *>(P + ((int64_t)split * M + m) * N + n) =
-                v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}), rP,
+                r < rows_c && n < N ? (r * N + n) * 4 : kOOB, 0, 0);
+          }
+      pend = kStoresF32;
+    } else {
+      // bf16 output through LDS. The accumulators go to LDS as fp32 straight from AGPRs (VALU work on them would
+      // need VGPR copies of all 128), one 32 x 64 block (two ni tiles) at a time; each lane then reads back 8
+      // consecutive columns of one row, scales, rounds, adds the bias and stores 16 bytes, 8 lanes to a 128-byte
+      // line of C. A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free both
+      // ways). Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. The next item's prologue
+      // loads go to A stages 0, 1 and B stage 0; the first loads into A stage 2 and B stage 1 come after the next
+      // item's first barrier, which group 1 reaches only when its epilogue is done.
+      GPIC_LDS uint8_t *cst =
+          (GPIC_LDS uint8_t *)smem + (group == 0 ? a_half(2) : b_half(1)) + (wave & 3) * kCStageBytes;
+      const __amdgpu_buffer_rsrc_t rC =
+          __builtin_amdgcn_make_buffer_rsrc((void *)(C + (int64_t)cur.m0 * ldc), 0, rows_c * (int)ldc * 2, kBufferFlags);
+      const int wr = el & 31, wh = el >> 5;
+      const int rr = el >> 3, rc = el & 7;
+      u32x2 bw[kTN / 2][2] = {};
+      if (bias) {
+#pragma unroll
+        for (int pair = 0; pair < kTN / 2; pair++) {
+          const int n = cur.n0 + wn * kWTN + pair * 64 + 8 * rc;
+          if (n < N) {
+            bw[pair][0] = *reinterpret_cast<const u32x2 *>(bias + n);
+            bw[pair][1] = *reinterpret_cast<const u32x2 *>(bias + n + 4);
           }
         }
-      continue;
-    }
-    // bf16 output through LDS. The accumulators go to LDS as fp32 straight from AGPRs (VALU work on them would need
-    // VGPR copies of all 128), one 32 x 64 block (two ni tiles) at a time; each lane then reads back 8 consecutive
-    // columns of one row, scales, rounds, adds the bias and stores 16 bytes, 8 lanes to a 128-byte line of C.
-    // A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free both ways).
-    // Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. Nothing reads or writes those between
-    // this work item's last barrier and the next one's first (the next prologue sends A(0), B(0), A(1)); the first
-    // loads into them come after that barrier, which group 1 reaches only when its epilogue is done.
-    GPIC_LDS uint8_t *cst =
-        (GPIC_LDS uint8_t *)smem + (group == 0 ? a_half(2) : b_half(1)) + (wave & 3) * kCStageBytes;
-    const int wr = el & 31, wh = el >> 5;
-    const int rr = el >> 3, rc = el & 7;
-    u32x2 bw[kTN / 2][2] = {};
-    if (bias) {
-#pragma unroll
-      for (int pair = 0; pair < kTN / 2; pair++) {
-        const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
-        if (n < N) {
-          bw[pair][0] = *reinterpret_cast<const u32x2 *>(bias + n);
-          bw[pair][1] = *reinterpret_cast<const u32x2 *>(bias + n + 4);
-        }
       }
-    }
 #pragma unroll
-    for (int mi = 0; mi < kTM; mi++) {
+      for (int mi = 0; mi < kTM; mi++) {
 #pragma unroll
-      for (int pair = 0; pair < kTN / 2; pair++) {
+        for (int pair = 0; pair < kTN / 2; pair++) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const v16f &v = acc[2 * pair + h][mi];
+          for (int h = 0; h < 2; h++) {
+            const v16f &v = acc[2 * pair + h][mi];
 #pragma unroll
-          for (int q = 0; q < 4; q++)
-            *(GPIC_LDS f4a_t *)(cst + wr * 256 + 16 * ((8 * h + 2 * q + wh) ^ (wr & 15))) =
-                f4a_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int r = 8 * j + rr;
-          const f4a_t x0 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc) ^ (r & 15)));
-          const f4a_t x1 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc + 1) ^ (r & 15)));
-          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-          st16_t w;
-#pragma unroll
-          for (int e = 0; e < 4; e++) w[e] = pack_bf16(x[2 * e] * s, x[2 * e + 1] * s);
-          if (bias) {   // bf16(bf16(acc * s) + bias): the output is rounded, then the bias add is rounded again
-            const uint32_t b[4] = {bw[pair][0].x, bw[pair][0].y, bw[pair][1].x, bw[pair][1].y};
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-              w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
+            for (int q = 0; q < 4; q++)
+              *(GPIC_LDS f4a_t *)(cst + wr * 256 + 16 * ((8 * h + 2 * q + wh) ^ (wr & 15))) =
+                  f4a_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
           }
-          const int m = m0 + wm * kWTM + mi * 32 + r;
-          const int n = n0 + wn * kWTN + pair * 64 + 8 * rc;
-          if (m < M && n < N) *reinterpret_cast<st16_t *>(C + (int64_t)m * ldc + n) = w;
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int r = 8 * j + rr;
+            const f4a_t x0 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc) ^ (r & 15)));
+            const f4a_t x1 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc + 1) ^ (r & 15)));
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            st16_t w;
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = pack_bf16(x[2 * e] * s, x[2 * e + 1] * s);
+            if (bias) {   // bf16(bf16(acc * s) + bias): the output is rounded, then the bias add is rounded again
+              const uint32_t b[4] = {bw[pair][0].x, bw[pair][0].y, bw[pair][1].x, bw[pair][1].y};
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
+            }
+            const int rl = wm * kWTM + mi * 32 + r;   // row within the tile
+            const int n = cur.n0 + wn * kWTN + pair * 64 + 8 * rc;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), rC,
+                                                   rl < rows_c && n < N ? (rl * (int)ldc + n) * 2 : kOOB, 0, 0);
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
       }
+      pend = kStoresBF16;
     }
-  }  // work items
+    if (!more) break;
+    it = nit;
+    cur = item(opaque(nit));   // recomputed rather than kept live through the epilogue
+  }
 }
 
 // Sum of the split-K partials in split order, then the same epilogue as the single-pass kernel.
