@@ -88,10 +88,12 @@ int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_
 /*
  * gpic_fp8_swiglu_tcast plus the transposed bytes qt [H, ldt] (H % 16 == 0, ldt % 16 == 0, ldt >= M; columns
  * M..ldt-1 zero): the K-major operand of w3's FP8 wgrad. Same bytes and scale as gpic_fp8_swiglu_tcast.
+ *   a  [M, H] bf16, contiguous, or NULL: when given, the SwiGLU product is written there by the amax pass and the
+ *      cast reads it instead of recomputing it (the same bytes; faster: the product is computed once)
  * No counterpart in the reference (its w3 wgrad is bf16, fp8_native.py:225,265); the FP8-wgrad extension.
  */
-int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, uint8_t *qt,
-                            int64_t ldt, float *dequant, void *ws, void *stream);
+int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint16_t *a, uint8_t *q, int64_t sq,
+                            uint8_t *qt, int64_t ldt, float *dequant, void *ws, void *stream);
 
 /*
  * gpic_fp8_swiglu_bwd plus the transposed bytes dzqt [2H, ldt] (ldt % 16 == 0, ldt >= M; columns M..ldt-1 zero):

@@ -360,9 +360,11 @@ __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int6
 // cast pass of the same call.
 constexpr int kRowsPer = 4;
 
+// Partial maxima of the SwiGLU product a; when `a` is given, also writes a ([M, H] bf16, contiguous; its values are
+// bf16 already, so the write is exact) for a cast that then reads it instead of recomputing it.
 __global__ __launch_bounds__(kCastThreads) void swiglu_amax_kernel(const uint16_t *__restrict__ z, int64_t M, int64_t H,
                                                                     int64_t sz, uint32_t *__restrict__ partial,
-                                                                    float *__restrict__ table) {
+                                                                    float *__restrict__ table, uint16_t *__restrict__ a) {
   __shared__ float lut[kLutSize];
   lut_build(lut);
   if (blockIdx.x == 0 && table)
@@ -382,19 +384,25 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_amax_kernel(const uint16_
       }
 #pragma unroll
       for (int k = 0; k < kRowsPer; k++) {
-        float a[8];
-        swiglu8(lut, z1[k], z2[k], a);
+        float v[8];
+        swiglu8(lut, z1[k], z2[k], v);
 #pragma unroll
-        for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(a[i]));
+        for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(v[i]));
+        if (a)
+          *reinterpret_cast<u32x4 *>(a + (r + k * rstride) * H + 8 * u) =
+              u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
       }
     }
     for (; r < M; r += rstride) {
       const uint16_t *zr = z + r * sz;
-      float a[8];
+      float v[8];
       swiglu8(lut, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u)),
-              __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u)), a);
+              __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u)), v);
 #pragma unroll
-      for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(a[i]));
+      for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(v[i]));
+      if (a)
+        *reinterpret_cast<u32x4 *>(a + r * H + 8 * u) =
+            u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
     }
   }
   m = block_max_u32(m);
@@ -553,24 +561,27 @@ int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, u
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws));
+  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws), nullptr);
   swiglu_cast_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, g, q, sq, dequant, ws_table(ws));
   return (int)hipGetLastError();
 }
 
-int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, uint8_t *qt,
-                            int64_t ldt, float *dequant, void *ws, void *stream) {
+int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint16_t *a, uint8_t *q, int64_t sq,
+                            uint8_t *qt, int64_t ldt, float *dequant, void *ws, void *stream) {
   if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !q)) || (H > 0 && ldt > 0 && !qt))
     return GPIC_EINVAL;
   if (H % 16 != 0 || sz % 8 != 0 || sq % 8 != 0 || sz < 2 * H || sq < H || ldt % 16 != 0 || ldt < M)
     return GPIC_ESHAPE;
-  if (!aligned16(z) || !aligned16(q) || !aligned16(qt) || !aligned16(ws)) return GPIC_EALIGN;
+  if (!aligned16(z) || !aligned16(a) || !aligned16(q) || !aligned16(qt) || !aligned16(ws)) return GPIC_EALIGN;
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws));
+  // with `a`, the first pass writes the product and the cast reads it; without, the cast recomputes it from z
+  swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws), a);
   if (H == 0 || ldt == 0)
     cast_kernel<uint16_t><<<1, kCastThreads, 0, st>>>(nullptr, 0, partial, g, nullptr, dequant);
+  else if (a)
+    launch_cast_t(SrcBF16{a, H}, M, H, g, q, sq, qt, ldt, dequant, partial, st);
   else
     launch_cast_t(SrcSwiGLU{z, sz, H, ws_table(ws)}, M, H, g, q, sq, qt, ldt, dequant, partial, st);
   return (int)hipGetLastError();

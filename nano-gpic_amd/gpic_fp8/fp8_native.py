@@ -140,10 +140,12 @@ def swiglu_tcast_t(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.T
     q = torch.empty(M, H, dtype=E4, device=z.device)
     qt = torch.empty(H, _r16(M), dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
+    # the product a goes through HBM once (written by the amax pass, read by the cast) instead of being recomputed
+    a = torch.empty(M, H, dtype=torch.bfloat16, device=z.device)
     with torch.cuda.device(z.device):
         ws = L.cast_workspace(z.device)
-        L.check(L.lib().gpic_fp8_swiglu_tcast_t(zc.data_ptr(), M, H, zc.stride(0), q.data_ptr(), q.stride(0),
-                                                qt.data_ptr(), qt.shape[1], s.data_ptr(), ws.data_ptr(),
+        L.check(L.lib().gpic_fp8_swiglu_tcast_t(zc.data_ptr(), M, H, zc.stride(0), a.data_ptr(), q.data_ptr(),
+                                                q.stride(0), qt.data_ptr(), qt.shape[1], s.data_ptr(), ws.data_ptr(),
                                                 L.stream_ptr(z.device)), "gpic_fp8_swiglu_tcast_t")
     return q, qt, s
 

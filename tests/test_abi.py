@@ -57,7 +57,7 @@ def test_validation_codes():
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 12, 24, wsp, 12, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 16, 16, wsp, 16, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_bwd(wsp, wsp, 4, 16, 32, 8, wsp, wsp, wsp, wsp, None) == -3
-    assert lib.gpic_fp8_swiglu_tcast_t(wsp, 40, 16, 32, wsp, 16, wsp, 32, wsp, wsp, None) == -3
+    assert lib.gpic_fp8_swiglu_tcast_t(wsp, 40, 16, 32, None, wsp, 16, wsp, 32, wsp, wsp, None) == -3
     # GEMM: K % 16, N % 16, leading dimensions, null scales
     g = lib.gpic_fp8_gemm
     assert g(wsp, 24, wsp, wsp, 24, wsp, None, wsp, 16, 4, 16, 24, 1, None, 0, None) == -3

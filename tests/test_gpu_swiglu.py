@@ -122,6 +122,31 @@ def test_transposing_variants(dev):
     assert not dqt.view(torch.uint8)[:, M:].any()
 
 
+@pytest.mark.parametrize("M,H", [(1000, 256), (33, 16)])
+def test_tcast_t_with_and_without_product_buffer(dev, M, H):
+    """gpic_fp8_swiglu_tcast_t either writes the product a and casts it, or recomputes it inside the cast: the same
+    bytes and scale; the written product equals the oracle's."""
+    from gpic_fp8 import _lib as L
+    z = rand_bf16((M, 2 * H), 3.0, seed=M + 31).to(dev)
+    m16 = (M + 15) // 16 * 16
+    out = []
+    for with_a in (True, False):
+        a = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+        q = torch.empty(M, H, dtype=torch.uint8, device=dev)
+        qt = torch.empty(H, m16, dtype=torch.uint8, device=dev)
+        s = torch.empty(1, dtype=torch.float32, device=dev)
+        ws = L.cast_workspace(dev)
+        rc = L.lib().gpic_fp8_swiglu_tcast_t(z.data_ptr(), M, H, z.stride(0), a.data_ptr() if with_a else None,
+                                             q.data_ptr(), H, qt.data_ptr(), m16, s.data_ptr(), ws.data_ptr(),
+                                             L.stream_ptr(dev))
+        assert rc == 0
+        torch.cuda.synchronize()
+        out.append((a, q, qt, s.item()))
+    (a, q1, qt1, s1), (_, q2, qt2, s2) = out
+    assert s1 == s2 and torch.equal(q1, q2) and torch.equal(qt1, qt2)
+    assert np.array_equal(bits(a), O.swiglu_product(bits(z.cpu())))
+
+
 def test_bwd_matches_eager_torch_within_one_ulp(dev):
     """The eager phase-1 backward (fp8_native.py:226-231, torch.sigmoid) agrees with the kernel's dz within 1 ulp."""
     M, H = 512, 1024
