@@ -506,6 +506,105 @@ static void launch_cast_t(Src src, int64_t rows, int64_t cols, int nparts, uint8
   cast_t_kernel<Src><<<grid, 256, 0, st>>>(src, rows, cols, partial, nparts, q, ldq, qt, ldt, dequant);
 }
 
+// The transposing cast of a bf16 source, persistent: each workgroup folds the partial maxima once, then walks its
+// tiles, loading the next tile's bf16 (kept raw: 32 VGPRs) while it casts, transposes and stores the current one.
+// Same tile layout and bytes as cast_t_kernel.
+__global__ __launch_bounds__(256) void cast_t_bf16_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows,
+                                                          int64_t cols, const uint32_t *__restrict__ partial, int nparts,
+                                                          uint8_t *__restrict__ q, int64_t ldq, uint8_t *__restrict__ qt,
+                                                          int64_t ldt, float *__restrict__ dequant) {
+  constexpr int kPitch = kTT / 4 + 1;          // words per LDS row (one word of padding)
+  __shared__ uint32_t tile[kTT * kPitch];      // [row][col / 4] e4m3 bytes
+  constexpr int kPer = kTT * (kTT / 8) / 256;  // 8-element chunks per thread per tile: 8
+  const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
+  // chunk i of a thread: row id / 16, columns 8 (id % 16) .. + 7 of the tile, id = tid + 256 i; zero outside x
+  auto load_raw = [&](int64_t t, u32x4 (&R)[kPer]) {
+    const int64_t c0 = (t % tiles_c) * kTT, r0 = (t / tiles_c) * kTT;
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int id = threadIdx.x + 256 * i;
+      const int64_t gr = r0 + (id >> 4), gc = c0 + 8 * (id & 15);
+      R[i] = gr < rows && gc < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + gr * ld + gc))
+                                    : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  int64_t t = blockIdx.x;   // < tiles: the grid never exceeds the tile count
+  u32x4 R[kPer];
+  load_raw(t, R);
+  float scale, deq;
+  scales_from_amax(fold_partials(partial, nparts), scale, deq);   // its barriers wait for LDS only
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  for (; t < tiles; t += gridDim.x) {
+    const int64_t tn = t + gridDim.x;
+    u32x4 Rn[kPer];
+    if (tn < tiles) {
+      load_raw(tn, Rn);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPer; i++) Rn[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+    const int64_t c0 = (t % tiles_c) * kTT, r0 = (t / tiles_c) * kTT;
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int id = threadIdx.x + 256 * i;
+      const int r = id >> 4, cc = id & 15;
+      const int64_t gr = r0 + r, gc = c0 + 8 * cc;
+      float v[8];
+      unpack8(R[i], v);
+      u32x2 o;
+      o.x = e4m3x4(sat(v[0] * scale), sat(v[1] * scale), sat(v[2] * scale), sat(v[3] * scale));
+      o.y = e4m3x4(sat(v[4] * scale), sat(v[5] * scale), sat(v[6] * scale), sat(v[7] * scale));
+      if (q && gr < rows && gc < cols) *reinterpret_cast<u32x2 *>(q + gr * ldq + gc) = o;
+      tile[r * kPitch + 2 * cc] = o.x;
+      tile[r * kPitch + 2 * cc + 1] = o.y;
+    }
+    lds_barrier();
+    // qt rows c0 + 4k .. c0 + 4k + 3 get bytes r0 + 16p .. r0 + 16p + 15 of their columns, k = tid / 8, p = tid % 8
+    // (as in cast_t_kernel)
+    {
+      const int k = threadIdx.x >> 3, p = threadIdx.x & 7;
+      u32x4 out[4];
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const uint32_t *w = tile + (16 * p + 4 * g) * kPitch + k;
+        const uint32_t w0 = w[0], w1 = w[kPitch], w2 = w[2 * kPitch], w3 = w[3 * kPitch];
+        const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+        out[0][g] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+        out[1][g] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+        out[2][g] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+        out[3][g] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+      }
+      const int64_t gr = r0 + 16 * p;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int64_t gc = c0 + 4 * k + j;
+        if (gc < cols && gr < ldt) *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = out[j];
+      }
+    }
+    lds_barrier();   // the tile buffer is rewritten by the next tile
+#pragma unroll
+    for (int i = 0; i < kPer; i++) R[i] = Rn[i];
+  }
+}
+
+// bf16 sources take the persistent kernel above up to 8 tiles per workgroup, the one-tile kernel beyond (measured on
+// [32768, C]: persistent 7-15% faster for C = 2048..4096, 5% slower for C = 8192)
+constexpr int64_t kCastTPersistentTiles = 8 * kCastTBlocks;
+static void launch_cast_t(SrcBF16 src, int64_t rows, int64_t cols, int nparts, uint8_t *q, int64_t ldq, uint8_t *qt,
+                          int64_t ldt, float *dequant, const uint32_t *partial, hipStream_t st) {
+  const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
+  if (tiles > kCastTPersistentTiles) {
+    cast_t_kernel<SrcBF16><<<(int)tiles, 256, 0, st>>>(src, rows, cols, partial, nparts, q, ldq, qt, ldt, dequant);
+    return;
+  }
+  const int grid = (int)(tiles < kCastTBlocks ? tiles : kCastTBlocks);
+  cast_t_bf16_kernel<<<grid, 256, 0, st>>>(src.x, src.ld, rows, cols, partial, nparts, q, ldq, qt, ldt, dequant);
+}
+
+
 // SwiGLU kernels: rows strided over at most kSwigluBlocks workgroups (each builds its 24 KiB sigmoid table once).
 static inline int swiglu_grid(int64_t M) { return (int)(M < 1 ? 1 : (M > kSwigluBlocks ? kSwigluBlocks : M)); }
 

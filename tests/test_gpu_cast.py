@@ -114,6 +114,22 @@ def test_tcast_t_matches_oracle(dev):
         assert np.array_equal(qtn[:, :rows], oq.T) and not qtn[:, rows:].any()
 
 
+@pytest.mark.parametrize("rows,cols", [(4099, 4112), (8193, 16400)])
+def test_tcast_t_large_ragged(dev, rows, cols):
+    """Both bf16 transposing kernels: 1089 tiles on the persistent grid (some workgroups take two tiles, the second
+    prefetched) and 8385 tiles, past the persistent limit (one tile per workgroup). q equals the flat cast's bytes,
+    qt its transpose with zero padding."""
+    g = torch.Generator(device=dev).manual_seed(rows)
+    x = (torch.randn(rows, cols, generator=g, device=dev) * 5).to(torch.bfloat16)
+    q, qt, s = G.tcast_t(x)
+    qf, sf = G.tcast(x)
+    r16 = (rows + 15) // 16 * 16
+    assert s.item() == sf.item() and torch.equal(q.view(torch.uint8), qf.view(torch.uint8))
+    qtb = qt.view(torch.uint8)
+    assert qtb.shape == (cols, r16) and torch.equal(qtb[:, :rows], q.view(torch.uint8).t())
+    assert not qtb[:, rows:].any()
+
+
 def test_transpose_invariant(dev):
     """tcast_t(w).qt == tcast(w.t().contiguous()).q: the reference casts the transposed weight (fp8_native.py:259)."""
     w = (torch.randn(1024, 4096, device=dev) / 64).to(torch.bfloat16)
