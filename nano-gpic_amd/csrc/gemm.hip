@@ -23,6 +23,8 @@
 //    range of tiles in groups of kGroupM tile rows (neighbouring workgroups share A and B panels in that XCD's L2).
 //  * Split-K (for the small-output wgrad shapes): each split writes fp32 partials; a second kernel sums them in
 //    split order (deterministic) and applies scale, bias and the bf16 rounding.
+#include <algorithm>
+
 #include "gpic_device.h"
 #include "gpic_launch.h"
 
@@ -433,19 +435,36 @@ static int num_cus() {
   return cus;
 }
 
-// Split K only when the output has too few tiles to fill the chip and each split keeps >= 8 K tiles.
+// The K split: the number of splits s (and K tiles per split) that minimises a model of the run time. Work items
+// (tiles x splits) run in rounds of one per CU; a round lasts as long as its items' K tiles plus a fixed cost per
+// item (prologue, epilogue); splitting adds the reduce, which reads s fp32 partials of C and writes C. Model constants
+// from measured d12 shapes: ~1.45 us per K tile, ~4 us per item (5 with fp32 partials), ~5 TB/s for the reduce.
+// Split-K also needs N < 2^21 (the partials' 32-bit buffer offsets).
 static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
   Plan p;
   p.tiles_m = (int)((M + kBM - 1) / kBM);
   p.tiles_n = (int)((N + kBN - 1) / kBN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
   const int64_t ktiles = (K + kBK - 1) / kBK;
-  int splits = 1;
-  const int cus = num_cus();
-  while (tiles * splits < cus && ktiles / (splits * 2) >= 8) splits *= 2;
-  const int64_t kt_per = (ktiles + splits - 1) / splits;
-  p.ksplit = (int)(kt_per * kBK);
-  p.splits = (int)((ktiles + kt_per - 1) / kt_per);
+  const int64_t cus = num_cus();
+  const int64_t max_splits = N < (1 << 21) ? std::min<int64_t>(ktiles, 64) : 1;
+  double best = 0.0;
+  int64_t best_per = ktiles;
+  for (int64_t s = 1; s <= max_splits; s++) {
+    const int64_t per = (ktiles + s - 1) / s;          // K tiles per split
+    const int64_t splits = (ktiles + per - 1) / per;   // splits actually needed
+    if (splits != s) continue;
+    const int64_t rounds = (tiles * splits + cus - 1) / cus;
+    double t = (double)rounds * ((double)per * 1.45 + (splits > 1 ? 5.0 : 4.0));
+    if (splits > 1) t += ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
+    if (s == 1 || t < best) {
+      best = t;
+      best_per = per;
+    }
+  }
+  p.ksplit = (int)(best_per * kBK);
+  p.splits = (int)((ktiles + best_per - 1) / best_per);
+  if (ktiles == 0) p.splits = 1;
   return p;
 }
 
