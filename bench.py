@@ -59,15 +59,23 @@ def parse():
     return p.parse_args()
 
 
-def make_inputs(dev, seed=0):
+def make_inputs(dev, seed=0, C=C, H=H, outliers=0.0):
+    """The block's inputs: X ~ N(0,1), W ~ N(0, 1/K), dY ~ N(0, 1e-2), bf16. With `outliers`, that fraction of the
+    activation channels (the same columns in every X) is scaled by 50 before the bf16 rounding (config 5)."""
     import torch
     g = torch.Generator(device=dev).manual_seed(seed)
+    cols = torch.randperm(C, generator=g, device=dev)[:round(outliers * C)]
 
     def bf(*shape, std=1.0):
         return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16)
 
+    def act():
+        x = torch.randn(M_TOK, C, generator=g, device=dev)
+        x[:, cols] *= 50.0
+        return x.to(torch.bfloat16)
+
     t = {
-        "x_qkv": bf(M_TOK, C), "x_proj": bf(M_TOK, C), "x_mlp": bf(M_TOK, C),
+        "x_qkv": act(), "x_proj": act(), "x_mlp": act(),
         "w_qkv": bf(3 * C, C, std=C ** -0.5), "w_proj": bf(C, C, std=C ** -0.5),
         "w12": bf(2 * H, C, std=C ** -0.5), "w3": bf(C, H, std=H ** -0.5),
         "dy_qkv": bf(M_TOK, 3 * C, std=0.1), "dy_proj": bf(M_TOK, C, std=0.1), "dy_mlp": bf(M_TOK, C, std=0.1),
@@ -241,6 +249,32 @@ def main():
     xc = xc.to(torch.bfloat16).to(dev)
     cast_ms = time_region(lambda: G.tcast(xc), 50, 10)
     cast_bytes = xc.numel() * 3 + 4
+    # the same with L2 / MALL flushed before each call (a 512 MB write between the timed launches)
+    flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    cold = []
+    for _ in range(20):
+        flush.fill_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        G.tcast(xc)
+        e1.record()
+        e1.synchronize()
+        cold.append(e0.elapsed_time(e1))
+    cast_cold_ms = sorted(cold)[len(cold) // 2]
+    del flush
+
+    # ---- config 5: the d18 block (C = 1792, H = 7168) with 1% outlier activation channels, fwd + bwd
+    C18, H18 = 1792, 7168
+    t18 = make_inputs(dev, seed=5, C=C18, H=H18, outliers=0.01)
+
+    def run18():
+        for v in t18.values():
+            v.grad = None
+        step(G, t18)
+
+    fl18 = flops(gemm_shapes(M_TOK, C18, H18))
+    ms18 = time_region(run18, 5, 2)
+    del t18
 
     # ---- comparator: hipBLASLt FP8 GEMM (torch._scaled_mm) on the same shapes
     hip = None
@@ -287,7 +321,11 @@ def main():
         "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale", "us": round(cast_ms * 1e3, 2),
                  "achieved_GBs": round(cast_bytes / cast_ms / 1e6, 1), "peak_GBs": PEAK_HBM_GBS,
                  "frac": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4),
-                 "algorithmic_bytes": cast_bytes},
+                 "algorithmic_bytes": cast_bytes, "us_l2_flushed": round(cast_cold_ms * 1e3, 2),
+                 "frac_l2_flushed": round(cast_bytes / cast_cold_ms / 1e6 / PEAK_HBM_GBS, 4)},
+        "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
+                      "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
+                      "tflops": round(fl18 / ms18 / 1e9, 1)},
         "hipblaslt_compare": hip,
         "cpu_baseline": cpu,
     }
