@@ -156,3 +156,32 @@ def test_d12_shapes(dev, name, M, N, K):
     c = G.fp8_gemm(xq, sx, wq, sw)
     assert rel(c, ref_fp32(xq, sx, wq, sw)) < 4e-3
     assert_elementwise(c, xq, sx.item(), wq, sw.item())
+
+
+@pytest.mark.parametrize("M,N,K,bias,lda_pad", [
+    (9000, 4000, 512, False, 0),      # 36 x 16 = 576 work items: 3 rounds per CU, ragged last row / column of tiles
+    (4999, 2992, 1040, True, 16),     # partial K tile (K % 128 = 16), bias, padded leading dimension of A
+    (700, 528, 9984, False, 0),       # few tiles: split K, the last split shorter
+    (33, 4112, 2048, True, 0),        # one tile row, many columns, bias
+    (6000, 256, 4096, False, 48),     # one tile column, split K may or may not apply
+    (257, 257 // 16 * 16 + 16, 160, True, 0),   # tiny K, two splits with a partial tile
+])
+def test_shape_sweep(dev, M, N, K, bias, lda_pad):
+    """Shapes that put several work items on each CU, partial tiles in M, N and K, split-K with a short last split,
+    the bias epilogue and a padded leading dimension: every element within the bound of assert_elementwise against
+    the float64 product, and the same bytes on a second call."""
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    base = (torch.randn(M, K + lda_pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)
+    a = base[:, :K]
+    b = rand_e4((N, K), 20.0, M + 1, dev)
+    sa = torch.tensor([0.011], device=dev)
+    sb = torch.tensor([0.017], device=dev)
+    bv = (torch.randn(N, generator=g, device=dev) * 0.5).to(torch.bfloat16) if bias else None
+    pollute(dev)
+    c = G.fp8_gemm(a, sa, b, sb, bv)
+    if bias:
+        c0 = G.fp8_gemm(a, sa, b, sb)
+        assert torch.equal(c, (c0.float() + bv.float()).to(torch.bfloat16))
+        c = c0
+    assert_elementwise(c, a, 0.011, b, 0.017)
+    assert torch.equal(c, G.fp8_gemm(a, sa, b, sb))
