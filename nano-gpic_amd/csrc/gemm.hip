@@ -49,8 +49,6 @@ constexpr int kAStages = 3, kBStages = 2;              // A is sent two K tiles 
 constexpr int kBBase = kAStages * kHalfBytes;          // B stages follow the A stages
 constexpr int kLdsBytes = (kAStages + kBStages) * kHalfBytes;   // 160 KiB, all of gfx950's LDS
 static_assert(kBM == kBN, "A and B K tiles have the same size");
-constexpr int kCStageBytes = 32 * 256;                 // per wave: a 32 x 64 fp32 block of C on its way out
-static_assert(kThreads / 2 / 64 * kCStageBytes == kHalfBytes, "each group's C blocks fill one half stage");
 constexpr int kLoaders = 4;                            // waves of a group
 constexpr int kLoads = kBM / 8 / kLoaders;             // 8 wave-instructions (1 KiB each) per operand K tile per wave
 constexpr int kGroupM = 4;
@@ -58,6 +56,16 @@ constexpr int kBufferFlags = 0x00020000;               // raw buffer descriptor 
 constexpr int kOOB = (int)0x80000000;                  // an offset past any descriptor's range: reads zeros
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+// The column of C that MFMA output row i (0..31) of a 32 x 32 tile stands for: i with bits 2 and 3 exchanged. Lane l
+// holds output rows 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15; through this map those are the columns
+// 16 (v / 8) + 8 (l / 32) + v % 8, i.e. two runs of 8 consecutive columns. An involution that keeps every aligned
+// group of 16 rows, so with N % 16 == 0 the rows past N stay past N.
+__host__ __device__ constexpr int col_of(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+constexpr int kCStageBytes = 32 * 256;                 // per wave: a 32 x 128 bf16 block of C on its way out
+static_assert(kThreads / 2 / 64 * kCStageBytes == kHalfBytes, "each group's C blocks fill one half stage");
+static_assert(col_of(13) == 13 && col_of(8) == 4 && col_of(4) == 8 && col_of(17) == 17 && col_of(col_of(22)) == 22,
+              "col_of swaps bits 2 and 3");
 
 // Raw buffer descriptor (stride 0) over [base, base + bytes): offsets at or past `bytes` read as zero.
 __device__ __forceinline__ v4i buffer_rsrc(const void *base, int bytes) {
@@ -79,6 +87,14 @@ __device__ __forceinline__ void lds_dma16(v4i rsrc, int voffset, int soffset, ui
                :
                : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds)
                : "memory", "m0");
+}
+
+// One accumulator element copied from its AGPR right where it is used. Read through plain C++, the compiler copies
+// all 128 accumulators to VGPRs at once when the K loop ends (spilling what does not fit).
+__device__ __forceinline__ float acc_read(float x) {
+  float r;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
+  return r;
 }
 
 // A uniform value the compiler must recompute where it is used: keeps it from hoisting the 16 per-load row offsets
@@ -125,7 +141,9 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // range-checks); only the K position goes to the scalar offset.
   const int lrow = (wave & 3) * 8 + (lane >> 3);
   const int kchunk = 16 * ((lane & 7) ^ swz(lrow));
-  const int baseA = lrow * lda + kchunk, baseB = lrow * ldb + kchunk;
+  // B rows are permuted inside each group of 32: LDS row r holds B row col_of(r), so that each lane's accumulators
+  // hold runs of 8 consecutive columns of C (see the epilogue).
+  const int baseA = lrow * lda + kchunk, baseB = col_of(lrow) * ldb + kchunk;
   const float s = sa[0] * sb[0];
 
   // ---- persistent: work item `it` (a tile and a K split) goes to workgroup it % gridDim.x. The grid is a multiple
@@ -241,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
     }
   };
-  constexpr int kStoresBF16 = kTM * (kTN / 2) * 4;   // bf16 epilogue: 16 buffer stores per wave, always issued
+  constexpr int kStoresBF16 = kTM * kTN * 2;         // bf16 epilogue: 16 buffer stores per wave, always issued
   constexpr int kStoresF32 = kTN * kTM * 4;          // split-K partials: 32
 
   int it = blockIdx.x;
@@ -305,13 +323,16 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const bool more = nit < work;
     if (more && group == 0) send_prologue(item(nit));
 
-    // ---- epilogue: acc[ni][mi] lane l holds D[n][m] for m = mi * 32 + (l & 31) and
-    // n = ni * 32 + 8 * (r / 4) + 4 * (l >> 5) + r % 4, r = 0..15: runs of 4 consecutive columns. Every store is a
-    // buffer store issued by every wave (lanes outside M x N get an offset past the descriptor's range and write
-    // nothing), so group 0 knows exactly how many stores follow its prologue loads.
+    // ---- epilogue: acc[ni][mi] lane l holds C[m][n] for m = mi * 32 + (l & 31) and, through col_of,
+    // n = ni * 32 + 16 * (r / 8) + 8 * (l >> 5) + r % 8, r = 0..15: two runs of 8 consecutive columns, each one
+    // 16-byte bf16 store (or two fp32 ones) straight from the accumulators; the lanes l and l + 32 of a row fill 32
+    // contiguous bytes of it. Every store is a buffer store issued by every wave (lanes outside M x N get an offset
+    // past the descriptor's range and write nothing), so group 0 knows exactly how many stores follow its prologue
+    // loads.
     const int el = opaque_v(lane);
     const int rows_c = min(M - cur.m0, kBM);
-    if (P) {   // split-K fp32 partials: 16-byte stores straight from the accumulators
+    const int wr = el & 31, wh = el >> 5;
+    if (P) {   // split-K fp32 partials
       const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(P + ((int64_t)cur.split * M + cur.m0) * N), 0, rows_c * N * 4, kBufferFlags);
 #pragma unroll
@@ -320,8 +341,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
         for (int mi = 0; mi < kTM; mi++)
 #pragma unroll
           for (int q = 0; q < 4; q++) {
-            const int r = wm * kWTM + mi * 32 + (el & 31);
-            const int n = cur.n0 + wn * kWTN + ni * 32 + 8 * q + 4 * (el >> 5);
+            const int r = wm * kWTM + mi * 32 + wr;
+            const int n = cur.n0 + wn * kWTN + ni * 32 + 16 * (q >> 1) + 8 * wh + 4 * (q & 1);
             const v16f &v = acc[ni][mi];
             __builtin_amdgcn_raw_buffer_store_b128(
                 __builtin_bit_cast(u32x4, v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}), rP,
@@ -329,65 +350,51 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
           }
       pend = kStoresF32;
     } else {
-      // bf16 output through LDS. The accumulators go to LDS as fp32 straight from AGPRs (VALU work on them would
-      // need VGPR copies of all 128), one 32 x 64 block (two ni tiles) at a time; each lane then reads back 8
-      // consecutive columns of one row, scales, rounds, adds the bias and stores 16 bytes, 8 lanes to a 128-byte
-      // line of C. A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free both
-      // ways). Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. The next item's prologue
-      // loads go to A stages 0, 1 and B stage 0; the first loads into A stage 2 and B stage 1 come after the next
-      // item's first barrier, which group 1 reaches only when its epilogue is done.
+      // bf16 output through LDS: each lane rounds its runs of 8 columns (scaled) to bf16 and writes them to LDS as
+      // 16 bytes, one 32 x 128 block (an mi tile row) of the wave at a time; each lane then reads back 16 bytes of
+      // one row, adds the bias (a second rounding, as the reference) and stores them, 16 lanes to a 256-byte row
+      // segment of C. A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free
+      // both ways). Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. The next item's
+      // prologue loads go to A stages 0, 1 and B stage 0; the first loads into A stage 2 and B stage 1 come after the
+      // next item's first barrier, which group 1 reaches only when its epilogue is done.
       GPIC_LDS uint8_t *cst =
           (GPIC_LDS uint8_t *)smem + (group == 0 ? a_half(2) : b_half(1)) + (wave & 3) * kCStageBytes;
       const __amdgpu_buffer_rsrc_t rC =
           __builtin_amdgcn_make_buffer_rsrc((void *)(C + (int64_t)cur.m0 * ldc), 0, rows_c * (int)ldc * 2, kBufferFlags);
-      const int wr = el & 31, wh = el >> 5;
-      const int rr = el >> 3, rc = el & 7;
-      u32x2 bw[kTN / 2][2] = {};
-      if (bias) {
-#pragma unroll
-        for (int pair = 0; pair < kTN / 2; pair++) {
-          const int n = cur.n0 + wn * kWTN + pair * 64 + 8 * rc;
-          if (n < N) {
-            bw[pair][0] = *reinterpret_cast<const u32x2 *>(bias + n);
-            bw[pair][1] = *reinterpret_cast<const u32x2 *>(bias + n + 4);
-          }
-        }
+      const int rr = el >> 4, rc = el & 15;        // read-back: rows 4 j + rr, chunk rc
+      const int n = cur.n0 + wn * kWTN + 8 * rc;   // the read-back lane's 8 columns
+      uint32_t b[4] = {0, 0, 0, 0};
+      if (bias && n < N) {
+        const u32x2 b0 = *reinterpret_cast<const u32x2 *>(bias + n), b1 = *reinterpret_cast<const u32x2 *>(bias + n + 4);
+        b[0] = b0.x, b[1] = b0.y, b[2] = b1.x, b[3] = b1.y;
       }
 #pragma unroll
       for (int mi = 0; mi < kTM; mi++) {
 #pragma unroll
-        for (int pair = 0; pair < kTN / 2; pair++) {
+        for (int ni = 0; ni < kTN; ni++)
 #pragma unroll
-          for (int h = 0; h < 2; h++) {
-            const v16f &v = acc[2 * pair + h][mi];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-              *(GPIC_LDS f4a_t *)(cst + wr * 256 + 16 * ((8 * h + 2 * q + wh) ^ (wr & 15))) =
-                  f4a_t{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-          }
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            const int r = 8 * j + rr;
-            const f4a_t x0 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc) ^ (r & 15)));
-            const f4a_t x1 = *(const GPIC_LDS f4a_t *)(cst + r * 256 + 16 * ((2 * rc + 1) ^ (r & 15)));
-            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          for (int hh = 0; hh < 2; hh++) {
+            const v16f &v = acc[ni][mi];
             st16_t w;
 #pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = pack_bf16(x[2 * e] * s, x[2 * e + 1] * s);
-            if (bias) {   // bf16(bf16(acc * s) + bias): the output is rounded, then the bias add is rounded again
-              const uint32_t b[4] = {bw[pair][0].x, bw[pair][0].y, bw[pair][1].x, bw[pair][1].y};
-#pragma unroll
-              for (int e = 0; e < 4; e++)
-                w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
-            }
-            const int rl = wm * kWTM + mi * 32 + r;   // row within the tile
-            const int n = cur.n0 + wn * kWTN + pair * 64 + 8 * rc;
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), rC,
-                                                   rl < rows_c && n < N ? (rl * (int)ldc + n) * 2 : kOOB, 0, 0);
+            for (int e = 0; e < 4; e++)
+              w[e] = pack_bf16(acc_read(v[8 * hh + 2 * e]) * s, acc_read(v[8 * hh + 2 * e + 1]) * s);
+            *(GPIC_LDS st16_t *)(cst + wr * 256 + 16 * ((4 * ni + 2 * hh + wh) ^ (wr & 15))) = w;
           }
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int r = 4 * j + rr;
+          st16_t w = *(const GPIC_LDS st16_t *)(cst + r * 256 + 16 * (rc ^ (r & 15)));
+          if (bias) {   // bf16(bf16(acc * s) + bias)
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
+          }
+          const int rl = wm * kWTM + mi * 32 + r;   // row within the tile
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), rC,
+                                                 rl < rows_c && n < N ? (rl * (int)ldc + n) * 2 : kOOB, 0, 0);
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
       }
       pend = kStoresBF16;
     }
