@@ -13,8 +13,10 @@
  *   - `stream` is a hipStream_t (void * here so this header needs no HIP headers). Work is enqueued on it; nothing
  *     synchronises with the host, nothing is allocated, and scales stay on the device.
  *   - `ws` is a caller-provided device workspace of at least the size the matching *_workspace_bytes() returns,
- *     16-byte aligned. The cast entry points keep no state in it between calls (it never needs zeroing); two calls
- *     that may run concurrently (different streams) need different workspaces.
+ *     16-byte aligned. The cast workspace is zeroed once when it is created and then kept for the cast calls: the
+ *     single-pass casts tag their partial maxima with a call number, and a stale word from an earlier call never
+ *     matches a later one; nothing else carries over between calls. Two calls that may run concurrently (different
+ *     streams) need different workspaces.
  *   - Tensor data pointers are 16-byte aligned; leading dimensions are in elements.
  *   - Return value: 0 on success, a negative GPIC_E* code for invalid arguments (nothing was launched), or a positive
  *     hipError_t from the launch.
@@ -43,8 +45,17 @@ extern "C" {
 const char *gpic_fp8_version(void);
 const char *gpic_fp8_status_string(int status);
 
-/* Bytes of workspace the cast entry points need (the partial maxima of the amax pass). */
+/* Bytes of workspace the cast entry points need (the partial maxima of the amax pass, the SwiGLU sigmoid table and
+ * the single-pass casts' tagged partials). */
 size_t gpic_fp8_cast_workspace_bytes(void);
+
+/* Tuning and test knob (process-wide, not synchronised with calls in flight; no counterpart in the reference, whose
+ * casts are always two Triton launches). gpic_fp8_tcast and gpic_fp8_tcast_t cast a bf16 (or, flat, fp32) tensor
+ * that fits in the chip's registers in one launch (x read once) and larger ones in two (amax pass, then cast pass).
+ * enabled = 0 forces the two-pass path; wait_us bounds how long a workgroup of the single pass waits for another's
+ * partial maximum before computing it from x itself (< 0: the default, 200 us; 0 makes every missing partial a direct
+ * computation, which tests use to exercise that path). The results are the same bytes either way. */
+void gpic_fp8_set_single_pass(int enabled, int wait_us);
 
 /*
  * Tensorwise current-amax cast to e4m3fn.

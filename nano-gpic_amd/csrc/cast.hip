@@ -7,6 +7,9 @@
 //   2. a cast pass: each workgroup folds all partials (<= kMaxParts words, served from L2), derives the scale with
 //      IEEE division and streams its share: 128-bit loads, 128-bit e4m3 stores.
 // Workgroup 0 of pass 2 writes the dequantization scale.
+#include <algorithm>
+#include <atomic>
+
 #include "gpic_device.h"
 #include "gpic_launch.h"
 
@@ -506,6 +509,75 @@ static void launch_cast_t(Src src, int64_t rows, int64_t cols, int nparts, uint8
   cast_t_kernel<Src><<<grid, 256, 0, st>>>(src, rows, cols, partial, nparts, q, ldq, qt, ldt, dequant);
 }
 
+// A 128 x 128 bf16 tile (rows r0.., columns c0..) as thread tid's 8 raw chunks: chunk i is row id / 16, columns
+// 8 (id % 16) .. + 7 of the tile, id = tid + 256 i; zero outside x.
+constexpr int kTPitch = kTT / 4 + 1;            // words per LDS row of the e4m3 tile (one word of padding)
+constexpr int kTPer = kTT * (kTT / 8) / 256;    // 8-element chunks per thread per tile: 8
+__device__ __forceinline__ void load_tile_bf16(const uint16_t *__restrict__ x, int64_t ld, int64_t rows, int64_t cols,
+                                               int64_t r0, int64_t c0, u32x4 (&R)[kTPer]) {
+#pragma unroll
+  for (int i = 0; i < kTPer; i++) {
+    const int id = threadIdx.x + 256 * i;
+    const int64_t gr = r0 + (id >> 4), gc = c0 + 8 * (id & 15);
+    R[i] = gr < rows && gc < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + gr * ld + gc))
+                                  : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// The tile held in R (as load_tile_bf16 left it) as e4m3 bytes with `scale`: 8 bytes per chunk.
+__device__ __forceinline__ void cvt_tile_bf16(const u32x4 (&R)[kTPer], float scale, u32x2 (&E)[kTPer]) {
+#pragma unroll
+  for (int i = 0; i < kTPer; i++) {
+    float v[8];
+    unpack8(R[i], v);
+    E[i].x = e4m3x4(sat(v[0] * scale), sat(v[1] * scale), sat(v[2] * scale), sat(v[3] * scale));
+    E[i].y = e4m3x4(sat(v[4] * scale), sat(v[5] * scale), sat(v[6] * scale), sat(v[7] * scale));
+  }
+}
+
+// Stores a tile's e4m3 bytes E (from cvt_tile_bf16): q rows from registers, qt through the LDS buffer `tile`
+// ([row][col / 4] e4m3 words), which is free again when this returns. Same bytes as cast_t_kernel.
+__device__ __forceinline__ void emit_tile(const u32x2 (&E)[kTPer], int64_t r0, int64_t c0, int64_t rows, int64_t cols,
+                                          uint8_t *__restrict__ q, int64_t ldq, uint8_t *__restrict__ qt, int64_t ldt,
+                                          uint32_t *tile) {
+#pragma unroll
+  for (int i = 0; i < kTPer; i++) {
+    const int id = threadIdx.x + 256 * i;
+    const int r = id >> 4, cc = id & 15;
+    const int64_t gr = r0 + r, gc = c0 + 8 * cc;
+    if (q && gr < rows && gc < cols) *reinterpret_cast<u32x2 *>(q + gr * ldq + gc) = E[i];
+    tile[r * kTPitch + 2 * cc] = E[i].x;
+    tile[r * kTPitch + 2 * cc + 1] = E[i].y;
+  }
+  lds_barrier();
+  // qt rows c0 + 4k .. c0 + 4k + 3 get bytes r0 + 16p .. r0 + 16p + 15 of their columns, k = tid / 8, p = tid % 8
+  // (as in cast_t_kernel)
+  {
+    const int k = threadIdx.x >> 3, p = threadIdx.x & 7;
+    u32x4 out[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const uint32_t *w = tile + (16 * p + 4 * g) * kTPitch + k;
+      const uint32_t w0 = w[0], w1 = w[kTPitch], w2 = w[2 * kTPitch], w3 = w[3 * kTPitch];
+      const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+      out[0][g] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+      out[1][g] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+      out[2][g] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+      out[3][g] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+    }
+    const int64_t gr = r0 + 16 * p;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int64_t gc = c0 + 4 * k + j;
+      if (gc < cols && gr < ldt) *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = out[j];
+    }
+  }
+  lds_barrier();   // the tile buffer is rewritten by the next tile
+}
+
 // The transposing cast of a bf16 source, persistent: each workgroup folds the partial maxima once, then walks its
 // tiles, loading the next tile's bf16 (kept raw: 32 VGPRs) while it casts, transposes and stores the current one.
 // Same tile layout and bytes as cast_t_kernel.
@@ -513,80 +585,28 @@ __global__ __launch_bounds__(256) void cast_t_bf16_kernel(const uint16_t *__rest
                                                           int64_t cols, const uint32_t *__restrict__ partial, int nparts,
                                                           uint8_t *__restrict__ q, int64_t ldq, uint8_t *__restrict__ qt,
                                                           int64_t ldt, float *__restrict__ dequant) {
-  constexpr int kPitch = kTT / 4 + 1;          // words per LDS row (one word of padding)
-  __shared__ uint32_t tile[kTT * kPitch];      // [row][col / 4] e4m3 bytes
-  constexpr int kPer = kTT * (kTT / 8) / 256;  // 8-element chunks per thread per tile: 8
+  __shared__ uint32_t tile[kTT * kTPitch];
   const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
-  // chunk i of a thread: row id / 16, columns 8 (id % 16) .. + 7 of the tile, id = tid + 256 i; zero outside x
-  auto load_raw = [&](int64_t t, u32x4 (&R)[kPer]) {
-    const int64_t c0 = (t % tiles_c) * kTT, r0 = (t / tiles_c) * kTT;
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const int id = threadIdx.x + 256 * i;
-      const int64_t gr = r0 + (id >> 4), gc = c0 + 8 * (id & 15);
-      R[i] = gr < rows && gc < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + gr * ld + gc))
-                                    : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
   int64_t t = blockIdx.x;   // < tiles: the grid never exceeds the tile count
-  u32x4 R[kPer];
-  load_raw(t, R);
+  u32x4 R[kTPer];
+  load_tile_bf16(x, ld, rows, cols, (t / tiles_c) * kTT, (t % tiles_c) * kTT, R);
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);   // its barriers wait for LDS only
   if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
   for (; t < tiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
-    u32x4 Rn[kPer];
+    u32x4 Rn[kTPer];
     if (tn < tiles) {
-      load_raw(tn, Rn);
+      load_tile_bf16(x, ld, rows, cols, (tn / tiles_c) * kTT, (tn % tiles_c) * kTT, Rn);
     } else {
 #pragma unroll
-      for (int i = 0; i < kPer; i++) Rn[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < kTPer; i++) Rn[i] = u32x4{0u, 0u, 0u, 0u};
     }
-    const int64_t c0 = (t % tiles_c) * kTT, r0 = (t / tiles_c) * kTT;
+    u32x2 E[kTPer];
+    cvt_tile_bf16(R, scale, E);
+    emit_tile(E, (t / tiles_c) * kTT, (t % tiles_c) * kTT, rows, cols, q, ldq, qt, ldt, tile);
 #pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const int id = threadIdx.x + 256 * i;
-      const int r = id >> 4, cc = id & 15;
-      const int64_t gr = r0 + r, gc = c0 + 8 * cc;
-      float v[8];
-      unpack8(R[i], v);
-      u32x2 o;
-      o.x = e4m3x4(sat(v[0] * scale), sat(v[1] * scale), sat(v[2] * scale), sat(v[3] * scale));
-      o.y = e4m3x4(sat(v[4] * scale), sat(v[5] * scale), sat(v[6] * scale), sat(v[7] * scale));
-      if (q && gr < rows && gc < cols) *reinterpret_cast<u32x2 *>(q + gr * ldq + gc) = o;
-      tile[r * kPitch + 2 * cc] = o.x;
-      tile[r * kPitch + 2 * cc + 1] = o.y;
-    }
-    lds_barrier();
-    // qt rows c0 + 4k .. c0 + 4k + 3 get bytes r0 + 16p .. r0 + 16p + 15 of their columns, k = tid / 8, p = tid % 8
-    // (as in cast_t_kernel)
-    {
-      const int k = threadIdx.x >> 3, p = threadIdx.x & 7;
-      u32x4 out[4];
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const uint32_t *w = tile + (16 * p + 4 * g) * kPitch + k;
-        const uint32_t w0 = w[0], w1 = w[kPitch], w2 = w[2 * kPitch], w3 = w[3 * kPitch];
-        const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
-        out[0][g] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-        out[1][g] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-        out[2][g] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-        out[3][g] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-      }
-      const int64_t gr = r0 + 16 * p;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int64_t gc = c0 + 4 * k + j;
-        if (gc < cols && gr < ldt) *reinterpret_cast<u32x4 *>(qt + gc * ldt + gr) = out[j];
-      }
-    }
-    lds_barrier();   // the tile buffer is rewritten by the next tile
-#pragma unroll
-    for (int i = 0; i < kPer; i++) R[i] = Rn[i];
+    for (int i = 0; i < kTPer; i++) R[i] = Rn[i];
   }
 }
 
@@ -605,6 +625,277 @@ static void launch_cast_t(SrcBF16 src, int64_t rows, int64_t cols, int nparts, u
 }
 
 
+// ------------------------------------------------------------------------------------------- single pass
+//
+// A tensor that fits in the registers of the whole chip is cast in one launch: each workgroup loads its share into
+// registers, reduces it to a partial maximum and publishes it, takes the maximum of all workgroups' partials, and
+// casts from its registers. x is read once: 3 B/elem moved for bf16 instead of 5.
+//
+// Partials: one 64-bit word per workgroup, (call tag << 32) | amax bits, in the workspace. The tag is a host-side call
+// counter passed to the kernel, so a word left by any earlier call (or by a late workgroup of one) never matches; the
+// workspace is zeroed once, when it is created, and tag 0 is never used.
+// No workgroup waits on another without a bound: a partial that has not appeared within the wait bound (kOnceWaitUs by
+// default, about 8x a whole call) is computed by the waiting workgroup itself, from that workgroup's share of x. So
+// the launch needs no co-residency guarantee (a plain launch; the cooperative one costs ~17 us per call here), never
+// deadlocks when other work holds CUs, and the amax is exact either way. The workspace's fallback word counts such
+// direct computations (0 in normal runs).
+constexpr int kMaxOnceBlocks = 1024;
+constexpr size_t kOnceTagged = 28 * 1024;                         // uint64_t[kMaxOnceBlocks] tagged partials
+constexpr size_t kOnceFallback = kOnceTagged + 8 * kMaxOnceBlocks;  // uint32_t: partials computed by a waiter
+static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kOnceTagged, "two-pass scratch overlaps the single-pass words");
+static_assert(kOnceFallback + 4 <= kCastWorkspaceBytes, "cast workspace too small");
+template <typename T>
+constexpr int kOnceWords = sizeof(T) == 2 ? 16 : 12;   // 16-byte words a thread of the flat kernel holds (fp32: 12,
+                                                        // which its wider narrowing code needs to fit 128 VGPRs)
+constexpr int kOnceTiles = 2;       // 128 x 128 bf16 tiles a workgroup of the transposing kernel holds (64 VGPRs)
+constexpr int kOnceWaitUs = 200;
+
+// Marks held words as redefined here, so the compiler cannot hoist their conversion above the fold's wait (it would
+// widen all of them to fp32 at once and spill).
+template <int W>
+__device__ __forceinline__ void hold(u32x4 (&w)[W]) {
+#pragma unroll
+  for (int i = 0; i < W; i++) asm volatile("" : "+v"(w[i]));
+}
+
+// max |x| bits of one 16-byte word, NaN excluded (the rule of amax_kernel, element by element).
+template <typename T>
+__device__ __forceinline__ uint32_t word_amax_exact(u32x4 w) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t v = w[j];
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t a0 = (v & 0x7fffu) << 16, a1 = v & 0x7fff0000u;
+      if (a0 <= 0x7f800000u) m = max(m, a0);
+      if (a1 <= 0x7f800000u) m = max(m, a1);
+    } else {
+      const uint32_t a = v & 0x7fffffffu;
+      if (a <= 0x7f800000u) m = max(m, a);
+    }
+  }
+  return m;
+}
+
+// max |x| over a thread's words: packed maxima first; a thread that saw a NaN folds its words again exactly. Zero
+// words (outside x) change nothing.
+template <typename T, int W>
+__device__ __forceinline__ uint32_t words_amax(const u32x4 (&w)[W]) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < W; i++) m = word_max<T>(m, w[i]);
+  bool nan;
+  if constexpr (sizeof(T) == 2) {
+    m = max(m & 0xffffu, m >> 16);
+    nan = m > 0x7f80u;
+    m <<= 16;
+  } else {
+    nan = m > 0x7f800000u;
+  }
+  if (nan) {
+    m = 0;
+#pragma unroll
+    for (int i = 0; i < W; i++) m = max(m, word_amax_exact<T>(w[i]));
+  }
+  return m;
+}
+
+// Publishes this workgroup's maximum m (held by every thread) as call `tag`'s partial, then returns the maximum over
+// all G partials to every thread. share_max(c) must return (to every thread of the workgroup) workgroup c's maximum
+// computed from x; it runs only for a partial that did not appear within wait_ticks.
+template <class ShareMax>
+__device__ __forceinline__ uint32_t once_fold(uint32_t m, uint32_t tag, void *ws, uint32_t wait_ticks,
+                                              ShareMax share_max) {
+  __shared__ int missing[kMaxOnceBlocks];
+  __shared__ int nmissing;
+  uint64_t *tagged = reinterpret_cast<uint64_t *>((char *)ws + kOnceTagged);
+  const int G = gridDim.x;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(tagged + blockIdx.x, ((uint64_t)tag << 32) | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    nmissing = 0;
+  }
+  __syncthreads();
+  uint32_t g = m;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = threadIdx.x; i < G; i += blockDim.x) {
+    uint64_t w = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while ((uint32_t)(w >> 32) != tag && __builtin_amdgcn_s_memrealtime() - t0 < wait_ticks) {
+      __builtin_amdgcn_s_sleep(2);
+      w = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if ((uint32_t)(w >> 32) == tag) g = max(g, (uint32_t)w);
+    else missing[atomicAdd(&nmissing, 1)] = i;
+  }
+  g = block_max_u32(g);   // its barriers also publish `missing`
+  const int nm = nmissing;
+  if (nm > 0) {
+    for (int k = 0; k < nm; k++) g = max(g, share_max(missing[k]));
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)nm, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return g;
+}
+
+// Flat single-pass cast. x as nw 16-byte words (8 bf16 or 4 fp32 elements) plus `tail` (< 8 or < 4) elements;
+// workgroup b owns words [b P, (b + 1) P), P = 256 wpt, thread t words b P + 256 j + t, j < wpt <= kOnceWords<T>.
+template <typename T>
+__global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__ x, int64_t n, int wpt,
+                                                           uint8_t *__restrict__ q, float *__restrict__ dequant,
+                                                           void *ws, uint32_t tag, uint32_t wait_ticks) {
+  constexpr int kE = 16 / sizeof(T);   // elements per word
+  const int64_t nw = n / kE;
+  const int tail = (int)(n % kE);
+  const u32x4 *xv = reinterpret_cast<const u32x4 *>(x);
+  const int64_t P = 256 * (int64_t)wpt;
+  auto word = [&](int64_t b, int j) { return b * P + 256 * j + threadIdx.x; };
+  constexpr int kW = kOnceWords<T>;
+  u32x4 w[kW];
+#pragma unroll
+  for (int j = 0; j < kW; j++) {
+    const int64_t i = word(blockIdx.x, j);
+    w[j] = j < wpt && i < nw ? __builtin_nontemporal_load(xv + i) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // every workgroup folds the tail elements into its partial, so a partial computed from x includes them as well
+  auto tail_amax = [&]() {
+    uint32_t a = 0;
+    if (threadIdx.x < tail) {
+      const float v = sizeof(T) == 2 ? bf16_lo(reinterpret_cast<const uint16_t *>(x)[nw * kE + threadIdx.x])
+                                     : reinterpret_cast<const float *>(x)[nw * kE + threadIdx.x];
+      a = __float_as_uint(v) & 0x7fffffffu;
+      a = a <= 0x7f800000u ? a : 0u;
+    }
+    return a;
+  };
+  const uint32_t m = block_max_u32(max(words_amax<T, kW>(w), tail_amax()));
+  const uint32_t g = once_fold(m, tag, ws, wait_ticks, [&](int c) {
+    uint32_t a = tail_amax();
+    for (int j = 0; j < wpt; j++) {
+      const int64_t i = word(c, j);
+      if (i < nw) a = max(a, word_amax_exact<T>(__builtin_nontemporal_load(xv + i)));
+    }
+    return block_max_u32(a);
+  });
+  hold(w);
+  float scale, deq;
+  scales_from_amax(g, scale, deq);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+#pragma unroll
+  for (int j = 0; j < kW; j++) {
+    const int64_t i = word(blockIdx.x, j);
+    if (j < wpt && i < nw) {
+      if constexpr (sizeof(T) == 2) __builtin_nontemporal_store(cast8_bf16(w[j], scale), reinterpret_cast<u32x2 *>(q) + i);
+      else __builtin_nontemporal_store(cast4_f32(w[j], scale), reinterpret_cast<uint32_t *>(q) + i);
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x < tail) {
+    const int64_t i = nw * kE + threadIdx.x;
+    const float v = sizeof(T) == 2 ? bf16_lo(reinterpret_cast<const uint16_t *>(x)[i]) : reinterpret_cast<const float *>(x)[i];
+    q[i] = (uint8_t)e4m3x4(sat(v * scale), 0.f, 0.f, 0.f);
+  }
+}
+
+// Transposing single-pass cast of a bf16 source: workgroup b holds tiles b and b + G (when there is one).
+__global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows,
+                                                             int64_t cols, uint8_t *__restrict__ q, int64_t ldq,
+                                                             uint8_t *__restrict__ qt, int64_t ldt,
+                                                             float *__restrict__ dequant, void *ws, uint32_t tag,
+                                                             uint32_t wait_ticks) {
+  static_assert(kOnceTiles == 2, "two tiles per workgroup");
+  __shared__ uint32_t tile[kTT * kTPitch];
+  const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
+  const int64_t t0 = blockIdx.x, t1 = blockIdx.x + gridDim.x;   // t0 < tiles: the grid never exceeds the tile count
+  u32x4 R[2 * kTPer];
+  u32x4(&R0)[kTPer] = *reinterpret_cast<u32x4(*)[kTPer]>(R);
+  u32x4(&R1)[kTPer] = *reinterpret_cast<u32x4(*)[kTPer]>(R + kTPer);
+  load_tile_bf16(x, ld, rows, cols, (t0 / tiles_c) * kTT, (t0 % tiles_c) * kTT, R0);
+  if (t1 < tiles) {
+    load_tile_bf16(x, ld, rows, cols, (t1 / tiles_c) * kTT, (t1 % tiles_c) * kTT, R1);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kTPer; i++) R1[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  const uint32_t m = block_max_u32(words_amax<uint16_t, 2 * kTPer>(R));
+  const uint32_t g = once_fold(m, tag, ws, wait_ticks, [&](int c) {
+    uint32_t a = 0;
+    for (int64_t t = c; t < tiles && t < c + 2 * (int64_t)gridDim.x; t += gridDim.x) {
+      const int64_t r0 = (t / tiles_c) * kTT, c0 = (t % tiles_c) * kTT;
+      for (int i = 0; i < kTPer; i++) {
+        const int id = threadIdx.x + 256 * i;
+        const int64_t gr = r0 + (id >> 4), gc = c0 + 8 * (id & 15);
+        if (gr < rows && gc < cols) a = max(a, word_amax_exact<uint16_t>(*reinterpret_cast<const u32x4 *>(x + gr * ld + gc)));
+      }
+    }
+    return block_max_u32(a);
+  });
+  hold(R);
+  float scale, deq;
+  scales_from_amax(g, scale, deq);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  u32x2 E0[kTPer], E1[kTPer];   // both tiles narrowed first: 32 VGPRs live instead of 64
+  cvt_tile_bf16(R0, scale, E0);
+  cvt_tile_bf16(R1, scale, E1);
+  emit_tile(E0, (t0 / tiles_c) * kTT, (t0 % tiles_c) * kTT, rows, cols, q, ldq, qt, ldt, tile);
+  if (t1 < tiles) emit_tile(E1, (t1 / tiles_c) * kTT, (t1 % tiles_c) * kTT, rows, cols, q, ldq, qt, ldt, tile);
+}
+
+// Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and
+// the wait bound in microseconds.
+static int g_once_enabled = 1;
+static int g_once_wait_us = kOnceWaitUs;
+static std::atomic<uint32_t> g_once_calls{0};
+
+static uint32_t once_next_tag() {
+  uint32_t t = ++g_once_calls;
+  while (t == 0) t = ++g_once_calls;   // 0 is the zeroed workspace's tag
+  return t;
+}
+
+// Workgroups of `kernel` (256 threads) that the device holds at once; computed once per kernel (`cache`).
+static int once_capacity(const void *kernel, int *cache) {
+  if (*cache < 0) {
+    int dev = 0, per = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess)
+      per = 0;
+    (void)hipGetLastError();
+    *cache = std::min(per * cus, kMaxOnceBlocks);
+  }
+  return *cache;
+}
+
+// s_memrealtime counts at 100 MHz on this target
+static uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us) * 100u; }
+
+// The single-pass flat cast when x fits (false, nothing launched, when it does not).
+template <typename T>
+static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant, void *ws, hipStream_t st) {
+  static int cache = -1;
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T>), &cache);
+  constexpr int kE = 16 / sizeof(T);
+  const int64_t nw = n / kE;
+  if (!g_once_enabled || cap <= 0 || n <= 0 || nw > (int64_t)kOnceWords<T> * 256 * cap) return false;
+  const int64_t groups = std::max<int64_t>(1, (nw + 255) / 256);   // 256-word groups
+  const int grid = (int)std::min<int64_t>(groups, cap);
+  const int wpt = (int)((groups + grid - 1) / grid);
+  cast_once_kernel<T><<<grid, 256, 0, st>>>(x, n, wpt, q, dequant, ws, once_next_tag(), once_wait_ticks());
+  return true;
+}
+
+// The single-pass transposing cast of a bf16 source when it fits (false, nothing launched, otherwise).
+static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,
+                                float *dequant, void *ws, hipStream_t st) {
+  static int cache = -1;
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), &cache);
+  const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
+  if (!g_once_enabled || cap <= 0 || tiles <= 0 || tiles > (int64_t)kOnceTiles * cap) return false;
+  const int grid = (int)std::min<int64_t>(tiles, cap);
+  cast_t_once_kernel<<<grid, 256, 0, st>>>(x, cols, rows, cols, q, cols, qt, ldt, dequant, ws, once_next_tag(),
+                                           once_wait_ticks());
+  return true;
+}
+
 // SwiGLU kernels: rows strided over at most kSwigluBlocks workgroups (each builds its 24 KiB sigmoid table once).
 static inline int swiglu_grid(int64_t M) { return (int)(M < 1 ? 1 : (M > kSwigluBlocks ? kSwigluBlocks : M)); }
 
@@ -616,14 +907,25 @@ extern "C" {
 
 size_t gpic_fp8_cast_workspace_bytes(void) { return kCastWorkspaceBytes; }
 
+void gpic_fp8_set_single_pass(int enabled, int wait_us) {
+  g_once_enabled = enabled != 0;
+  g_once_wait_us = wait_us < 0 ? kOnceWaitUs : wait_us;
+}
+
 int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *ws, void *stream) {
   if (n < 0 || !dequant || !ws || (n > 0 && (!x || !q))) return GPIC_EINVAL;
   if (dtype != GPIC_DTYPE_BF16 && dtype != GPIC_DTYPE_F32) return GPIC_EDTYPE;
   if (!aligned16(x) || !aligned16(q) || !aligned16(ws)) return GPIC_EALIGN;
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
-  if (dtype == GPIC_DTYPE_BF16) return launch_tcast(static_cast<const uint16_t *>(x), n, q, dequant, partial, st);
-  return launch_tcast(static_cast<const float *>(x), n, q, dequant, partial, st);
+  if (dtype == GPIC_DTYPE_BF16) {
+    const uint16_t *xb = static_cast<const uint16_t *>(x);
+    if (launch_tcast_once(xb, n, q, dequant, ws, st)) return (int)hipGetLastError();
+    return launch_tcast(xb, n, q, dequant, partial, st);
+  }
+  const float *xf = static_cast<const float *>(x);
+  if (launch_tcast_once(xf, n, q, dequant, ws, st)) return (int)hipGetLastError();
+  return launch_tcast(xf, n, q, dequant, partial, st);
 }
 
 int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,
@@ -635,6 +937,9 @@ int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8
   if (!aligned16(x) || (q && !aligned16(q)) || !aligned16(qt) || !aligned16(ws)) return GPIC_EALIGN;
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
+  if (dtype == GPIC_DTYPE_BF16 && rows > 0 && cols > 0 &&
+      launch_tcast_t_once(static_cast<const uint16_t *>(x), rows, cols, q, qt, ldt, dequant, ws, st))
+    return (int)hipGetLastError();
   const int64_t n = rows * cols;
   const int ga = grid_for((n / 16 + kUnroll - 1) / kUnroll, kAmaxBlocks);
   if (dtype == GPIC_DTYPE_BF16)

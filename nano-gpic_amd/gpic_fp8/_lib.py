@@ -22,6 +22,7 @@ SIGNATURES = {
     "gpic_fp8_version": (ctypes.c_char_p, []),
     "gpic_fp8_status_string": (ctypes.c_char_p, [_int]),
     "gpic_fp8_cast_workspace_bytes": (_sz, []),
+    "gpic_fp8_set_single_pass": (None, [_int, _int]),
     "gpic_fp8_tcast": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _vp]),
     "gpic_fp8_tcast_t": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_swiglu_tcast": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
@@ -78,7 +79,23 @@ def aligned(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+_WORKSPACES = {}
+
+
+def set_single_pass(enabled=True, wait_us=-1):
+    """Single-pass casts on (default) or off, and the wait bound in microseconds (-1: the library default); see
+    gpic_fp8_set_single_pass in include/gpic_fp8.h. The output bytes do not depend on either."""
+    lib().gpic_fp8_set_single_pass(int(bool(enabled)), int(wait_us))
+
+
 def cast_workspace(device):
-    """Scratch for the partial maxima of one cast (stateless between calls: no zeroing needed)."""
-    n = lib().gpic_fp8_cast_workspace_bytes()
-    return torch.empty(n // 4, dtype=torch.int32, device=device)
+    """The cast workspace of `device`'s current stream: partial maxima, the SwiGLU sigmoid table and the single-pass
+    casts' call counter. Created zeroed once per (device, stream) and kept: the counter must survive between calls,
+    and casts on different streams, which may overlap, get different workspaces."""
+    device = torch.device(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_ptr(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        n = lib().gpic_fp8_cast_workspace_bytes()
+        ws = _WORKSPACES[key] = torch.zeros(n // 4, dtype=torch.int32, device=device)
+    return ws

@@ -14,7 +14,7 @@ HEADER = os.path.join(ROOT, "include", "gpic_fp8.h")
 
 def declared():
     src = open(HEADER).read()
-    return set(re.findall(r"^(?:int|size_t|const char \*)\s*(gpic_fp8_\w+)\(", src, flags=re.M))
+    return set(re.findall(r"^(?:int|void|size_t|const char \*)\s*(gpic_fp8_\w+)\(", src, flags=re.M))
 
 
 def test_header_declares_the_bound_functions():

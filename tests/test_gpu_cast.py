@@ -7,6 +7,7 @@ import pytest
 import torch
 
 import gpic_fp8 as G
+from gpic_fp8 import _lib as L
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -168,3 +169,129 @@ def test_other_float_dtypes_widen(dev):
     q, s = G.tcast(x)
     q2, s2 = G.tcast(x.float())
     assert s.item() == s2.item() and torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+
+
+# The single-pass casts write their tagged partial maxima from byte 28672 of the cast workspace (one 64-bit word per
+# workgroup, the call tag in the high half) and count partials a workgroup had to compute from x itself at byte 36864
+# (cast.hip: kOnceTagged, kOnceFallback).
+ONCE_WORD0, ONCE_FALLBACK = 28672 // 8, 36864 // 4
+
+
+def once_state(dev):
+    ws = L.cast_workspace(dev)
+    torch.cuda.synchronize()
+    return int(ws.view(torch.int64)[ONCE_WORD0].item()), int(ws[ONCE_FALLBACK].item())
+
+
+@pytest.fixture
+def single_pass_default():
+    L.set_single_pass(True, -1)
+    yield
+    L.set_single_pass(True, -1)
+
+
+def test_single_pass_taken_when_the_tensor_fits(dev, single_pass_default):
+    """Config 2 ([32768 x 1024] bf16) fits the single-pass kernels (64 MiB held in registers): the flat and the
+    transposing cast each write new tagged partials and match the oracle; a tensor of 3x the size takes the two-pass
+    path (the partial words unchanged) with the oracle's bytes. No partial had to be computed from x."""
+    x = config2_input()
+    xh = bits(x)
+    oq, od, _ = O.tcast(xh)
+    xd = x.to(dev)
+    w0, f0 = once_state(dev)
+    q, s = G.tcast(xd)
+    w1, _ = once_state(dev)
+    assert w1 >> 32 != w0 >> 32
+    assert s.item() == od and np.array_equal(qb(q), oq)
+    q, qt, s = G.tcast_t(xd)
+    w2, f2 = once_state(dev)
+    assert w2 >> 32 != w1 >> 32 and f2 == f0
+    assert s.item() == od and np.array_equal(qb(q), oq)
+    assert torch.equal(qt.view(torch.uint8), q.view(torch.uint8).t())
+    big = torch.cat([xd, xd * 2, xd * 0.5], dim=1)
+    q, s = G.tcast(big)
+    w3, f3 = once_state(dev)
+    assert w3 == w2 and f3 == f0
+    oq, od, _ = O.tcast(bits(big.cpu()))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_single_pass_direct_fallback_and_two_pass_agree(dev, single_pass_default):
+    """The same tensors through the single pass with its normal wait, with a zero wait (every partial not yet
+    published is computed by the waiting workgroup from x: the path that keeps the single pass exact when other work
+    holds CUs) and through the forced two-pass path: identical bytes and scales, equal to the oracle's."""
+    g = torch.Generator(device=dev).manual_seed(3)
+    cases = [(torch.randn(4096, 1024, generator=g, device=dev) * 3).to(torch.bfloat16),
+             (torch.randn(777, 4096, generator=g, device=dev) / 64),                      # fp32 weight
+             (torch.randn(1_000_003, generator=g, device=dev)).to(torch.bfloat16)]         # flat with a tail
+    cases[0][17, 5] = float("nan")
+    cases[2][999_999] = -88.0
+    for x in cases:
+        xn = bits(x.cpu()) if x.dtype == torch.bfloat16 else x.cpu().numpy()
+        oq, od, _ = O.tcast(xn)
+        outs = []
+        for enabled, wait in ((True, -1), (True, 0), (False, -1)):
+            L.set_single_pass(enabled, wait)
+            _, f0 = once_state(dev)
+            q, s = G.tcast(x)
+            _, f1 = once_state(dev)
+            if enabled and wait == 0:
+                assert f1 > f0          # the direct computation did run
+            outs.append((qb(q), s.item()))
+            if x.dim() == 2 and x.dtype == torch.bfloat16:
+                q2, qt2, s2 = G.tcast_t(x)
+                assert np.array_equal(qb(q2), qb(q)) and s2.item() == s.item()
+                assert torch.equal(qt2.view(torch.uint8)[:, :x.shape[0]], q2.view(torch.uint8).t())
+        L.set_single_pass(True, -1)
+        for q, s in outs:
+            assert s == od and np.array_equal(q, oq)
+
+
+@pytest.mark.parametrize("n", [41_000_007, 1_000_003])
+def test_nan_inf_tail_both_paths(dev, n):
+    """NaNs (ignored by the amax), an odd tail (n % 16 != 0) and a planted maximum, on a flat bf16 tensor above the
+    single-pass capacity (two passes) and one below it (single pass): bytes and scale equal the oracle's."""
+    g = torch.Generator(device=dev).manual_seed(n)
+    x = (torch.randn(n, generator=g, device=dev) * 3).to(torch.bfloat16)
+    x[::1_000_001] = float("nan")
+    x[n // 3] = -float("nan")
+    x[n - 2] = 977.0                       # the maximum sits in the tail
+    q, s = G.tcast(x)
+    oq, od, _ = O.tcast(bits(x))
+    assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_fp32_weight_both_paths(dev):
+    """fp32 (DDP) weights: [2048 x 4096] fits the single-pass fp32 kernel, [5000 x 4096] does not."""
+    for rows in (2048, 5000):
+        w = torch.randn(rows, 4096, device=dev) / 64
+        w[rows // 2, 7] = -3.5
+        q, s = G.tcast(w)
+        oq, od, _ = O.tcast(w.cpu().numpy())
+        assert s.item() == od and np.array_equal(qb(q), oq)
+
+
+def test_single_pass_back_to_back_calls(dev):
+    """Forty stream-ordered calls with no host synchronisation between them, alternating single-pass tensors of
+    different amax with two-pass ones on the same workspace: each result is checked afterwards against the first by
+    the power-of-two scale invariance (same bytes, dequant scale times 2^k)."""
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = (torch.randn(4096, 1024, generator=g, device=dev) * 2).to(torch.bfloat16)
+    y = (torch.randn(6000, 8192, generator=g, device=dev)).to(torch.bfloat16)   # 49M elements: two passes
+    outs = []
+    for i in range(40):
+        k = i % 5 - 2
+        if i % 4 == 3:
+            outs.append(("y", G.tcast(y)))
+        else:
+            outs.append((k, G.tcast_t(x * 2.0 ** k)))
+    q0, qt0, s0 = G.tcast_t(x)
+    qy, sy = G.tcast(y)
+    for k, out in outs:
+        if k == "y":
+            assert torch.equal(out[0].view(torch.uint8), qy.view(torch.uint8)) and out[1].item() == sy.item()
+        else:
+            q, qt, s = out
+            assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
+            assert torch.equal(qt.view(torch.uint8), qt0.view(torch.uint8))
+            assert s.item() == s0.item() * 2.0 ** k
