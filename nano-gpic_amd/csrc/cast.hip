@@ -446,42 +446,55 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_cast_kernel(const uint16_
 
 // dz = [d1 | d2] (fp8_native.py:88-96), each operation rounded on its own, left to right:
 //   sg = sigmoid(z1); sl = bf16(z1 * sg); d1 = bf16((da * z2) * (sg * (1 + z1 * (1 - sg)))); d2 = bf16(da * sl)
-// dz = [dz1 | dz2] and the partial maxima of its bf16 values.
+// for the 8 elements of one 16-byte word of z1, z2 and da: h1, h2 are the bf16 words of d1 and d2.
+__device__ __forceinline__ void dz_words(const float *lut, u32x4 z1v, u32x4 z2v, u32x4 dav, u32x4 &h1, u32x4 &h2) {
+  float z1[8], z2[8], dv[8], sg[8];
+  unpack8(z1v, z1);
+  unpack8(z2v, z2);
+  unpack8(dav, dv);
+  sigmoid8(lut, z1v, z1, sg);
+  float d1[8], d2[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    d1[i] = dz1_of(z1[i], z2[i], dv[i], sg[i]);
+    d2[i] = dz2_of(z1[i], dv[i], sg[i]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    h1[j] = pack_bf16(d1[2 * j], d1[2 * j + 1]);
+    h2[j] = pack_bf16(d2[2 * j], d2[2 * j + 1]);
+  }
+}
+
+// dz = [dz1 | dz2] (written when dz is given) and the partial maxima of its bf16 values; workgroup 0 also publishes
+// its sigmoid table to `table` (when given) for a later pass of the same call.
 __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t *__restrict__ z,
                                                                    const uint16_t *__restrict__ da, int64_t M, int64_t H,
                                                                    int64_t sz, int64_t sda, uint16_t *__restrict__ dz,
-                                                                   int64_t sdz, uint32_t *__restrict__ partial) {
+                                                                   int64_t sdz, uint32_t *__restrict__ partial,
+                                                                   float *__restrict__ table) {
   __shared__ float lut[kLutSize];
   lut_build(lut);
+  if (blockIdx.x == 0 && table)
+    for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) table[i] = lut[i];
   const int64_t units = H / 8;
   uint32_t m = 0;
   for (int64_t r = blockIdx.x; r < M; r += gridDim.x) {
     const uint16_t *zr = z + r * sz;
     for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
-      const u32x4 z1v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u));
-      const u32x4 z2v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
-      const u32x4 dav = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + r * sda + 8 * u));
-      float z1[8], z2[8], dv[8], sg[8];
-      unpack8(z1v, z1);
-      unpack8(z2v, z2);
-      unpack8(dav, dv);
-      sigmoid8(lut, z1v, z1, sg);
-      float d1[8], d2[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        d1[i] = dz1_of(z1[i], z2[i], dv[i], sg[i]);
-        d2[i] = dz2_of(z1[i], dv[i], sg[i]);
-      }
       u32x4 h1, h2;
+      dz_words(lut, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u)),
+               __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u)),
+               __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + r * sda + 8 * u)), h1, h2);
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        h1[j] = pack_bf16(d1[2 * j], d1[2 * j + 1]);
-        h2[j] = pack_bf16(d2[2 * j], d2[2 * j + 1]);
         m = max(m, max(absbits_nonan(bf16_lo(h1[j])), absbits_nonan(bf16_hi(h1[j]))));
         m = max(m, max(absbits_nonan(bf16_lo(h2[j])), absbits_nonan(bf16_hi(h2[j]))));
       }
-      *reinterpret_cast<u32x4 *>(dz + r * sdz + 8 * u) = h1;
-      *reinterpret_cast<u32x4 *>(dz + r * sdz + H + 8 * u) = h2;
+      if (dz) {
+        *reinterpret_cast<u32x4 *>(dz + r * sdz + 8 * u) = h1;
+        *reinterpret_cast<u32x4 *>(dz + r * sdz + H + 8 * u) = h2;
+      }
     }
   }
   m = block_max_u32(m);
@@ -623,6 +636,58 @@ __global__ __launch_bounds__(256) void cast_t_bf16_kernel(const uint16_t *__rest
     emit_tile(E, ((tiles - 1 - t) / tiles_c) * kTT, ((tiles - 1 - t) % tiles_c) * kTT, rows, cols, q, ldq, qt, ldt, tile);
 #pragma unroll
     for (int i = 0; i < kTPer; i++) R[i] = Rn[i];
+  }
+}
+
+// The SwiGLU backward's cast without dz in memory: dz is recomputed from z and da (the same bf16 values as
+// swiglu_bwd_kernel) tile by tile and cast to dzq [M, 2H] and dzqt [2H, ldt] at once. A tile is 128 rows x 128
+// columns h of BOTH halves, so z1, z2 and da are read once for dz1 and dz2; each half leaves through emit_tile. The
+// scale comes from the partial maxima of swiglu_bwd_kernel run without dz, which also published the sigmoid table.
+// Persistent workgroups (each copies the 24 KiB table once) walk the tiles last to first (the amax pass streamed z
+// and da first to last).
+__global__ __launch_bounds__(256) void swiglu_bwd_cast_t_kernel(const uint16_t *__restrict__ z,
+                                                                const uint16_t *__restrict__ da, int64_t M, int64_t H,
+                                                                int64_t sz, int64_t sda,
+                                                                const uint32_t *__restrict__ partial, int nparts,
+                                                                const float *__restrict__ table, uint8_t *__restrict__ dzq,
+                                                                uint8_t *__restrict__ dzqt, int64_t ldt,
+                                                                float *__restrict__ dequant) {
+  __shared__ float lut[kLutSize];
+  __shared__ uint32_t tile[kTT * kTPitch];
+  lut_load(lut, table);
+  float scale, deq;
+  scales_from_amax(fold_partials(partial, nparts), scale, deq);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  const int64_t tiles_h = (H + kTT - 1) / kTT, tiles = tiles_h * ((ldt + kTT - 1) / kTT);
+  for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+    const int64_t tr = tiles - 1 - t;
+    const int64_t r0 = (tr / tiles_h) * kTT, h0 = (tr % tiles_h) * kTT;
+    u32x2 E1[kTPer], E2[kTPer];
+#pragma unroll
+    for (int b = 0; b < kTPer; b += 4) {   // two batches of 4 chunks: 12 loads in flight per thread
+      u32x4 Z1[4], Z2[4], D[4];
+      bool ok[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int id = threadIdx.x + 256 * (b + i);
+        const int64_t gr = r0 + (id >> 4), gh = h0 + 8 * (id & 15);
+        ok[i] = gr < M && gh < H;
+        const uint16_t *zr = z + gr * sz + gh;
+        Z1[i] = ok[i] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr)) : u32x4{0u, 0u, 0u, 0u};
+        Z2[i] = ok[i] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H)) : u32x4{0u, 0u, 0u, 0u};
+        D[i] = ok[i] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + gr * sda + gh))
+                     : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        u32x4 h1, h2;
+        dz_words(lut, Z1[i], Z2[i], D[i], h1, h2);
+        E1[b + i] = ok[i] ? cast8_bf16(h1, scale) : u32x2{0u, 0u};
+        E2[b + i] = ok[i] ? cast8_bf16(h2, scale) : u32x2{0u, 0u};
+      }
+    }
+    emit_tile(E1, r0, h0, M, H, dzq, 2 * H, dzqt, ldt, tile);
+    emit_tile(E2, r0, h0, M, H, dzq + H, 2 * H, dzqt + H * ldt, ldt, tile);
   }
 }
 
@@ -1012,7 +1077,15 @@ static int swiglu_bwd_common(const uint16_t *z, const uint16_t *da, int64_t M, i
                              hipStream_t st) {
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  swiglu_bwd_kernel<<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, dz, 2 * H, partial);
+  if (!dz) {   // dzq and dzqt straight from z and da: an amax pass, then the recomputing transposing cast
+    swiglu_bwd_kernel<<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, nullptr, 0, partial, ws_table(ws));
+    const int64_t tiles = ((H + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
+    const int grid = (int)std::min<int64_t>(std::max<int64_t>(tiles, 1), kSwigluCastTBlocks);
+    swiglu_bwd_cast_t_kernel<<<grid, 256, 0, st>>>(z, da, M, H, sz, sda, partial, g, ws_table(ws), dzq, dzqt, ldt,
+                                                   dequant);
+    return (int)hipGetLastError();
+  }
+  swiglu_bwd_kernel<<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, dz, 2 * H, partial, nullptr);
   const int64_t n = M * 2 * H;
   if (dzqt && H > 0 && ldt > 0) {
     launch_cast_t(SrcBF16{dz, 2 * H}, M, 2 * H, g, dzq, 2 * H, dzqt, ldt, dequant, partial, st);
@@ -1034,12 +1107,13 @@ int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_
 int gpic_fp8_swiglu_bwd_t(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                           uint16_t *dz, uint8_t *dzq, uint8_t *dzqt, int64_t ldt, float *dequant, void *ws,
                           void *stream) {
-  if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !da || !dz || !dzq)) ||
-      (H > 0 && ldt > 0 && !dzqt))
+  if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !da || !dzq)) || (H > 0 && ldt > 0 && !dzqt) ||
+      (!dz && M > 0 && H > 0 && ldt == 0))
     return GPIC_EINVAL;
   if (H % 8 != 0 || sz % 8 != 0 || sda % 8 != 0 || sz < 2 * H || sda < H || ldt % 16 != 0 || ldt < M)
     return GPIC_ESHAPE;
-  if (!aligned16(z) || !aligned16(da) || !aligned16(dz) || !aligned16(dzq) || !aligned16(dzqt) || !aligned16(ws))
+  if (!aligned16(z) || !aligned16(da) || (dz && !aligned16(dz)) || !aligned16(dzq) || !aligned16(dzqt) ||
+      !aligned16(ws))
     return GPIC_EALIGN;
   return swiglu_bwd_common(z, da, M, H, sz, sda, dz, dzq, dzqt, ldt, dequant, ws, (hipStream_t)stream);
 }

@@ -13,6 +13,7 @@ constexpr int kAmaxBlocks = 512;                      // workgroups of a flat am
 constexpr int kSwigluBlocks = 512;                    // workgroups of a SwiGLU pass
 constexpr int kMaxCastBlocks = 8192;                  // workgroups of a streaming cast pass
 constexpr int kCastTBlocks = 1024;                    // workgroups of a (persistent) transposing cast pass
+constexpr int kSwigluCastTBlocks = 768;               // workgroups of the SwiGLU backward's recomputing cast (3 per CU)
 constexpr size_t kCastWorkspaceBytes = 40 * 1024;     // partial maxima (4 KiB), the SwiGLU sigmoid table (24 KiB),
                                                       // the single-pass tagged partials (8 KiB) and call counter
 

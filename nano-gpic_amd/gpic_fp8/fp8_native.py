@@ -190,26 +190,30 @@ def _(z, da):
 
 
 @torch.library.custom_op("gpic::fp8_swiglu_bwd_t", mutates_args=())
-def swiglu_bwd_t(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """swiglu_bwd plus the transposed bytes dzqt [2H, M16] (zero past M): the K-major operand of w12's FP8 wgrad."""
+def swiglu_bwd_t(z: torch.Tensor, da: torch.Tensor,
+                 want_dz: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """swiglu_bwd plus the transposed bytes dzqt [2H, M16] (zero past M): the K-major operand of w12's FP8 wgrad.
+    want_dz=False returns an empty dz and never writes it: dzq and dzqt (the same bytes) are cast from dz recomputed
+    from z and da, which moves less memory than writing dz and reading it back."""
     zc, dac = _bwd_prep(z, da)
     M, H2 = zc.shape
-    dz = torch.empty(M, H2, dtype=torch.bfloat16, device=z.device)
+    dz = torch.empty(M if want_dz else 0, H2, dtype=torch.bfloat16, device=z.device)
     dq = torch.empty(M, H2, dtype=E4, device=z.device)
     dqt = torch.empty(H2, _r16(M), dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
     with torch.cuda.device(z.device):
         ws = L.cast_workspace(z.device)
         L.check(L.lib().gpic_fp8_swiglu_bwd_t(zc.data_ptr(), dac.data_ptr(), M, H2 // 2, zc.stride(0), dac.stride(0),
-                                              dz.data_ptr(), dq.data_ptr(), dqt.data_ptr(), dqt.shape[1], s.data_ptr(),
+                                              dz.data_ptr() if want_dz else None, dq.data_ptr(), dqt.data_ptr(),
+                                              dqt.shape[1], s.data_ptr(),
                                               ws.data_ptr(), L.stream_ptr(z.device)), "gpic_fp8_swiglu_bwd_t")
     return dz, dq, dqt, s
 
 
 @swiglu_bwd_t.register_fake
-def _(z, da):
+def _(z, da, want_dz=True):
     M, H2 = z.shape
-    return (z.new_empty(M, H2), z.new_empty(M, H2, dtype=E4), z.new_empty(H2, _r16(M), dtype=E4),
+    return (z.new_empty(M if want_dz else 0, H2), z.new_empty(M, H2, dtype=E4), z.new_empty(H2, _r16(M), dtype=E4),
             z.new_empty(1, dtype=torch.float32))
 
 
@@ -402,7 +406,7 @@ class _Fp8MLPF8(torch.autograd.Function):
         dyq, dyqt, sdy = tcast_t(dy2)
         da = fp8_gemm(dyq, sdy, w3qt, s3, None, False)           # [M, H]
         dw3 = fp8_gemm(dyqt, sdy, aqt, sa, None, False)          # [C, H]
-        _, dzq, dzqt, sdz = swiglu_bwd_t(z, da)
+        _, dzq, dzqt, sdz = swiglu_bwd_t(z, da, False)   # dz itself is not needed: never written
         dx = fp8_gemm(dzq, sdz, w12qt, s12, None, False)         # [M, C]
         dw12 = fp8_gemm(dzqt, sdz, xqt, sx, None, False)         # [2H, C]
         return dx.view(ctx.shape), dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1])

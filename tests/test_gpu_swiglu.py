@@ -122,6 +122,38 @@ def test_transposing_variants(dev):
     assert not dqt.view(torch.uint8)[:, M:].any()
 
 
+@pytest.mark.parametrize("M,H", [(300, 512), (33, 16), (1000, 2064), (4100, 1040)])
+def test_bwd_t_without_dz_matches(dev, M, H):
+    """swiglu_bwd_t(want_dz=False) never writes dz: it casts dz recomputed from z and da, tile by tile for both halves.
+    Same dzq, dzqt and scale as the path through dz, and as the oracle; ragged M and H (partial 128-tiles in both)."""
+    z = rand_bf16((M, 2 * H), 3.0, seed=M + H)
+    da = rand_bf16((M, H), 0.05, seed=M + H + 1)
+    z[0, :5] = torch.tensor([0.0, -0.0, 1e-30, 300.0, -300.0]).to(torch.bfloat16)   # sigmoid outside the table range
+    zd, dad = z.to(dev), da.to(dev)
+    dz, dq, dqt, s = G.swiglu_bwd_t(zd, dad)
+    dz0, dq0, dqt0, s0 = G.swiglu_bwd_t(zd, dad, False)
+    assert dz0.numel() == 0 and s0.item() == s.item()
+    assert torch.equal(dq0.view(torch.uint8), dq.view(torch.uint8))
+    assert torch.equal(dqt0.view(torch.uint8), dqt.view(torch.uint8))
+    _, oq, od, _ = O.swiglu_bwd(bits(z), bits(da))
+    assert np.array_equal(qb(dq0), oq) and s0.item() == od
+
+
+def test_bwd_t_without_dz_full_size(dev):
+    """The d12 shape (M 32768, H 4096) with NaN and inf planted in z and da: both paths give the same bytes."""
+    g = torch.Generator(device=dev).manual_seed(12)
+    z = (torch.randn(32768, 8192, generator=g, device=dev) * 2).to(torch.bfloat16)
+    da = (torch.randn(32768, 4096, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    z[5, 7] = float("nan")
+    da[100, 3] = float("inf")
+    z[31000, 4100] = -float("inf")
+    dz, dq, dqt, s = G.swiglu_bwd_t(z, da)
+    _, dq0, dqt0, s0 = G.swiglu_bwd_t(z, da, False)
+    assert s0.item() == s.item()
+    assert torch.equal(dq0.view(torch.uint8), dq.view(torch.uint8))
+    assert torch.equal(dqt0.view(torch.uint8), dqt.view(torch.uint8))
+
+
 @pytest.mark.parametrize("M,H", [(1000, 256), (33, 16)])
 def test_tcast_t_with_and_without_product_buffer(dev, M, H):
     """gpic_fp8_swiglu_tcast_t either writes the product a and casts it, or recomputes it inside the cast: the same
