@@ -56,6 +56,8 @@ def parse():
                    help="only copy a 1 GiB buffer (the known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE)")
     p.add_argument("--traffic", action="store_true",
                    help="only run each of the 12 GEMM shapes once, in the printed order (one counter row per shape)")
+    p.add_argument("--step-only", type=int, default=0, metavar="N",
+                   help="only run the d12 step N times (for a kernel-by-kernel trace of one step)")
     return p.parse_args()
 
 
@@ -222,6 +224,13 @@ def main():
         for v in t.values():
             v.grad = None
         step(G, t)
+
+    if args.step_only:
+        for _ in range(args.step_only):
+            run()
+        torch.cuda.synchronize()
+        print(json.dumps({"steps_run": args.step_only}), flush=True)
+        return
 
     shapes = gemm_shapes()
     fl = flops(shapes)
