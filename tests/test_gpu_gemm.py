@@ -165,6 +165,8 @@ def test_d12_shapes(dev, name, M, N, K):
     (33, 4112, 2048, True, 0),        # one tile row, many columns, bias
     (6000, 256, 4096, False, 48),     # one tile column, split K may or may not apply
     (257, 257 // 16 * 16 + 16, 160, True, 0),   # tiny K, two splits with a partial tile
+    (1024, 1024, 6592, False, 0),     # text-block proj wgrad: K = 128 images x 51.5 tokens, many splits, tail tile
+    (6592, 1024, 3072, True, 0),      # text-block qkv dgrad: 104 tiles, split K
 ])
 def test_shape_sweep(dev, M, N, K, bias, lda_pad):
     """Shapes that put several work items on each CU, partial tiles in M, N and K, split-K with a short last split,
