@@ -762,10 +762,10 @@ static void launch_cast_t(SrcBF16 src, int64_t rows, int64_t cols, int nparts, u
 // counter passed to the kernel, so a word left by any earlier call (or by a late workgroup of one) never matches; the
 // workspace is zeroed once, when it is created, and tag 0 is never used.
 // No workgroup waits on another without a bound: a partial that has not appeared within the wait bound (kOnceWaitUs by
-// default, about 8x a whole call) is computed by the waiting workgroup itself, from that workgroup's share of x. So
-// the launch needs no co-residency guarantee (a plain launch; the cooperative one costs ~17 us per call here), never
-// deadlocks when other work holds CUs, and the amax is exact either way. The workspace's fallback word counts such
-// direct computations (0 in normal runs).
+// default, about 8x a whole call) is computed by the waiting workgroup itself, from that workgroup's share of x, and
+// published for the other waiters. So the launch needs no co-residency guarantee (a plain launch; the cooperative one
+// costs ~17 us per call here), never deadlocks when other work holds CUs, and the amax is exact either way. The
+// workspace's fallback word counts such direct computations (0 in normal runs).
 constexpr int kMaxOnceBlocks = 1024;
 constexpr size_t kOnceTagged = 28 * 1024;                         // uint64_t[kMaxOnceBlocks] tagged partials
 constexpr size_t kOnceFallback = kOnceTagged + 8 * kMaxOnceBlocks;  // uint32_t: partials computed by a waiter
@@ -856,10 +856,31 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, uint32_t tag, void *ws
   g = block_max_u32(g);   // its barriers also publish `missing`
   const int nm = nmissing;
   if (nm > 0) {
-    for (int k = 0; k < nm; k++) g = max(g, share_max(missing[k]));
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)nm, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    // Waiters help each other: each starts at a different missing partial, computes it from x and publishes it (the
+    // same word its owner writes), and checks every other one again before computing it, so the missing partials are
+    // computed about once between all waiters rather than once by each.
+    __shared__ uint64_t seen;
+    int computed = 0;
+    for (int k = 0; k < nm; k++) {
+      const int c = missing[(k + blockIdx.x) % nm];
+      if (threadIdx.x == 0)   // (a zero wait bound skips the check: every partial missing at the first poll is computed)
+        seen = wait_ticks ? __hip_atomic_load(tagged + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+      __syncthreads();
+      const uint64_t w = seen;
+      __syncthreads();   // `seen` is rewritten by the next iteration
+      if ((uint32_t)(w >> 32) == tag) {
+        g = max(g, (uint32_t)w);
+      } else {
+        const uint32_t v = share_max(c);
+        g = max(g, v);
+        computed++;
+        if (threadIdx.x == 0)
+          __hip_atomic_store(tagged + c, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (threadIdx.x == 0 && computed > 0)
+      __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)computed,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   return g;
 }

@@ -295,3 +295,33 @@ def test_single_pass_back_to_back_calls(dev):
             assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
             assert torch.equal(qt.view(torch.uint8), qt0.view(torch.uint8))
             assert s.item() == s0.item() * 2.0 ** k
+
+
+def test_single_pass_concurrent_streams(dev, single_pass_default):
+    """Two streams (default priority, separate workspaces) cast config-2-size tensors at the same time, so the two
+    single-pass grids compete for the CUs and not every workgroup is resident while the others wait: waits run out,
+    missing partial maxima are computed from x and shared between the waiters, and every result equals the one
+    computed alone (bytes and scale), flat and transposing."""
+    g = torch.Generator(device=dev).manual_seed(21)
+    xs = [(torch.randn(32768, 1024, generator=g, device=dev) * (1 + 3 * i)).to(torch.bfloat16) for i in range(3)]
+    ref = [G.tcast(x) for x in xs]
+    ref_t = [G.tcast_t(x) for x in xs]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    out1, out2 = [], []
+    with torch.cuda.stream(s1):
+        for _ in range(3):
+            for x in xs:
+                out1.append(G.tcast(x))
+    with torch.cuda.stream(s2):
+        for _ in range(3):
+            for x in reversed(xs):
+                out2.append(G.tcast_t(x))
+    torch.cuda.synchronize()
+    for i, (q, s) in enumerate(out1):
+        rq, rs = ref[i % 3]
+        assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
+    for i, (q, qt, s) in enumerate(out2):
+        rq, rqt, rs = ref_t[2 - i % 3]
+        assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
+        assert torch.equal(qt.view(torch.uint8), rqt.view(torch.uint8))
