@@ -109,6 +109,8 @@ int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz,
 /*
  * gpic_fp8_swiglu_bwd plus the transposed bytes dzqt [2H, ldt] (ldt % 16 == 0, ldt >= M; columns M..ldt-1 zero):
  * the K-major operand of w12's FP8 wgrad. Same dz, dzq and scale as gpic_fp8_swiglu_bwd.
+ *   dz may be NULL (then ldt > 0 and dzqt are required): dz is not written; dzq and dzqt, the same bytes, are cast from
+ *      dz recomputed from z and da tile by tile (less memory traffic than writing dz and reading it back).
  * No counterpart in the reference (its w12 wgrad is bf16, fp8_native.py:264); the FP8-wgrad extension.
  */
 int gpic_fp8_swiglu_bwd_t(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
