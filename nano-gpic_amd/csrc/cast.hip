@@ -775,7 +775,15 @@ template <typename T>
 constexpr int kOnceWords = sizeof(T) == 2 ? 16 : 12;   // 16-byte words a thread of the flat kernel holds (fp32: 12,
                                                         // which its wider narrowing code needs to fit 128 VGPRs)
 constexpr int kOnceTiles = 2;       // 128 x 128 bf16 tiles a workgroup of the transposing kernel holds (64 VGPRs)
+constexpr int kHybridTiles = 8;     // the transposing kernel takes up to this many tiles per workgroup (2 held)
 constexpr int kOnceWaitUs = 200;
+
+// A uniform index the compiler must treat as new here, so it recomputes the addresses derived from it instead of
+// keeping (and spilling) them across the fold's wait.
+__device__ __forceinline__ int64_t opaque_s64(int64_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
 
 // Marks held words as redefined here, so the compiler cannot hoist their conversion above the fold's wait (it would
 // widen all of them to fp32 at once and spill).
@@ -943,7 +951,10 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
   }
 }
 
-// Transposing single-pass cast of a bf16 source: workgroup b holds tiles b and b + G (when there is one).
+// Transposing single-pass cast of a bf16 source: workgroup b holds tiles b and b + G (when there is one) in registers.
+// A larger x (at most kHybridTiles tiles) takes the same kernel as a hybrid: workgroup b's further tiles b + k G,
+// k >= 2, are streamed once for the maximum and once more, last first, for the cast, so only the part of x that does
+// not fit is read twice.
 __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows,
                                                              int64_t cols, uint8_t *__restrict__ q, int64_t ldq,
                                                              uint8_t *__restrict__ qt, int64_t ldt,
@@ -952,22 +963,30 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
   static_assert(kOnceTiles == 2, "two tiles per workgroup");
   __shared__ uint32_t tile[kTT * kTPitch];
   const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
-  const int64_t t0 = blockIdx.x, t1 = blockIdx.x + gridDim.x;   // t0 < tiles: the grid never exceeds the tile count
+  const int64_t G = gridDim.x;
+  const int64_t t0 = blockIdx.x, t1 = blockIdx.x + G;   // t0 < tiles: the grid never exceeds the tile count
+  auto r0_of = [&](int64_t t) { return (t / tiles_c) * kTT; };
+  auto c0_of = [&](int64_t t) { return (t % tiles_c) * kTT; };
   u32x4 R[2 * kTPer];
   u32x4(&R0)[kTPer] = *reinterpret_cast<u32x4(*)[kTPer]>(R);
   u32x4(&R1)[kTPer] = *reinterpret_cast<u32x4(*)[kTPer]>(R + kTPer);
-  load_tile_bf16(x, ld, rows, cols, (t0 / tiles_c) * kTT, (t0 % tiles_c) * kTT, R0);
+  load_tile_bf16(x, ld, rows, cols, r0_of(t0), c0_of(t0), R0);
   if (t1 < tiles) {
-    load_tile_bf16(x, ld, rows, cols, (t1 / tiles_c) * kTT, (t1 % tiles_c) * kTT, R1);
+    load_tile_bf16(x, ld, rows, cols, r0_of(t1), c0_of(t1), R1);
   } else {
 #pragma unroll
     for (int i = 0; i < kTPer; i++) R1[i] = u32x4{0u, 0u, 0u, 0u};
   }
-  const uint32_t m = block_max_u32(words_amax<uint16_t, 2 * kTPer>(R));
-  const uint32_t g = once_fold(m, tag, ws, wait_ticks, [&](int c) {
+  uint32_t m = words_amax<uint16_t, 2 * kTPer>(R);
+  for (int64_t t = blockIdx.x + 2 * G; t < tiles; t += G) {   // hybrid: the tiles that are not held
+    u32x4 S[kTPer];
+    load_tile_bf16(x, ld, rows, cols, r0_of(t), c0_of(t), S);
+    m = max(m, words_amax<uint16_t, kTPer>(S));
+  }
+  const uint32_t g = once_fold(block_max_u32(m), tag, ws, wait_ticks, [&](int c) {
     uint32_t a = 0;
-    for (int64_t t = c; t < tiles && t < c + 2 * (int64_t)gridDim.x; t += gridDim.x) {
-      const int64_t r0 = (t / tiles_c) * kTT, c0 = (t % tiles_c) * kTT;
+    for (int64_t t = c; t < tiles; t += G) {
+      const int64_t r0 = r0_of(t), c0 = c0_of(t);
       for (int i = 0; i < kTPer; i++) {
         const int id = threadIdx.x + 256 * i;
         const int64_t gr = r0 + (id >> 4), gc = c0 + 8 * (id & 15);
@@ -983,8 +1002,21 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
   u32x2 E0[kTPer], E1[kTPer];   // both tiles narrowed first: 32 VGPRs live instead of 64
   cvt_tile_bf16(R0, scale, E0);
   cvt_tile_bf16(R1, scale, E1);
-  emit_tile(E0, (t0 / tiles_c) * kTT, (t0 % tiles_c) * kTT, rows, cols, q, ldq, qt, ldt, tile);
-  if (t1 < tiles) emit_tile(E1, (t1 / tiles_c) * kTT, (t1 % tiles_c) * kTT, rows, cols, q, ldq, qt, ldt, tile);
+  // hybrid: the streamed tiles again, last first (the most recently read are the likeliest still in the MALL), the
+  // next one's loads in flight while the current one is cast
+  int64_t ts = blockIdx.x + 2 * G;
+  if (ts < tiles) ts += ((tiles - 1 - ts) / G) * G;   // the last tile of this workgroup
+  u32x4 S[kTPer];
+  if (ts < tiles) load_tile_bf16(x, ld, rows, cols, r0_of(ts), c0_of(ts), S);
+  const int64_t u0 = opaque_s64(t0), u1 = u0 + G;
+  emit_tile(E0, r0_of(u0), c0_of(u0), rows, cols, q, ldq, qt, ldt, tile);
+  if (u1 < tiles) emit_tile(E1, r0_of(u1), c0_of(u1), rows, cols, q, ldq, qt, ldt, tile);
+  for (; ts >= 2 * G && ts < tiles; ts -= G) {
+    u32x2 E[kTPer];
+    cvt_tile_bf16(S, scale, E);
+    if (ts - G >= 2 * G) load_tile_bf16(x, ld, rows, cols, r0_of(ts - G), c0_of(ts - G), S);
+    emit_tile(E, r0_of(ts), c0_of(ts), rows, cols, q, ldq, qt, ldt, tile);
+  }
 }
 
 // Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and
@@ -1037,7 +1069,7 @@ static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, u
   static int cache = -1;
   const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), &cache);
   const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
-  if (!g_once_enabled || cap <= 0 || tiles <= 0 || tiles > (int64_t)kOnceTiles * cap) return false;
+  if (!g_once_enabled || cap <= 0 || tiles <= 0 || tiles > (int64_t)kHybridTiles * cap) return false;
   const int grid = (int)std::min<int64_t>(tiles, cap);
   cast_t_once_kernel<<<grid, 256, 0, st>>>(x, cols, rows, cols, q, cols, qt, ldt, dequant, ws, once_next_tag(),
                                            once_wait_ticks());

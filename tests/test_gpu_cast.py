@@ -325,3 +325,30 @@ def test_single_pass_concurrent_streams(dev, single_pass_default):
         rq, rqt, rs = ref_t[2 - i % 3]
         assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
         assert torch.equal(qt.view(torch.uint8), rqt.view(torch.uint8))
+
+
+@pytest.mark.parametrize("rows,cols", [(5000, 7008), (9000, 9008), (32768, 3072), (32768, 4096)])
+def test_tcast_t_hybrid_matches_two_pass(dev, rows, cols, single_pass_default):
+    """Transposing casts of 2049..8192 tiles take the hybrid single pass (two tiles per workgroup held in registers,
+    the rest streamed twice): the same bytes and scale as the forced two-pass path and as the zero-wait path (missing
+    partials computed from x), ragged in both dimensions, with a NaN and an infinity planted; the [32768 x 3072] dY of
+    qkv also against the oracle."""
+    g = torch.Generator(device=dev).manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g, device=dev) * 4).to(torch.bfloat16)
+    x[rows // 3, cols // 5] = float("nan")
+    x[rows - 1, cols - 1] = 1.0e4
+    outs = []
+    for enabled, wait in ((True, -1), (False, -1), (True, 0)):
+        L.set_single_pass(enabled, wait)
+        q, qt, s = G.tcast_t(x)
+        outs.append((q.view(torch.uint8).clone(), qt.view(torch.uint8).clone(), s.item()))
+        del q, qt
+    L.set_single_pass(True, -1)
+    q0, qt0, s0 = outs[0]
+    r16 = (rows + 15) // 16 * 16
+    assert qt0.shape == (cols, r16) and torch.equal(qt0[:, :rows], q0.t()) and not qt0[:, rows:].any()
+    for q, qt, s in outs[1:]:
+        assert s == s0 and torch.equal(q, q0) and torch.equal(qt, qt0)
+    if (rows, cols) == (32768, 3072):
+        oq, od, _ = O.tcast(bits(x.cpu()))
+        assert s0 == od and np.array_equal(q0.cpu().numpy(), oq)
