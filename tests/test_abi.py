@@ -58,6 +58,11 @@ def test_validation_codes():
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 16, 16, wsp, 16, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_bwd(wsp, wsp, 4, 16, 32, 8, wsp, wsp, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_tcast_t(wsp, 40, 16, 32, None, wsp, 16, wsp, 32, wsp, wsp, None) == -3
+    # SwiGLU backward without dz: needs the transposed output (dzqt, ldt > 0); a given dz must be aligned
+    b = lib.gpic_fp8_swiglu_bwd_t
+    assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, wsp, 0, wsp, wsp, None) == -1
+    assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, None, 16, wsp, wsp, None) == -1
+    assert b(wsp, wsp, 4, 16, 32, 16, wsp + 8, wsp, wsp, 16, wsp, wsp, None) == -4
     # GEMM: K % 16, N % 16, leading dimensions, null scales
     g = lib.gpic_fp8_gemm
     assert g(wsp, 24, wsp, wsp, 24, wsp, None, wsp, 16, 4, 16, 24, 1, None, 0, None) == -3
@@ -66,6 +71,12 @@ def test_validation_codes():
     assert g(wsp, 32, None, wsp, 32, wsp, None, wsp, 16, 4, 16, 32, 1, None, 0, None) == -1
     # empty output: nothing to do
     assert g(None, 32, wsp, None, 32, wsp, None, None, 16, 0, 16, 32, 1, None, 0, None) == 0
+
+
+def test_single_pass_knob_is_host_only():
+    """gpic_fp8_set_single_pass only records the setting (no device call): safe without a GPU; defaults restored."""
+    L.set_single_pass(False, 0)
+    L.set_single_pass(True, -1)
 
 
 def test_loader_fails_loudly_without_library(monkeypatch, tmp_path):
