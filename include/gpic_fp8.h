@@ -92,6 +92,8 @@ int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, u
  * _swiglu_bwd_kernel :83-98, then _cast_flat).
  *   z [M, 2H] (row stride sz), da [M, H] (row stride sda) bf16 ->
  *   dz [M, 2H] bf16 contiguous, dzq [M, 2H] e4m3 contiguous, dequant 1 fp32
+ *   dz may be NULL: dz is not written and dzq is cast from dz recomputed from z and da (the same bytes; less memory
+ *      traffic than writing dz and reading it back) -- for a caller whose weight gradient takes dzq, not dz.
  */
 int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                         uint16_t *dz, uint8_t *dzq, float *dequant, void *ws, void *stream);
@@ -136,6 +138,20 @@ size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
                   const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, int fast_accum,
                   void *ws, size_t ws_bytes, void *stream);
+
+/*
+ * Scaled FP8 GEMM with both operands "MN-major" (K is their row index): the weight gradient straight from the
+ * untransposed e4m3 bytes of the layer's output gradient and input.
+ *   C[m, n] = bf16(sa * sb * sum_k A[k, m] * B[k, n]);  if bias: C[m, n] = bf16(C[m, n] + bias[n])
+ *   A [K, M] e4m3, row stride lda;  B [K, N] e4m3, row stride ldb;  C [M, N] bf16, row stride ldc
+ *   M % 16 == 0, N % 16 == 0, lda / ldb % 16 == 0, ldc % 8 == 0, K * lda and K * ldb < 2^31; any K.
+ * Bit-identical to gpic_fp8_gemm on the transposed operands (A^T [M, K], B^T [N, K]): the same products summed in
+ * the same order, with the same workspace (gpic_fp8_gemm_workspace_bytes(M, N, K)).
+ * No counterpart in the reference (its wgrads are bf16, fp8_native.py:202, 264-265); the FP8-wgrad extension.
+ */
+int gpic_fp8_gemm_mn(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
+                     const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, void *ws,
+                     size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -547,6 +547,53 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
+// The flat cast of dz without dz in memory: dz recomputed from z and da (the same bf16 values as swiglu_bwd_kernel)
+// and cast to dzq [M, 2H] (contiguous) with the scale from swiglu_bwd_kernel<false>'s partial maxima and its
+// sigmoid table. Rows strided over workgroups, kRowsPer rows' loads in flight per thread (as the amax pass).
+__global__ __launch_bounds__(kCastThreads) void swiglu_bwd_cast_kernel(const uint16_t *__restrict__ z,
+                                                                        const uint16_t *__restrict__ da, int64_t M,
+                                                                        int64_t H, int64_t sz, int64_t sda,
+                                                                        const uint32_t *__restrict__ partial, int nparts,
+                                                                        const float *__restrict__ table,
+                                                                        uint8_t *__restrict__ dzq,
+                                                                        float *__restrict__ dequant) {
+  __shared__ float lut[kLutSize];
+  lut_load(lut, table);
+  float scale, deq;
+  scales_from_amax(fold_partials(partial, nparts), scale, deq);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  const int64_t units = H / 8;
+  const int64_t rstride = gridDim.x;
+  auto emit = [&](int64_t r, int64_t u, u32x4 z1, u32x4 z2, u32x4 d) {
+    u32x4 h1, h2;
+    dz_words(lut, z1, z2, d, h1, h2);
+    uint8_t *o = dzq + r * 2 * H + 8 * u;
+    __builtin_nontemporal_store(cast8_bf16(h1, scale), reinterpret_cast<u32x2 *>(o));
+    __builtin_nontemporal_store(cast8_bf16(h2, scale), reinterpret_cast<u32x2 *>(o + H));
+  };
+  for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
+    int64_t r = blockIdx.x;
+    for (; r + (kRowsPer - 1) * rstride < M; r += kRowsPer * rstride) {
+      u32x4 Z1[kRowsPer], Z2[kRowsPer], D[kRowsPer];
+#pragma unroll
+      for (int k = 0; k < kRowsPer; k++) {
+        const uint16_t *zr = z + (r + k * rstride) * sz + 8 * u;
+        Z1[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr));
+        Z2[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H));
+        D[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + (r + k * rstride) * sda + 8 * u));
+      }
+#pragma unroll
+      for (int k = 0; k < kRowsPer; k++) emit(r + k * rstride, u, Z1[k], Z2[k], D[k]);
+    }
+    for (; r < M; r += rstride) {
+      const uint16_t *zr = z + r * sz + 8 * u;
+      emit(r, u, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr)),
+           __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H)),
+           __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + r * sda + 8 * u)));
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------- host side
 
 static inline int grid_for(int64_t units, int cap) {
@@ -1176,6 +1223,11 @@ static int swiglu_bwd_common(const uint16_t *z, const uint16_t *da, int64_t M, i
                              hipStream_t st) {
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
+  if (!dz && !dzqt) {   // dzq straight from z and da: an amax pass, then the recomputing flat cast
+    swiglu_bwd_kernel<false><<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, nullptr, 0, partial, ws_table(ws));
+    swiglu_bwd_cast_kernel<<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, partial, g, ws_table(ws), dzq, dequant);
+    return (int)hipGetLastError();
+  }
   if (!dz) {   // dzq and dzqt straight from z and da: an amax pass, then the recomputing transposing cast
     swiglu_bwd_kernel<false><<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, nullptr, 0, partial, ws_table(ws));
     const int64_t tiles = ((H + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
@@ -1197,9 +1249,10 @@ static int swiglu_bwd_common(const uint16_t *z, const uint16_t *da, int64_t M, i
 
 int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                         uint16_t *dz, uint8_t *dzq, float *dequant, void *ws, void *stream) {
-  if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !da || !dz || !dzq))) return GPIC_EINVAL;
+  if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !da || !dzq))) return GPIC_EINVAL;
   if (H % 8 != 0 || sz % 8 != 0 || sda % 8 != 0 || sz < 2 * H || sda < H) return GPIC_ESHAPE;
-  if (!aligned16(z) || !aligned16(da) || !aligned16(dz) || !aligned16(dzq) || !aligned16(ws)) return GPIC_EALIGN;
+  if (!aligned16(z) || !aligned16(da) || (dz && !aligned16(dz)) || !aligned16(dzq) || !aligned16(ws))
+    return GPIC_EALIGN;
   return swiglu_bwd_common(z, da, M, H, sz, sda, dz, dzq, nullptr, 0, dequant, ws, (hipStream_t)stream);
 }
 

@@ -33,10 +33,12 @@ namespace gpic {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 // Types for the C staging block in LDS and the bf16 stores: may_alias, since LDS holding fragments of A and B as
 // one type is reused for C as another, and type-based alias analysis must not separate the two.
 typedef float f4a_t __attribute__((ext_vector_type(4), __may_alias__));
 typedef uint32_t st16_t __attribute__((ext_vector_type(4), __may_alias__));
+typedef uint32_t st8_t __attribute__((ext_vector_type(2), __may_alias__));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 #define GPIC_LDS __attribute__((address_space(3)))
@@ -57,6 +59,10 @@ constexpr int kBufferFlags = 0x00020000;               // raw buffer descriptor 
 constexpr int kOOB = (int)0x80000000;                  // an offset past any descriptor's range: reads zeros
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+// MN-major K tiles (rows of 256 bytes): 16-byte chunk c of K row r lives in slot c ^ mn_swz(r). A transposing read
+// takes two adjacent chunks (2c', 2c' + 1) of 8 consecutive rows; the XOR with 2 (r & 7) sends those 16 chunks to 16
+// different slots, i.e. all 64 banks.
+__device__ __forceinline__ int mn_swz(int r) { return (r & 7) << 1; }
 
 // The column of C that MFMA output row i (0..31) of a 32 x 32 tile stands for: i with bits 2 and 3 exchanged. Lane l
 // holds output rows 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15; through this map those are the columns
@@ -111,7 +117,11 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
-template <bool kTail>
+// kMN: both operands stored with K as their row index ("MN-major"): A [K, M] (row stride lda), B [K, N] (row stride
+// ldb), C[m, n] = bf16(sa * sb * sum_k A[k, m] B[k, n]) -- the FP8 wgrad reading the untransposed e4m3 activations
+// and gradients. A K tile of an operand is then 128 rows (K) x 256 bytes (MN) in LDS and its fragments are read with
+// the transposing ds_read_b64_tr_b8.
+template <bool kTail, bool kMN>
 __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
                                                             const uint8_t *__restrict__ B, int ldb,
                                                             const float *__restrict__ sa, const float *__restrict__ sb,
@@ -133,7 +143,13 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int kchunk = 16 * ((lane & 7) ^ swz(lrow));
   // B rows are permuted inside each group of 32: LDS row r holds B row col_of(r), so that each lane's accumulators
   // hold runs of 8 consecutive columns of C (see the epilogue).
-  const int baseA = lrow * lda + kchunk, baseB = col_of(lrow) * ldb + kchunk;
+  // MN-major: instruction i of a wave fills K rows [R0, R0 + 4), R0 = (i * 4 + wave % 4) * 4 = 16 i + mrow - lane / 16;
+  // lane j writes 16-byte slot j & 15 of row 16 i + mrow, i.e. MN chunk (j & 15) ^ mn_swz(row), and mn_swz depends on
+  // row & 7 = mrow & 7 only.
+  const int mrow = (wave & 3) * 4 + (lane >> 4);
+  const int mchunk = (lane & 15) ^ mn_swz(mrow);
+  const int baseA = kMN ? mrow * lda + 16 * mchunk : lrow * lda + kchunk;
+  const int baseB = kMN ? mrow * ldb + 16 * mchunk : col_of(lrow) * ldb + kchunk;
   const float s = sa[0] * sb[0];
 
   // ---- persistent: work item `it` (a tile and a K split) goes to workgroup it % gridDim.x. The grid is a multiple
@@ -144,6 +160,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   struct Item {
     int m0, n0, split, kbeg, kend, nk;
     v4i rA, rB;   // buffer descriptors over the item's rows of A and B (rows past M / N read as zero)
+    int voA, voB; // MN-major: this lane's load offsets, or kOOB where its chunk lies past M / N
   };
   auto item = [&](int it) {
     Item w;
@@ -158,8 +175,16 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     w.kbeg = w.split * ksplit;
     w.kend = min(K, w.kbeg + ksplit);
     w.nk = (w.kend - w.kbeg + kBK - 1) / kBK;
-    w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
-    w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBN) * ldb);
+    if constexpr (kMN) {   // descriptors from the item's first column to the end of the matrix (K x ld bytes)
+      w.rA = buffer_rsrc(A + w.m0, K * lda - w.m0);
+      w.rB = buffer_rsrc(B + w.n0, K * ldb - w.n0);
+      w.voA = w.m0 + 16 * mchunk < M ? baseA : kOOB;
+      w.voB = w.n0 + 16 * mchunk < N ? baseB : kOOB;
+    } else {
+      w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
+      w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBN) * ldb);
+      w.voA = w.voB = 0;
+    }
     return w;
   };
 
@@ -168,11 +193,23 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // register held across the loop for each load. In the last, partial K tile (kTail instance only), chunks at or past
   // kend read zeros.
   auto load = [&](const Item &w, bool isA, int dst, int k0, int i) {
-    const int R0 = (i * kLoaders + (wave & 3)) * 8;
-    const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + i * opaque(32 * ldb);
-    const uint32_t to = lds_addr(smem) + dst + R0 * kBK;
-    if (!kTail || k0 + kBK <= w.kend) lds_dma16(isA ? w.rA : w.rB, vo, k0, to);
-    else lds_dma16(isA ? w.rA : w.rB, k0 + kchunk < w.kend ? vo + k0 : kOOB, 0, to);
+    if constexpr (kMN) {
+      // K rows k0 + 16 i + mrow; the K position goes to the scalar offset (k0 * ld), the row within the tile and the
+      // chunk to the lane's; lanes whose chunk lies past M / N start from kOOB
+      const int ld = isA ? lda : ldb;
+      const int R0 = (i * kLoaders + (wave & 3)) * 4;
+      // (kOOB + these offsets stays in [2^31, 2^32): still past the range, which is below 2^31)
+      const int vo = (isA ? w.voA : w.voB) + i * opaque(16 * ld);
+      const uint32_t to = lds_addr(smem) + dst + R0 * 256;
+      if (!kTail || k0 + kBK <= w.kend) lds_dma16(isA ? w.rA : w.rB, vo, k0 * ld, to);
+      else lds_dma16(isA ? w.rA : w.rB, k0 + 16 * i + mrow < w.kend ? vo + k0 * ld : kOOB, 0, to);
+    } else {
+      const int R0 = (i * kLoaders + (wave & 3)) * 8;
+      const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + i * opaque(32 * ldb);
+      const uint32_t to = lds_addr(smem) + dst + R0 * kBK;
+      if (!kTail || k0 + kBK <= w.kend) lds_dma16(isA ? w.rA : w.rB, vo, k0, to);
+      else lds_dma16(isA ? w.rA : w.rB, k0 + kchunk < w.kend ? vo + k0 : kOOB, 0, to);
+    }
   };
   auto a_half = [](int stage) { return stage * kHalfBytes; };
   auto b_half = [](int stage) { return kBBase + stage * kHalfBytes; };
@@ -196,8 +233,30 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int frow = lane & 31;
   const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
   const int c0 = 2 * (lane >> 5);
+  // MN-major: a fragment is 4 ds_read_b64_tr_b8. In each 16-lane group g = lane / 16, source lane s = lane % 16 reads
+  // 8 bytes of K row 32 (g / 2) + 8 q + s / 2 (+ 64 step), MN bytes mnb + 16 (g % 2) + 8 (s % 2) + [0, 8); the
+  // transposing read hands output lane j of the group byte r of source lane 2 r + j / 8, i.e. K row 8 q + r of MN
+  // index mnb + 16 (g % 2) + j: lane l gets MN index mnb + (l & 31) and K 32 (l / 32) + 8 q + [0, 8) in bytes
+  // 8 q .. 8 q + 7 of its operand -- the layout of the K-major fragment. The chunk index (mnb / 16 + g % 2) ^ 2 (s / 2)
+  // equals (mnb / 16) ^ tr_x since mnb / 16 is even.
+  const int tr_g = lane >> 4, tr_s = lane & 15;
+  const int tr_row = 32 * (tr_g >> 1) + (tr_s >> 1);
+  const int tr_off = tr_row * 256 + 8 * (tr_s & 1);
+  const int tr_x = 16 * ((tr_g & 1) | mn_swz(tr_row));
   auto read_frag = [&](int ast, int bst, int j) {
     const int step = j / (kTM + kTN), f = j % (kTM + kTN);
+    if constexpr (kMN) {
+      const int mnb = f < kTM ? wm * kWTM + f * 32 : wn * kWTN + (f - kTM) * 32;
+      const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem + (f < kTM ? a_half(ast) : b_half(bst)) +
+                                  step * 64 * 256 + tr_off + (mnb ^ tr_x);
+      v2i r[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) r[q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GPIC_LDS v2i *)(p + q * 8 * 256));
+      const v8i v{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
+      if (f < kTM) fa[step][f] = v;
+      else fb[step][f - kTM] = v;
+      return;
+    }
     const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
     const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem +
                                 (f < kTM ? a_half(ast) + (wm * kWTM + f * 32 + frow) * kBK
@@ -332,7 +391,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             const int r = wm * kWTM + mi * 32 + wr;
-            const int n = cur.n0 + wn * kWTN + ni * 32 + 16 * (q >> 1) + 8 * wh + 4 * (q & 1);
+            const int n = cur.n0 + wn * kWTN + ni * 32 +
+                          (kMN ? 8 * q + 4 * wh : 16 * (q >> 1) + 8 * wh + 4 * (q & 1));
             const v16f &v = acc[ni][mi];
             __builtin_amdgcn_raw_buffer_store_b128(
                 __builtin_bit_cast(u32x4, v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}), rP,
@@ -361,21 +421,32 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 #pragma unroll
       for (int mi = 0; mi < kTM; mi++) {
 #pragma unroll
-        for (int ni = 0; ni < kTN; ni++)
+        for (int ni = 0; ni < kTN; ni++) {
+          const v16f &v = acc[ni][mi];
+          if constexpr (kMN) {
+            // natural column order: runs of 4 (columns 32 ni + 8 q + 4 wh + [0, 4)), 8 bytes each, into half
+            // wh ^ (wr / 16) of the chunk (rows wr and wr + 16 share a slot: the halves keep them apart)
 #pragma unroll
-          for (int hh = 0; hh < 2; hh++) {
-            const v16f &v = acc[ni][mi];
-            st16_t w;
+            for (int q = 0; q < 4; q++)
+              *(GPIC_LDS st8_t *)(cst + wr * 256 + 16 * ((4 * ni + q) ^ (wr & 15)) + 8 * (wh ^ (wr >> 4))) =
+                  st8_t{pack_bf16(v[4 * q] * s, v[4 * q + 1] * s), pack_bf16(v[4 * q + 2] * s, v[4 * q + 3] * s)};
+          } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-              w[e] = pack_bf16(v[8 * hh + 2 * e] * s, v[8 * hh + 2 * e + 1] * s);
-            *(GPIC_LDS st16_t *)(cst + wr * 256 + 16 * ((4 * ni + 2 * hh + wh) ^ (wr & 15))) = w;
+            for (int hh = 0; hh < 2; hh++) {
+              st16_t w;
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                w[e] = pack_bf16(v[8 * hh + 2 * e] * s, v[8 * hh + 2 * e + 1] * s);
+              *(GPIC_LDS st16_t *)(cst + wr * 256 + 16 * ((4 * ni + 2 * hh + wh) ^ (wr & 15))) = w;
+            }
           }
+        }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           const int r = 4 * j + rr;
           st16_t w = *(const GPIC_LDS st16_t *)(cst + r * 256 + 16 * (rc ^ (r & 15)));
+          if (kMN && r >= 16) w = st16_t{w[2], w[3], w[0], w[1]};   // halves exchanged (j >= 4: known here)
           if (bias) {   // bf16(bf16(acc * s) + bias)
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
@@ -465,6 +536,40 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
   return p;
 }
 
+// The launch shared by both operand layouts (arguments checked by the entry points).
+template <bool kMN>
+static int launch_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
+                       const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, void *ws,
+                       size_t ws_bytes, hipStream_t st) {
+  if (M == 0 || N == 0) return GPIC_OK;
+  if (K > 0 && (!A || !B)) return GPIC_EINVAL;
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && ((uintptr_t)bias & 7u))) return GPIC_EALIGN;
+  const Plan p = K > 0 ? plan_gemm(M, N, K) : Plan{(int)((M + kBM - 1) / kBM), (int)((N + kBN - 1) / kBN), 1, kBK};
+  float *P = nullptr;
+  if (p.splits > 1) {
+    const size_t need = (size_t)p.splits * M * N * sizeof(float);
+    if (!ws || ws_bytes < need) return GPIC_EWORKSPACE;
+    if (!aligned16(ws)) return GPIC_EALIGN;
+    P = static_cast<float *>(ws);
+  }
+  // One workgroup per CU at most (160 KiB of LDS each); a persistent grid is a multiple of 8, one per XCD.
+  const int work = p.tiles_m * p.tiles_n * p.splits;
+  const int slots = num_cus() & ~7;
+  const int grid = work <= slots || slots < 8 ? work : slots;
+  // the partial-K-tile load path is compiled only into the instance that needs it
+  auto *kernel = K % kBK ? gemm_tn_kernel<true, kMN> : gemm_tn_kernel<false, kMN>;
+  kernel<<<grid, kThreads, 0, st>>>(
+      A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
+      p.splits);
+  if (P) {
+    const int64_t quads = M * (N / 4);
+    int64_t g = (quads + 255) / 256;
+    if (g > 8192) g = 8192;
+    splitk_reduce_kernel<<<(int)g, 256, 0, st>>>(P, p.splits, (int)M, (int)N, sa, sb, bias, C, ldc);
+  }
+  return (int)hipGetLastError();
+}
+
 }  // namespace gpic
 
 using namespace gpic;
@@ -485,34 +590,19 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
   if (K % 16 != 0 || N % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldc % 8 != 0) return GPIC_ESHAPE;
   if (lda < K || ldb < K || ldc < N || lda >= (1 << 23) || ldb >= (1 << 23) || M >= (1 << 30) || N >= (1 << 30))
     return GPIC_ESHAPE;
-  if (M == 0 || N == 0) return GPIC_OK;
-  if (K > 0 && (!A || !B)) return GPIC_EINVAL;
-  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && ((uintptr_t)bias & 7u))) return GPIC_EALIGN;
-  hipStream_t st = (hipStream_t)stream;
-  const Plan p = K > 0 ? plan_gemm(M, N, K) : Plan{(int)((M + kBM - 1) / kBM), (int)((N + kBN - 1) / kBN), 1, kBK};
-  float *P = nullptr;
-  if (p.splits > 1) {
-    const size_t need = (size_t)p.splits * M * N * sizeof(float);
-    if (!ws || ws_bytes < need) return GPIC_EWORKSPACE;
-    if (!aligned16(ws)) return GPIC_EALIGN;
-    P = static_cast<float *>(ws);
-  }
-  // One workgroup per CU at most (160 KiB of LDS each); a persistent grid is a multiple of 8, one per XCD.
-  const int work = p.tiles_m * p.tiles_n * p.splits;
-  const int slots = num_cus() & ~7;
-  const int grid = work <= slots || slots < 8 ? work : slots;
-  // the partial-K-tile load path is compiled only into the instance that needs it
-  auto *kernel = K % kBK ? gemm_tn_kernel<true> : gemm_tn_kernel<false>;
-  kernel<<<grid, kThreads, 0, st>>>(
-      A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
-      p.splits);
-  if (P) {
-    const int64_t quads = M * (N / 4);
-    int64_t g = (quads + 255) / 256;
-    if (g > 8192) g = 8192;
-    splitk_reduce_kernel<<<(int)g, 256, 0, st>>>(P, p.splits, (int)M, (int)N, sa, sb, bias, C, ldc);
-  }
-  return (int)hipGetLastError();
+  return launch_gemm<false>(A, lda, sa, B, ldb, sb, bias, C, ldc, M, N, K, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int gpic_fp8_gemm_mn(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
+                     const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, void *ws,
+                     size_t ws_bytes, void *stream) {
+  if (M < 0 || N < 0 || K < 0 || !sa || !sb || (M > 0 && N > 0 && !C)) return GPIC_EINVAL;
+  if (M % 16 != 0 || N % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldc % 8 != 0) return GPIC_ESHAPE;
+  // every load offset (K row x row stride) is a 32-bit buffer offset
+  if (lda < M || ldb < N || ldc < N || K * lda >= (int64_t(1) << 31) || K * ldb >= (int64_t(1) << 31) ||
+      M >= (1 << 30) || N >= (1 << 30))
+    return GPIC_ESHAPE;
+  return launch_gemm<true>(A, lda, sa, B, ldb, sb, bias, C, ldc, M, N, K, ws, ws_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -14,7 +14,9 @@ Phases (convert_native / convert_fp8 recipes):
 - phase 1 ("native"): forward GEMMs in FP8, backward in bf16 -- as the reference;
 - phase 2 ("native2"): the MLP as one function with FP8 dgrads, bf16 wgrads -- as the reference;
 - phase 3 ("native3", an extension): every forward, dgrad and wgrad GEMM of qkv_x, proj, w12 and w3 in FP8. The
-  forward keeps the e4m3 bytes of its inputs (transposed, K-major) for the wgrad instead of the bf16 inputs.
+  forward keeps the e4m3 bytes of its inputs for the wgrad instead of the bf16 inputs; the wgrad GEMM reads them and
+  the output gradient's bytes as they are (fp8_gemm_mn: K, the token index, is their row index), so the activations
+  and gradients are cast flat, with no transposed copies.
 """
 from typing import Optional
 
@@ -166,27 +168,45 @@ def _bwd_prep(z, da):
     return zc, _prep_rows(da, H2 // 2)
 
 
-@torch.library.custom_op("gpic::fp8_swiglu_bwd", mutates_args=())
-def swiglu_bwd(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """z [M, 2H] bf16, da [M, H] bf16 -> dz [M, 2H] bf16, dz as e4m3 [M, 2H] and its tensorwise scale [1] fp32.
-    (fp8_native.py:153-166)"""
+def _swiglu_bwd(z, da, want_dz):
     zc, dac = _bwd_prep(z, da)
     M, H2 = zc.shape
-    dz = torch.empty(M, H2, dtype=torch.bfloat16, device=z.device)
+    dz = torch.empty(M, H2, dtype=torch.bfloat16, device=z.device) if want_dz else None
     dq = torch.empty(M, H2, dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
     with torch.cuda.device(z.device):
         ws = L.cast_workspace(z.device)
         L.check(L.lib().gpic_fp8_swiglu_bwd(zc.data_ptr(), dac.data_ptr(), M, H2 // 2, zc.stride(0), dac.stride(0),
-                                            dz.data_ptr(), dq.data_ptr(), s.data_ptr(), ws.data_ptr(),
+                                            L.ptr(dz), dq.data_ptr(), s.data_ptr(), ws.data_ptr(),
                                             L.stream_ptr(z.device)), "gpic_fp8_swiglu_bwd")
     return dz, dq, s
+
+
+@torch.library.custom_op("gpic::fp8_swiglu_bwd", mutates_args=())
+def swiglu_bwd(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """z [M, 2H] bf16, da [M, H] bf16 -> dz [M, 2H] bf16, dz as e4m3 [M, 2H] and its tensorwise scale [1] fp32.
+    (fp8_native.py:153-166)"""
+    return _swiglu_bwd(z, da, True)
 
 
 @swiglu_bwd.register_fake
 def _(z, da):
     M, H2 = z.shape
     return z.new_empty(M, H2), z.new_empty(M, H2, dtype=E4), z.new_empty(1, dtype=torch.float32)
+
+
+@torch.library.custom_op("gpic::fp8_swiglu_bwd_q", mutates_args=())
+def swiglu_bwd_q(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """swiglu_bwd without dz in memory: (dzq [M, 2H] e4m3, scale [1] fp32), the same bytes, cast from dz recomputed
+    from z and da -- for phase 3, whose w12 wgrad takes dzq instead of dz (an extension of the reference)."""
+    _, dq, s = _swiglu_bwd(z, da, False)
+    return dq, s
+
+
+@swiglu_bwd_q.register_fake
+def _(z, da):
+    M, H2 = z.shape
+    return z.new_empty(M, H2, dtype=E4), z.new_empty(1, dtype=torch.float32)
 
 
 @torch.library.custom_op("gpic::fp8_swiglu_bwd_t", mutates_args=())
@@ -265,6 +285,52 @@ def _(a, sa, b, sb, bias=None, fast=True):
     return a.new_empty(a.shape[0], b.shape[0], dtype=torch.bfloat16)
 
 
+def _gemm_operand_mn(t, name):
+    if t.dtype != E4 or t.dim() != 2:
+        raise ValueError(f"{name} must be a 2-D float8_e4m3fn tensor, got {t.dtype} {tuple(t.shape)}")
+    if t.stride(1) != 1 or t.stride(0) % 16 or t.stride(0) < t.shape[1] or t.data_ptr() % 16:
+        t = L.aligned(t.contiguous())
+    return t
+
+
+@torch.library.custom_op("gpic::fp8_gemm_mn", mutates_args=())
+def fp8_gemm_mn(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
+                bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a [K, M] e4m3, b [K, N] e4m3 (both with K as the row index), sa / sb [1] fp32 ->
+    C [M, N] bf16 = bf16(sa * sb * a^T @ b) (then bf16(C + bias)). The FP8 weight gradient from the untransposed
+    bytes of the output gradient (a) and the input (b): the same bytes as fp8_gemm(a.t(), sa, b.t(), sb) without the
+    transposed copies. An extension of the reference, whose wgrads are bf16 (fp8_native.py:202, 264-265)."""
+    L.require_gpu(a, b, sa, sb, bias)
+    a = _gemm_operand_mn(a, "a")
+    b = _gemm_operand_mn(b, "b")
+    K, M = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError(f"fp8_gemm_mn: a is [{K}, {M}] but b is {tuple(b.shape)}")
+    if M % 16 or N % 16:
+        raise ValueError(f"fp8_gemm_mn needs M % 16 == 0 and N % 16 == 0, got M={M} N={N} K={K}")
+    sa = sa.to(torch.float32).reshape(1)
+    sb = sb.to(torch.float32).reshape(1)
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+        if bias.numel() != N:
+            raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
+        bias = bias if bias.data_ptr() % 8 == 0 else bias.clone()
+    c = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    with torch.cuda.device(a.device):
+        nws = L.lib().gpic_fp8_gemm_workspace_bytes(M, N, K)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=a.device) if nws else None
+        L.check(L.lib().gpic_fp8_gemm_mn(a.data_ptr(), a.stride(0), sa.data_ptr(), b.data_ptr(), b.stride(0),
+                                         sb.data_ptr(), L.ptr(bias), c.data_ptr(), c.stride(0), M, N, K,
+                                         L.ptr(ws), nws, L.stream_ptr(a.device)), "gpic_fp8_gemm_mn")
+    return c
+
+
+@fp8_gemm_mn.register_fake
+def _(a, sa, b, sb, bias=None):
+    return a.new_empty(a.shape[1], b.shape[1], dtype=torch.bfloat16)
+
+
 def _mm(xq, sx, wq, sw, fast=True):
     """[M, K] e4m3 x [N, K] e4m3 (each with its tensorwise scale) -> [M, N] bf16 (fp8_native.py:175-178)."""
     return fp8_gemm(xq, sx, wq, sw, None, fast)
@@ -296,26 +362,26 @@ class _Fp8Linear(torch.autograd.Function):
 
 
 class _Fp8LinearF8(torch.autograd.Function):
-    """Phase 3: forward, dgrad and wgrad GEMMs all in FP8. The forward keeps x's e4m3 bytes transposed (K-major over
-    the tokens, the wgrad's B operand) and w's transposed bytes (the dgrad's B operand) instead of bf16 copies."""
+    """Phase 3: forward, dgrad and wgrad GEMMs all in FP8. The forward keeps x's e4m3 bytes (the wgrad's B operand,
+    read with the tokens as its K rows) and w's transposed bytes (the dgrad's B operand) instead of bf16 copies."""
     @staticmethod
     def forward(ctx, x, w, b):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        xq, xqt, sx = tcast_t(x2)
+        xq, sx = tcast(x2)
         wq, wqt, sw = tcast_t(w)
         y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
-        ctx.save_for_backward(xqt, sx, wqt, sw)
+        ctx.save_for_backward(xq, sx, wqt, sw)
         ctx.has_b, ctx.shape, ctx.wdt = b is not None, shape, w.dtype
         return y.view(*shape[:-1], w.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
-        xqt, sx, wqt, sw = ctx.saved_tensors
+        xq, sx, wqt, sw = ctx.saved_tensors
         dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
-        dyq, dyqt, sdy = tcast_t(dy2)
+        dyq, sdy = tcast(dy2)
         dx = fp8_gemm(dyq, sdy, wqt, sw, None, False).view(ctx.shape)     # [M, N] . [K, N]^T
-        dw = fp8_gemm(dyqt, sdy, xqt, sx, None, False).to(ctx.wdt)      # [N, M16] . [K, M16]^T
+        dw = fp8_gemm_mn(dyq, sdy, xq, sx).to(ctx.wdt)                   # [M, N]^T . [M, K]
         db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
         return dx, dw, db
 
@@ -383,32 +449,32 @@ class _Fp8MLP(torch.autograd.Function):
 
 class _Fp8MLPF8(torch.autograd.Function):
     """Phase 3: the SwiGLU MLP with every GEMM in FP8 -- forward, both dgrads and both wgrads. The forward saves x's
-    and the SwiGLU product's transposed e4m3 bytes (the wgrads' K-major operands), z, and the weights' transposed
-    bytes (the dgrads' B operands)."""
+    and the SwiGLU product's e4m3 bytes (the wgrads' B operands, read with the tokens as K rows), z, and the weights'
+    transposed bytes (the dgrads' B operands)."""
     @staticmethod
     def forward(ctx, x, w12, w3):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        xq, xqt, sx = tcast_t(x2)
+        xq, sx = tcast(x2)
         w12q, w12qt, s12 = tcast_t(w12)
         z = fp8_gemm(xq, sx, w12q, s12)
-        aq, aqt, sa = swiglu_tcast_t(z)
+        aq, sa = swiglu_tcast(z)
         w3q, w3qt, s3 = tcast_t(w3)
         y = fp8_gemm(aq, sa, w3q, s3)
-        ctx.save_for_backward(xqt, sx, z, aqt, sa, w12qt, s12, w3qt, s3)
+        ctx.save_for_backward(xq, sx, z, aq, sa, w12qt, s12, w3qt, s3)
         ctx.shape, ctx.dt = shape, (w12.dtype, w3.dtype)
         return y.view(*shape[:-1], w3.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
-        xqt, sx, z, aqt, sa, w12qt, s12, w3qt, s3 = ctx.saved_tensors
+        xq, sx, z, aq, sa, w12qt, s12, w3qt, s3 = ctx.saved_tensors
         dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
-        dyq, dyqt, sdy = tcast_t(dy2)
+        dyq, sdy = tcast(dy2)
         da = fp8_gemm(dyq, sdy, w3qt, s3, None, False)           # [M, H]
-        dw3 = fp8_gemm(dyqt, sdy, aqt, sa, None, False)          # [C, H]
-        _, dzq, dzqt, sdz = swiglu_bwd_t(z, da, False)   # dz itself is not needed: never written
+        dw3 = fp8_gemm_mn(dyq, sdy, aq, sa)                      # [M, C]^T . [M, H] = [C, H]
+        dzq, sdz = swiglu_bwd_q(z, da)                           # dz itself is not needed: never written
         dx = fp8_gemm(dzq, sdz, w12qt, s12, None, False)         # [M, C]
-        dw12 = fp8_gemm(dzqt, sdz, xqt, sx, None, False)         # [2H, C]
+        dw12 = fp8_gemm_mn(dzq, sdz, xq, sx)                     # [M, 2H]^T . [M, C] = [2H, C]
         return dx.view(ctx.shape), dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1])
 
 

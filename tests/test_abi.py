@@ -71,6 +71,15 @@ def test_validation_codes():
     assert g(wsp, 32, None, wsp, 32, wsp, None, wsp, 16, 4, 16, 32, 1, None, 0, None) == -1
     # empty output: nothing to do
     assert g(None, 32, wsp, None, 32, wsp, None, None, 16, 0, 16, 32, 1, None, 0, None) == 0
+    # MN-major GEMM: M % 16, N % 16, lda >= M, ldb >= N, K * ld < 2^31, null scales, misaligned operand
+    mn = lib.gpic_fp8_gemm_mn
+    assert mn(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 32, 24, 32, 5, None, 0, None) == -3
+    assert mn(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 32, 32, 24, 5, None, 0, None) == -3
+    assert mn(wsp, 16, wsp, wsp, 32, wsp, None, wsp, 32, 32, 32, 5, None, 0, None) == -3
+    assert mn(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 32, 32, 32, 1 << 27, None, 0, None) == -3
+    assert mn(wsp, 32, None, wsp, 32, wsp, None, wsp, 32, 32, 32, 5, None, 0, None) == -1
+    assert mn(wsp + 8, 32, wsp, wsp, 32, wsp, None, wsp, 32, 32, 32, 5, None, 0, None) == -4
+    assert mn(None, 32, wsp, None, 32, wsp, None, None, 32, 0, 32, 5, None, 0, None) == 0
 
 
 def test_single_pass_knob_is_host_only():

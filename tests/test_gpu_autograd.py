@@ -68,6 +68,8 @@ def test_linear_phase3_all_fp8(dev):
     dyq, sdy = G.tcast(dy)
     assert rel(x.grad, deq(dyq, sdy) @ deq(wq, sw)) < 4e-3
     assert rel(w.grad, deq(dyq, sdy).t() @ deq(xq, sx)) < 4e-3
+    # the wgrad from the untransposed bytes is bit for bit the TN GEMM of the transposed bytes
+    assert torch.equal(w.grad, G.fp8_gemm(G.tcast_t(dy)[1], sdy, G.tcast_t(x.detach())[1], sx))
     assert torch.equal(b.grad, dy.sum(0).to(torch.bfloat16))
     # and close to the unquantized bf16 gradients
     assert rel(x.grad, dy.float() @ w.detach().float()) < 0.1
@@ -124,6 +126,9 @@ def test_mlp_phase3_grads_match_quantized_formula(dev):
     _, dzq, sdz = G.swiglu_bwd(z, da)
     assert rel(x.grad, deq(dzq, sdz) @ deq(w12q, s12)) < 4e-3
     assert rel(w12.grad, deq(dzq, sdz).t() @ deq(xq, sx)) < 4e-3
+    # the wgrads from the untransposed bytes are bit for bit the TN GEMMs of the transposed bytes
+    assert torch.equal(w3.grad, G.fp8_gemm(G.tcast_t(dy)[1], sdy, G.swiglu_tcast_t(z)[1], sa))
+    assert torch.equal(w12.grad, G.fp8_gemm(G.swiglu_bwd_t(z, da)[2], sdz, G.tcast_t(x.detach())[1], sx))
 
 
 def test_swiglu_w3_phase1(dev):

@@ -187,3 +187,41 @@ def test_shape_sweep(dev, M, N, K, bias, lda_pad):
         c = c0
     assert_elementwise(c, a, 0.011, b, 0.017)
     assert torch.equal(c, G.fp8_gemm(a, sa, b, sb))
+
+
+@pytest.mark.parametrize("M,N,K,bias,pad", [
+    (3072, 1024, 32768, False, 0),   # d12 qkv wgrad: dW [3N, C] from dY [T, 3N] and X [T, C]
+    (8192, 1024, 32768, False, 0),   # d12 w12 wgrad
+    (1024, 4096, 32768, False, 0),   # d12 w3 wgrad
+    (1024, 1024, 6592, False, 0),    # text-block proj wgrad: split K, partial last K tile
+    (272, 528, 300, True, 0),        # ragged tiles in M and N, K % 16 != 0 (rows past K read as zeros), bias
+    (16, 16, 1, False, 0),           # one K row
+    (4112, 2992, 1040, True, 32),    # padded leading dimensions, bias, partial K tile
+    (9008, 4000, 512, False, 16),    # several work items per CU
+])
+def test_mn_matches_tn(dev, M, N, K, bias, pad):
+    """gpic_fp8_gemm_mn (both operands with K as the row index, the untransposed bytes of the wgrad) gives the same
+    bits as gpic_fp8_gemm on the transposed operands: the MFMA sees the same values at every position (K padded
+    with zeros to a multiple of 16 for the TN call). Elementwise against the float64 product as well."""
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N * 3 + K)
+    a = (torch.randn(K, M + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :M]
+    b = (torch.randn(K, N + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :N]
+    sa = torch.tensor([0.013], device=dev)
+    sb = torch.tensor([0.007], device=dev)
+    bv = (torch.randn(N, generator=g, device=dev) * 0.5).to(torch.bfloat16) if bias else None
+    k16 = (K + 15) // 16 * 16
+    at = torch.zeros(M, k16, dtype=torch.uint8, device=dev)
+    bt = torch.zeros(N, k16, dtype=torch.uint8, device=dev)
+    at[:, :K] = a.view(torch.uint8).t()
+    bt[:, :K] = b.view(torch.uint8).t()
+    want = G.fp8_gemm(at.view(E4), sa, bt.view(E4), sb, bv)
+    pollute(dev)
+    c = G.fp8_gemm_mn(a, sa, b, sb, bv)
+    assert torch.equal(bits_t(c), bits_t(want)), f"{(c != want).sum().item()} elements differ"
+    if not bias and M * N <= 1 << 22:
+        assert_elementwise(c, a.t(), 0.013, b.t(), 0.007)
+    assert torch.equal(c, G.fp8_gemm_mn(a, sa, b, sb, bv))
+
+
+def bits_t(t):
+    return t.view(torch.int16)

@@ -139,6 +139,37 @@ def test_bwd_t_without_dz_matches(dev, M, H):
     assert np.array_equal(qb(dq0), oq) and s0.item() == od
 
 
+@pytest.mark.parametrize("M,H", [(300, 512), (33, 16), (1000, 2064), (4100, 1040)])
+def test_bwd_flat_without_dz_matches(dev, M, H):
+    """swiglu_bwd_q never writes dz: the flat cast recomputes dz from z and da. Same dzq and scale as the path through
+    dz (swiglu_bwd), and as the oracle; row counts that leave the 4-row batches with a remainder."""
+    z = rand_bf16((M, 2 * H), 3.0, seed=M + 2 * H)
+    da = rand_bf16((M, H), 0.05, seed=M + 2 * H + 1)
+    z[0, :5] = torch.tensor([0.0, -0.0, 1e-30, 300.0, -300.0]).to(torch.bfloat16)   # sigmoid outside the table range
+    zd, dad = z.to(dev), da.to(dev)
+    dz, dq, s = G.swiglu_bwd(zd, dad)
+    dq0, s0 = G.swiglu_bwd_q(zd, dad)
+    assert s0.item() == s.item()
+    assert torch.equal(dq0.view(torch.uint8), dq.view(torch.uint8))
+    _, oq, od, _ = O.swiglu_bwd(bits(z), bits(da))
+    assert np.array_equal(qb(dq0), oq) and s0.item() == od
+
+
+def test_bwd_flat_without_dz_full_size(dev):
+    """The d12 shape (M 32768, H 4096) with NaN and inf planted: the flat cast without dz gives the bytes of the
+    path through dz."""
+    g = torch.Generator(device=dev).manual_seed(13)
+    z = (torch.randn(32768, 8192, generator=g, device=dev) * 2).to(torch.bfloat16)
+    da = (torch.randn(32768, 4096, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    z[7, 5] = float("nan")
+    da[200, 9] = -float("inf")
+    z[30000, 100] = float("inf")
+    dz, dq, s = G.swiglu_bwd(z, da)
+    dq0, s0 = G.swiglu_bwd_q(z, da)
+    assert s0.item() == s.item()
+    assert torch.equal(dq0.view(torch.uint8), dq.view(torch.uint8))
+
+
 def test_bwd_t_without_dz_full_size(dev):
     """The d12 shape (M 32768, H 4096) with NaN and inf planted in z and da: both paths give the same bytes."""
     g = torch.Generator(device=dev).manual_seed(12)
