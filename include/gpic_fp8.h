@@ -103,6 +103,9 @@ int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_
  * M..ldt-1 zero): the K-major operand of w3's FP8 wgrad. Same bytes and scale as gpic_fp8_swiglu_tcast.
  *   a  [M, H] bf16, contiguous, or NULL: when given, the SwiGLU product is written there by the amax pass and the
  *      cast reads it instead of recomputing it (the same bytes; faster: the product is computed once)
+ *   qt may be NULL (then ldt == 0, and H % 8 == 0 suffices): q only. With `a` and sq == H the cast is a flat pass
+ *      over the product -- the same bytes as gpic_fp8_swiglu_tcast, which recomputes the product instead (and is the
+ *      slower of the two: measured 270 vs 225 us on d12's [32768, 8192]).
  * No counterpart in the reference (its w3 wgrad is bf16, fp8_native.py:225,265); the FP8-wgrad extension.
  */
 int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint16_t *a, uint8_t *q, int64_t sq,

@@ -549,7 +549,9 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
 
 // The flat cast of dz without dz in memory: dz recomputed from z and da (the same bf16 values as swiglu_bwd_kernel)
 // and cast to dzq [M, 2H] (contiguous) with the scale from swiglu_bwd_kernel<false>'s partial maxima and its
-// sigmoid table. Rows strided over workgroups, kRowsPer rows' loads in flight per thread (as the amax pass).
+// sigmoid table. Rows strided over workgroups, walked row-major two rows at a time: each thread has the loads of
+// two rows x two units in flight (12 x 16 bytes). Measured on the d12 shape: 18% faster than walking each unit
+// down all of the workgroup's rows first (that order left the dzq stores at 4.5 TB/s of combined traffic).
 __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_cast_kernel(const uint16_t *__restrict__ z,
                                                                         const uint16_t *__restrict__ da, int64_t M,
                                                                         int64_t H, int64_t sz, int64_t sda,
@@ -571,27 +573,31 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_cast_kernel(const uin
     __builtin_nontemporal_store(cast8_bf16(h1, scale), reinterpret_cast<u32x2 *>(o));
     __builtin_nontemporal_store(cast8_bf16(h2, scale), reinterpret_cast<u32x2 *>(o + H));
   };
-  for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
-    int64_t r = blockIdx.x;
-    for (; r + (kRowsPer - 1) * rstride < M; r += kRowsPer * rstride) {
-      u32x4 Z1[kRowsPer], Z2[kRowsPer], D[kRowsPer];
+  auto ld = [](const uint16_t *p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p)); };
+  int64_t r = blockIdx.x;
+  for (; r + rstride < M; r += 2 * rstride) {
+    for (int64_t u = threadIdx.x; u < units; u += 2 * blockDim.x) {
+      const bool two = u + blockDim.x < units;   // the thread's second unit of the row exists
+      u32x4 Z1[4], Z2[4], D[4];                  // k: row r + (k / 2) rstride, unit u + (k % 2) blockDim.x
 #pragma unroll
-      for (int k = 0; k < kRowsPer; k++) {
-        const uint16_t *zr = z + (r + k * rstride) * sz + 8 * u;
-        Z1[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr));
-        Z2[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H));
-        D[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + (r + k * rstride) * sda + 8 * u));
+      for (int k = 0; k < 4; k++) {
+        const int64_t rk = r + (k >> 1) * rstride, uk = u + (k & 1) * blockDim.x;
+        const bool ok = (k & 1) == 0 || two;
+        const uint16_t *zr = z + rk * sz + 8 * uk;
+        Z1[k] = ok ? ld(zr) : u32x4{0u, 0u, 0u, 0u};
+        Z2[k] = ok ? ld(zr + H) : u32x4{0u, 0u, 0u, 0u};
+        D[k] = ok ? ld(da + rk * sda + 8 * uk) : u32x4{0u, 0u, 0u, 0u};
       }
 #pragma unroll
-      for (int k = 0; k < kRowsPer; k++) emit(r + k * rstride, u, Z1[k], Z2[k], D[k]);
-    }
-    for (; r < M; r += rstride) {
-      const uint16_t *zr = z + r * sz + 8 * u;
-      emit(r, u, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr)),
-           __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H)),
-           __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(da + r * sda + 8 * u)));
+      for (int k = 0; k < 4; k++)
+        if ((k & 1) == 0 || two) emit(r + (k >> 1) * rstride, u + (k & 1) * blockDim.x, Z1[k], Z2[k], D[k]);
     }
   }
+  for (; r < M; r += rstride)   // the workgroup's last row when it has an odd count
+    for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
+      const uint16_t *zr = z + r * sz + 8 * u;
+      emit(r, u, ld(zr), ld(zr + H), ld(da + r * sda + 8 * u));
+    }
 }
 
 // ------------------------------------------------------------------------------------------- host side
@@ -1201,12 +1207,26 @@ int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz,
                             uint8_t *qt, int64_t ldt, float *dequant, void *ws, void *stream) {
   if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !q)) || (H > 0 && ldt > 0 && !qt))
     return GPIC_EINVAL;
-  if (H % 16 != 0 || sz % 8 != 0 || sq % 8 != 0 || sz < 2 * H || sq < H || ldt % 16 != 0 || ldt < M)
+  if (!qt && ldt != 0) return GPIC_EINVAL;
+  if ((qt ? H % 16 : H % 8) != 0 || sz % 8 != 0 || sq % 8 != 0 || sz < 2 * H || sq < H || ldt % 16 != 0 ||
+      (qt && ldt < M))
     return GPIC_ESHAPE;
   if (!aligned16(z) || !aligned16(a) || !aligned16(q) || !aligned16(qt) || !aligned16(ws)) return GPIC_EALIGN;
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
+  if (!qt) {   // q only: with `a` (and q contiguous) the product is written once and cast flat; else recomputed
+    const bool flat = a && sq == H;
+    swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws), flat ? a : nullptr);
+    if (flat) {
+      const int64_t n = M * H;
+      const int gc = grid_for((n / 16 + kUnroll - 1) / kUnroll, kMaxCastBlocks);
+      cast_kernel<uint16_t><<<gc, kCastThreads, 0, st>>>(a, n, partial, g, q, dequant);
+    } else {
+      swiglu_cast_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, g, q, sq, dequant, ws_table(ws));
+    }
+    return (int)hipGetLastError();
+  }
   // with `a`, the first pass writes the product and the cast reads it; without, the cast recomputes it from z
   swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws), a);
   if (H == 0 || ldt == 0)

@@ -111,17 +111,19 @@ def _swiglu_prep(z):
 @torch.library.custom_op("gpic::fp8_swiglu_tcast", mutates_args=())
 def swiglu_tcast(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """z [M, 2H] bf16 (w12's output) -> silu(z1) * z2 as e4m3 [M, H] and its tensorwise scale [1] fp32.
-    (fp8_native.py:130-144)"""
+    (fp8_native.py:130-144). The product goes through a temporary bf16 buffer (written by the amax pass, cast flat)
+    rather than being computed twice: gpic_fp8_swiglu_tcast_t with qt = NULL, the same bytes."""
     zc = _swiglu_prep(z)
     M, H2 = zc.shape
     H = H2 // 2
     q = torch.empty(M, H, dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
+    a = torch.empty(M, H, dtype=torch.bfloat16, device=z.device)
     with torch.cuda.device(z.device):
         ws = L.cast_workspace(z.device)
-        L.check(L.lib().gpic_fp8_swiglu_tcast(zc.data_ptr(), M, H, zc.stride(0), q.data_ptr(), q.stride(0),
-                                              s.data_ptr(), ws.data_ptr(), L.stream_ptr(z.device)),
-                "gpic_fp8_swiglu_tcast")
+        L.check(L.lib().gpic_fp8_swiglu_tcast_t(zc.data_ptr(), M, H, zc.stride(0), a.data_ptr(), q.data_ptr(),
+                                                q.stride(0), None, 0, s.data_ptr(), ws.data_ptr(),
+                                                L.stream_ptr(z.device)), "gpic_fp8_swiglu_tcast_t")
     return q, s
 
 

@@ -58,6 +58,10 @@ def test_validation_codes():
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 16, 16, wsp, 16, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_bwd(wsp, wsp, 4, 16, 32, 8, wsp, wsp, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_tcast_t(wsp, 40, 16, 32, None, wsp, 16, wsp, 32, wsp, wsp, None) == -3
+    # product cast with qt = NULL (q only): ldt must be 0; H % 8 suffices there, H % 16 with qt
+    assert lib.gpic_fp8_swiglu_tcast_t(wsp, 4, 16, 32, None, wsp, 16, None, 16, wsp, wsp, None) == -1
+    assert lib.gpic_fp8_swiglu_tcast_t(wsp, 4, 24, 48, None, wsp, 24, wsp, 16, wsp, wsp, None) == -3
+    assert lib.gpic_fp8_swiglu_tcast_t(wsp, 4, 12, 24, None, wsp, 16, None, 0, wsp, wsp, None) == -3
     # SwiGLU backward without dz: needs the transposed output (dzqt, ldt > 0); a given dz must be aligned
     b = lib.gpic_fp8_swiglu_bwd_t
     assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, wsp, 0, wsp, wsp, None) == -1

@@ -104,6 +104,35 @@ def test_bwd_matches_oracle(dev, M, H):
     assert np.array_equal(bits(dz), oz) and np.array_equal(qb(dzq), oq) and s.item() == od
 
 
+@pytest.mark.parametrize("M,H", [(300, 512), (33, 8), (4096, 4096)])
+def test_flat_product_cast_paths_agree(dev, M, H):
+    """The three flat product casts give the same bytes and scale: the op's (the product written once to a buffer,
+    then cast flat), gpic_fp8_swiglu_tcast (the product recomputed by the cast) and gpic_fp8_swiglu_tcast_t with
+    qt = NULL, with no buffer and with a buffer but a strided q (both recompute). H = 8 leaves a flat tail."""
+    from gpic_fp8 import _lib as L
+    z = rand_bf16((M, 2 * H), 3.0, seed=M + 3 * H).to(dev)
+    q0, s0 = G.swiglu_tcast(z)
+    lib, ws, st = L.lib(), L.cast_workspace(z.device), L.stream_ptr(z.device)
+    outs = []
+    for mode in ("plain", "t_nobuf", "t_strided"):
+        sq = H + 16 if mode == "t_strided" else H
+        q = torch.zeros(M, sq, dtype=torch.uint8, device=dev)
+        s = torch.empty(1, device=dev)
+        a = torch.empty(M, H, dtype=torch.bfloat16, device=dev) if mode == "t_strided" else None
+        if mode == "plain":
+            rc = lib.gpic_fp8_swiglu_tcast(z.data_ptr(), M, H, 2 * H, q.data_ptr(), sq, s.data_ptr(), ws.data_ptr(), st)
+        else:
+            rc = lib.gpic_fp8_swiglu_tcast_t(z.data_ptr(), M, H, 2 * H, L.ptr(a), q.data_ptr(), sq, None, 0,
+                                             s.data_ptr(), ws.data_ptr(), st)
+        assert rc == 0
+        outs.append((mode, q[:, :H], s))
+    for mode, q, s in outs:
+        assert s.item() == s0.item(), mode
+        assert torch.equal(q, q0.view(torch.uint8)), mode
+    oq, od, _ = O.swiglu_tcast(bits(z))
+    assert s0.item() == od and np.array_equal(qb(q0), oq)
+
+
 def test_transposing_variants(dev):
     M, H = 300, 512
     z = rand_bf16((M, 2 * H), 2.0, seed=9).to(dev)
