@@ -111,17 +111,28 @@ def time_region(fn, steps, warmup):
 
 
 def gemm_operands(G, dev, shapes):
+    """e4m3 operands of each shape in the layout the step gives them: forward and dgrad GEMMs K-major (a [M, K],
+    b [N, K]: fp8_gemm); wgrads MN-major, the untransposed output gradient and input over the tokens (a [K, M],
+    b [K, N]: fp8_gemm_mn)."""
     import torch
     g = torch.Generator(device=dev).manual_seed(1)
     ops = []
     for name, m, n, k in shapes:
-        a = (torch.randn(m, k, generator=g, device=dev)).to(torch.bfloat16)
-        b = (torch.randn(n, k, generator=g, device=dev) / k ** 0.5).to(torch.bfloat16)
+        mn = name.endswith(".wgrad")
+        a = (torch.randn(*((k, m) if mn else (m, k)), generator=g, device=dev)).to(torch.bfloat16)
+        b = (torch.randn(*((k, n) if mn else (n, k)), generator=g, device=dev) / k ** 0.5).to(torch.bfloat16)
         aq, sa = G.tcast(a)
         bq, sb = G.tcast(b)
-        ops.append((aq, sa, bq, sb))
+        ops.append((mn, aq, sa, bq, sb))
         del a, b
     return ops
+
+
+def run_gemm(G, op):
+    mn, aq, sa, bq, sb = op
+    if mn:
+        return G.fp8_gemm_mn(aq, sa, bq, sb)
+    return G.fp8_gemm(aq, sa, bq, sb, None, False)
 
 
 def cpu_baseline():
@@ -211,8 +222,8 @@ def main():
     if args.traffic:
         shapes = gemm_shapes()
         ops = gemm_operands(G, dev, shapes)
-        for aq, sa, bq, sb in ops:
-            G.fp8_gemm(aq, sa, bq, sb, None, False)
+        for op in ops:
+            run_gemm(G, op)
             torch.cuda.synchronize()
         print(json.dumps({"gemm_order": [name for name, *_ in shapes]}), flush=True)
         return
@@ -240,13 +251,13 @@ def main():
     ops = gemm_operands(G, dev, shapes)
 
     def gemms():
-        for aq, sa, bq, sb in ops:
-            G.fp8_gemm(aq, sa, bq, sb, None, False)
+        for op in ops:
+            run_gemm(G, op)
 
     gemm_ms = time_region(gemms, max(args.steps, 10), 3)
     per_shape = {}
-    for (name, m, n, k), (aq, sa, bq, sb) in zip(shapes, ops):
-        tm = time_region(lambda: G.fp8_gemm(aq, sa, bq, sb, None, False), 10, 2)
+    for (name, m, n, k), op in zip(shapes, ops):
+        tm = time_region(lambda: run_gemm(G, op), 10, 2)
         per_shape[name] = {"M": m, "N": n, "K": k, "us": round(tm * 1e3, 1),
                            "tflops": round(2.0 * m * n * k / tm / 1e9, 1)}
 
@@ -289,8 +300,12 @@ def main():
     hip = None
     if not args.no_compare:
         try:
+            # hipBLASLt takes A row-major and B column-major: the wgrads get transposed copies (outside the timing)
+            tn = [(aq.t().contiguous(), sa, bq.t().contiguous(), sb) if mn else (aq, sa, bq, sb)
+                  for mn, aq, sa, bq, sb in ops]
+
             def blaslt():
-                for aq, sa, bq, sb in ops:
+                for aq, sa, bq, sb in tn:
                     torch._scaled_mm(aq, bq.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
             hip_ms = time_region(blaslt, max(args.steps, 10), 3)
             hip = {"gemm_tflops": round(fl / hip_ms / 1e9, 1), "gemm_ms": round(hip_ms, 4)}
@@ -324,7 +339,8 @@ def main():
         "pct_fp8_peak": round(100.0 * fl / ms / 1e9 / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_FP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "gemm_tn_kernel (+ split-K reduce)", "launches_per_step": len(shapes),
+                     "kernel": "gemm_tn_kernel (K-major fwd / dgrad, MN-major wgrad instances; + split-K reduce)",
+                     "launches_per_step": len(shapes),
                      "avg_launch_us": round(gemm_ms * 1e3 / len(shapes), 1), "gemm_ms_per_step": round(gemm_ms, 4),
                      "per_shape": per_shape},
         "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale", "us": round(cast_ms * 1e3, 2),
