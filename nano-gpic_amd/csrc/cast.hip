@@ -829,6 +829,8 @@ constexpr int kOnceWords = sizeof(T) == 2 ? 16 : 12;   // 16-byte words a thread
                                                         // which its wider narrowing code needs to fit 128 VGPRs)
 constexpr int kOnceTiles = 2;       // 128 x 128 bf16 tiles a workgroup of the transposing kernel holds (64 VGPRs)
 constexpr int kHybridTiles = 8;     // the transposing kernel takes up to this many tiles per workgroup (2 held)
+constexpr int kHybridFlat = 8;      // the flat kernel takes up to this many times the words it can hold
+constexpr int kStream = 8;          // streamed words in flight per thread (flat hybrid)
 constexpr int kOnceWaitUs = 200;
 
 // A uniform index the compiler must treat as new here, so it recomputes the addresses derived from it instead of
@@ -947,17 +949,38 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, uint32_t tag, void *ws
 }
 
 // Flat single-pass cast. x as nw 16-byte words (8 bf16 or 4 fp32 elements) plus `tail` (< 8 or < 4) elements;
-// workgroup b owns words [b P, (b + 1) P), P = 256 wpt, thread t words b P + 256 j + t, j < wpt <= kOnceWords<T>.
+// workgroup b holds words [b P, (b + 1) P), P = 256 wpt, thread t words b P + 256 j + t, j < wpt <= kOnceWords<T>.
+// Hybrid (sgroups > 0, x larger than the grid holds): the 256-word groups past the held words, G P + 256 s + t, are
+// streamed by workgroup s % G twice -- for the maximum, then (last first, for MALL hits) for the cast -- so only
+// what does not fit is read twice.
 template <typename T>
 __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__ x, int64_t n, int wpt,
-                                                           uint8_t *__restrict__ q, float *__restrict__ dequant,
-                                                           void *ws, uint32_t tag, uint32_t wait_ticks) {
+                                                           int64_t sgroups, uint8_t *__restrict__ q,
+                                                           float *__restrict__ dequant, void *ws, uint32_t tag,
+                                                           uint32_t wait_ticks) {
   constexpr int kE = 16 / sizeof(T);   // elements per word
   const int64_t nw = n / kE;
   const int tail = (int)(n % kE);
   const u32x4 *xv = reinterpret_cast<const u32x4 *>(x);
   const int64_t P = 256 * (int64_t)wpt;
+  const int64_t G = gridDim.x;
   auto word = [&](int64_t b, int j) { return b * P + 256 * j + threadIdx.x; };
+  // streamed word index (below 2^31: a hybrid x is at most kHybridFlat x 4 Mi words)
+  auto sword = [&](int64_t s) { return (uint32_t)(G * P + 256 * s) + threadIdx.x; };
+  // the streamed groups' maximum of workgroup b
+  auto stream_amax = [&](int64_t b) {
+    uint32_t a = 0;
+    for (int64_t s = b; s < sgroups; s += kStream * G) {
+      u32x4 S[kStream];
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const int64_t sk = s + k * G, i = sword(sk);
+        S[k] = sk < sgroups && i < nw ? __builtin_nontemporal_load(xv + i) : u32x4{0u, 0u, 0u, 0u};
+      }
+      a = max(a, words_amax<T, kStream>(S));
+    }
+    return a;
+  };
   constexpr int kW = kOnceWords<T>;
   u32x4 w[kW];
 #pragma unroll
@@ -976,22 +999,26 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
     }
     return a;
   };
-  const uint32_t m = block_max_u32(max(words_amax<T, kW>(w), tail_amax()));
+  uint32_t m0 = max(words_amax<T, kW>(w), tail_amax());
+  if (sgroups > 0) m0 = max(m0, stream_amax(blockIdx.x));
+  const uint32_t m = block_max_u32(m0);
   const uint32_t g = once_fold(m, tag, ws, wait_ticks, [&](int c) {
     uint32_t a = tail_amax();
     for (int j = 0; j < wpt; j++) {
       const int64_t i = word(c, j);
       if (i < nw) a = max(a, word_amax_exact<T>(__builtin_nontemporal_load(xv + i)));
     }
+    if (sgroups > 0) a = max(a, stream_amax(c));
     return block_max_u32(a);
   });
   hold(w);
   float scale, deq;
   scales_from_amax(g, scale, deq);
   if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  const int64_t b2 = opaque_s64(blockIdx.x);   // the store addresses are recomputed, not kept from the loads
 #pragma unroll
   for (int j = 0; j < kW; j++) {
-    const int64_t i = word(blockIdx.x, j);
+    const int64_t i = word(b2, j);
     if (j < wpt && i < nw) {
       if constexpr (sizeof(T) == 2) __builtin_nontemporal_store(cast8_bf16(w[j], scale), reinterpret_cast<u32x2 *>(q) + i);
       else __builtin_nontemporal_store(cast4_f32(w[j], scale), reinterpret_cast<uint32_t *>(q) + i);
@@ -1001,6 +1028,26 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
     const int64_t i = nw * kE + threadIdx.x;
     const float v = sizeof(T) == 2 ? bf16_lo(reinterpret_cast<const uint16_t *>(x)[i]) : reinterpret_cast<const float *>(x)[i];
     q[i] = (uint8_t)e4m3x4(sat(v * scale), 0.f, 0.f, 0.f);
+  }
+  // hybrid: the streamed groups again, this workgroup's last first, kStream loads in flight
+  if (sgroups > (int64_t)blockIdx.x) {
+    const int64_t cnt = (sgroups - 1 - blockIdx.x) / G + 1;   // streamed groups of this workgroup
+    for (int64_t k0 = cnt - 1; k0 >= 0; k0 -= kStream) {
+      u32x4 S[kStream];
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const int64_t i = sword(blockIdx.x + (k0 - k) * G);
+        S[k] = k0 - k >= 0 && i < nw ? __builtin_nontemporal_load(xv + i) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const int64_t i = sword(blockIdx.x + (k0 - k) * G);
+        if (k0 - k >= 0 && i < nw) {
+          if constexpr (sizeof(T) == 2) __builtin_nontemporal_store(cast8_bf16(S[k], scale), reinterpret_cast<u32x2 *>(q) + i);
+          else __builtin_nontemporal_store(cast4_f32(S[k], scale), reinterpret_cast<uint32_t *>(q) + i);
+        }
+      }
+    }
   }
 }
 
@@ -1101,18 +1148,25 @@ static int once_capacity(const void *kernel, int *cache) {
 // s_memrealtime counts at 100 MHz on this target
 static uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us) * 100u; }
 
-// The single-pass flat cast when x fits (false, nothing launched, when it does not).
+// The single-pass flat cast when x fits, as a hybrid up to kHybridFlat times that (false, nothing launched, above).
 template <typename T>
 static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant, void *ws, hipStream_t st) {
   static int cache = -1;
   const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T>), &cache);
   constexpr int kE = 16 / sizeof(T);
   const int64_t nw = n / kE;
-  if (!g_once_enabled || cap <= 0 || n <= 0 || nw > (int64_t)kOnceWords<T> * 256 * cap) return false;
+  const int64_t held = (int64_t)kOnceWords<T> * 256 * cap;   // words the grid holds in registers
+  if (!g_once_enabled || cap <= 0 || n <= 0 || nw > kHybridFlat * held) return false;
+  if (nw > held) {   // hybrid: every workgroup holds its full share, the rest is streamed
+    const int64_t sgroups = (nw - held + 255) / 256;
+    cast_once_kernel<T><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_next_tag(),
+                                             once_wait_ticks());
+    return true;
+  }
   const int64_t groups = std::max<int64_t>(1, (nw + 255) / 256);   // 256-word groups
   const int grid = (int)std::min<int64_t>(groups, cap);
   const int wpt = (int)((groups + grid - 1) / grid);
-  cast_once_kernel<T><<<grid, 256, 0, st>>>(x, n, wpt, q, dequant, ws, once_next_tag(), once_wait_ticks());
+  cast_once_kernel<T><<<grid, 256, 0, st>>>(x, n, wpt, 0, q, dequant, ws, once_next_tag(), once_wait_ticks());
   return true;
 }
 

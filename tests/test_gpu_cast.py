@@ -192,8 +192,10 @@ def single_pass_default():
 
 def test_single_pass_taken_when_the_tensor_fits(dev, single_pass_default):
     """Config 2 ([32768 x 1024] bf16) fits the single-pass kernels (64 MiB held in registers): the flat and the
-    transposing cast each write new tagged partials and match the oracle; a tensor of 3x the size takes the two-pass
-    path (the partial words unchanged) with the oracle's bytes. No partial had to be computed from x."""
+    transposing cast each write new tagged partials and match the oracle; a tensor of 3x the size takes the flat
+    hybrid (held + streamed, new tags) with the oracle's bytes; one of 9x (past the hybrid's 8x) takes the two-pass
+    path (the partial words unchanged): three copies of the 3x tensor, so its bytes are three copies of the 3x result.
+    No partial had to be computed from x."""
     x = config2_input()
     xh = bits(x)
     oq, od, _ = O.tcast(xh)
@@ -211,9 +213,15 @@ def test_single_pass_taken_when_the_tensor_fits(dev, single_pass_default):
     big = torch.cat([xd, xd * 2, xd * 0.5], dim=1)
     q, s = G.tcast(big)
     w3, f3 = once_state(dev)
-    assert w3 == w2 and f3 == f0
+    assert w3 >> 32 != w2 >> 32 and f3 == f0
     oq, od, _ = O.tcast(bits(big.cpu()))
     assert s.item() == od and np.array_equal(qb(q), oq)
+    huge = big.repeat(1, 3)
+    qh, sh = G.tcast(huge)
+    w4, f4 = once_state(dev)
+    assert w4 == w3 and f4 == f0
+    assert sh.item() == s.item()
+    assert torch.equal(qh.view(torch.uint8).view(32768, 3, 3072), q.view(torch.uint8).unsqueeze(1).expand(-1, 3, -1))
 
 
 def test_single_pass_direct_fallback_and_two_pass_agree(dev, single_pass_default):
@@ -250,7 +258,8 @@ def test_single_pass_direct_fallback_and_two_pass_agree(dev, single_pass_default
 @pytest.mark.parametrize("n", [41_000_007, 1_000_003])
 def test_nan_inf_tail_both_paths(dev, n):
     """NaNs (ignored by the amax), an odd tail (n % 16 != 0) and a planted maximum, on a flat bf16 tensor above the
-    single-pass capacity (two passes) and one below it (single pass): bytes and scale equal the oracle's."""
+    single-pass capacity (the hybrid: held words + streamed ones) and one below it (single pass): bytes and scale equal
+    the oracle's."""
     g = torch.Generator(device=dev).manual_seed(n)
     x = (torch.randn(n, generator=g, device=dev) * 3).to(torch.bfloat16)
     x[::1_000_001] = float("nan")
@@ -262,7 +271,7 @@ def test_nan_inf_tail_both_paths(dev, n):
 
 
 def test_fp32_weight_both_paths(dev):
-    """fp32 (DDP) weights: [2048 x 4096] fits the single-pass fp32 kernel, [5000 x 4096] does not."""
+    """fp32 (DDP) weights: [2048 x 4096] fits the single-pass fp32 kernel, [5000 x 4096] takes its hybrid."""
     for rows in (2048, 5000):
         w = torch.randn(rows, 4096, device=dev) / 64
         w[rows // 2, 7] = -3.5
@@ -277,7 +286,7 @@ def test_single_pass_back_to_back_calls(dev):
     the power-of-two scale invariance (same bytes, dequant scale times 2^k)."""
     g = torch.Generator(device=dev).manual_seed(5)
     x = (torch.randn(4096, 1024, generator=g, device=dev) * 2).to(torch.bfloat16)
-    y = (torch.randn(6000, 8192, generator=g, device=dev)).to(torch.bfloat16)   # 49M elements: two passes
+    y = (torch.randn(6000, 8192, generator=g, device=dev)).to(torch.bfloat16)   # 49M elements: the flat hybrid
     outs = []
     for i in range(40):
         k = i % 5 - 2
@@ -325,6 +334,38 @@ def test_single_pass_concurrent_streams(dev, single_pass_default):
         rq, rqt, rs = ref_t[2 - i % 3]
         assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
         assert torch.equal(qt.view(torch.uint8), rqt.view(torch.uint8))
+
+
+@pytest.mark.parametrize("shape,dtype", [((32768, 3072), torch.bfloat16), ((41_000_009,), torch.bfloat16),
+                                         ((8192, 4096), torch.float32), ((4_194_304 * 8 * 8,), torch.bfloat16)])
+def test_flat_hybrid_matches_two_pass(dev, shape, dtype, single_pass_default):
+    """Flat casts above the single-pass capacity and up to 8x it take the hybrid (every workgroup holds its share,
+    the rest is streamed twice): the same bytes and scale as the forced two-pass path and as the zero-wait path
+    (missing partials, streamed part included, computed from x), with a NaN, an infinity and an odd tail; the
+    [32768 x 3072] dY of qkv and the exact 8x edge (268M elements) included, the first also against the oracle."""
+    g = torch.Generator(device=dev).manual_seed(len(shape) + shape[0])
+    x = (torch.randn(*shape, generator=g, device=dev) * 4).to(dtype)
+    flat = x.view(-1)
+    flat[flat.numel() // 3] = float("nan")
+    flat[flat.numel() - 1] = 1.0e4
+    flat[flat.numel() // 2] = -float("inf") if dtype == torch.float32 else -3.0e3
+    outs = []
+    for enabled, wait in ((True, -1), (False, -1), (True, 0)):
+        L.set_single_pass(enabled, wait)
+        _, f0 = once_state(dev)
+        q, s = G.tcast(x)
+        _, f1 = once_state(dev)
+        if enabled and wait == 0:
+            assert f1 > f0
+        outs.append((q.view(torch.uint8).clone(), s.item()))
+        del q
+    L.set_single_pass(True, -1)
+    q0, s0 = outs[0]
+    for q, s in outs[1:]:
+        assert s == s0 and torch.equal(q, q0)
+    if shape == (32768, 3072):
+        oq, od, _ = O.tcast(bits(x.cpu()))
+        assert s0 == od and np.array_equal(q0.cpu().numpy(), oq)
 
 
 @pytest.mark.parametrize("rows,cols", [(5000, 7008), (9000, 9008), (32768, 3072), (32768, 4096)])
