@@ -154,21 +154,26 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(const T *__restrict_
 // sigmoid(z1) for the bf16 values z1 with exponent field in [kLutELo, kLutEHi], i.e. 2^-16 <= |z1| < 2^8, both signs
 // (6144 floats = 24 KiB of LDS). Each workgroup fills its table with the same sigmoid() the other values use, so a
 // lookup returns exactly what the computation would; values outside the range (rare: tiny, huge, zero, NaN) are
-// computed directly.
+// computed directly. Entry r holds the value whose bf16 bits, rotated left by one (sign to bit 0), are
+// r + (kLutELo << 8): the index of a value is then a 16-bit rotate, subtract and clamp, done for both halves of a
+// 32-bit word of bf16 at once with packed 16-bit instructions. The clamp sends values outside the table to entry
+// kLutSize, which the LDS copy holds as -1 (no sigmoid is negative): that marks them for direct computation.
 constexpr int kLutELo = 111, kLutEHi = 134;
 constexpr int kLutHalf = (kLutEHi - kLutELo + 1) * 128;
 constexpr int kLutSize = 2 * kLutHalf;
+constexpr int kLutLds = kLutSize + 4;   // LDS copy: the table, the sentinel, padding
 static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kCastWorkspaceBytes, "cast workspace too small");
+static_assert((kLutELo << 8) + kLutSize <= 0x10000, "table indices are 16-bit");
 
 // The workspace: partial maxima at the start, the sigmoid table after them.
 __host__ __device__ inline float *ws_table(void *ws) { return reinterpret_cast<float *>((char *)ws + kMaxParts * 4); }
 
 __device__ __forceinline__ void lut_build(float *lut) {
   for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) {
-    const uint32_t neg = i >= kLutHalf;
-    const uint32_t mag = (kLutELo << 7) + (uint32_t)(i - (neg ? kLutHalf : 0));
-    lut[i] = sigmoid(bf16_lo(mag | (neg << 15)));
+    const uint32_t h = (uint32_t)(i + (kLutELo << 8));        // rotated bits
+    lut[i] = sigmoid(bf16_lo((h >> 1) | ((h & 1u) << 15)));
   }
+  if (threadIdx.x == 0) lut[kLutSize] = -1.0f;
   __syncthreads();
 }
 
@@ -176,6 +181,7 @@ __device__ __forceinline__ void lut_build(float *lut) {
 __device__ __forceinline__ void lut_load(float *lut, const float *__restrict__ g) {
   for (int i = threadIdx.x; i < kLutSize / 4; i += blockDim.x)
     reinterpret_cast<u32x4 *>(lut)[i] = reinterpret_cast<const u32x4 *>(g)[i];
+  if (threadIdx.x == 0) lut[kLutSize] = -1.0f;
   __syncthreads();
 }
 
@@ -184,19 +190,21 @@ __device__ __forceinline__ void sigmoid8(const float *lut, u32x4 w, const float 
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
   bool slow = false;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const uint32_t h = (ws[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-    const uint32_t idx = (h & 0x7fffu) - (uint32_t)(kLutELo << 7);   // unsigned: below the range wraps high
-    const bool in = idx < (uint32_t)kLutHalf;
-    sg[i] = lut[in ? idx + ((h >> 15) ? kLutHalf : 0) : 0];
-    slow |= !in;
+  for (int j = 0; j < 4; j++) {
+    u16x2 h = __builtin_bit_cast(u16x2, ws[j]);
+    h = (h << (uint16_t)1) | (h >> (uint16_t)15);
+    h = h - (uint16_t)(kLutELo << 8);                            // below the table wraps high
+    h = __builtin_elementwise_min(h, (u16x2)(uint16_t)kLutSize);  // past it: the sentinel
+    const uint32_t r = __builtin_bit_cast(uint32_t, h);
+    sg[2 * j] = lut[r & 0xffffu];
+    sg[2 * j + 1] = lut[r >> 16];
   }
+#pragma unroll
+  for (int i = 0; i < 8; i++) slow |= sg[i] < 0.0f;
   if (slow) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t h = (ws[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-      if ((h & 0x7fffu) - (uint32_t)(kLutELo << 7) >= (uint32_t)kLutHalf) sg[i] = sigmoid(z[i]);
-    }
+    for (int i = 0; i < 8; i++)
+      if (sg[i] < 0.0f) sg[i] = sigmoid(z[i]);
   }
 }
 
@@ -209,14 +217,25 @@ __device__ __forceinline__ void unpack8(u32x4 w, float (&v)[8]) {
   }
 }
 
-// a = bf16(bf16(z1 * sigmoid(z1)) * z2) for 8 pairs (fp8_native.py:55-58); returns exact bf16 values as fp32.
-__device__ __forceinline__ void swiglu8(const float *lut, u32x4 z1w, u32x4 z2w, float (&a)[8]) {
+// a = bf16(bf16(z1 * sigmoid(z1)) * z2) for 8 pairs (fp8_native.py:55-58) as 4 words of packed bf16 (each
+// rounding done for two values by one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ u32x4 swiglu8_words(const float *lut, u32x4 z1w, u32x4 z2w) {
   float z1[8], z2[8], sg[8];
   unpack8(z1w, z1);
   unpack8(z2w, z2);
   sigmoid8(lut, z1w, z1, sg);
+  u32x4 a;
 #pragma unroll
-  for (int i = 0; i < 8; i++) a[i] = bf16_round(bf16_round(z1[i] * sg[i]) * z2[i]);
+  for (int j = 0; j < 4; j++) {
+    const uint32_t sl = pack_bf16(z1[2 * j] * sg[2 * j], z1[2 * j + 1] * sg[2 * j + 1]);
+    a[j] = pack_bf16(bf16_lo(sl) * z2[2 * j], bf16_hi(sl) * z2[2 * j + 1]);
+  }
+  return a;
+}
+
+// The same as exact bf16 values in fp32.
+__device__ __forceinline__ void swiglu8(const float *lut, u32x4 z1w, u32x4 z2w, float (&a)[8]) {
+  unpack8(swiglu8_words(lut, z1w, z2w), a);
 }
 
 __device__ __forceinline__ uint32_t absbits_nonan(float v) {
@@ -291,7 +310,7 @@ __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int6
   __shared__ uint32_t tile[kTT * kPitch];      // [row][col / 4] e4m3 bytes
   const float *lut = nullptr;
   if constexpr (Src::kLut) {
-    __shared__ float table[kLutSize];
+    __shared__ float table[kLutLds];
     lut_load(table, src.table);
     lut = table;
   }
@@ -370,17 +389,25 @@ __global__ __launch_bounds__(256) void cast_t_kernel(Src src, int64_t rows, int6
 constexpr int kRowsPer = 4;
 
 // Partial maxima of the SwiGLU product a; when `a` is given, also writes a ([M, H] bf16, contiguous; its values are
-// bf16 already, so the write is exact) for a cast that then reads it instead of recomputing it.
+// bf16 already, so the write is exact) for a cast that then reads it instead of recomputing it. The maximum is taken
+// on the packed bf16 magnitudes (one v_pk_max_u16 per two values); a thread whose maximum is a NaN pattern folds its
+// rows again element by element without the NaNs (tl.max is maxnum).
 __global__ __launch_bounds__(kCastThreads) void swiglu_amax_kernel(const uint16_t *__restrict__ z, int64_t M, int64_t H,
                                                                     int64_t sz, uint32_t *__restrict__ partial,
                                                                     float *__restrict__ table, uint16_t *__restrict__ a) {
-  __shared__ float lut[kLutSize];
+  __shared__ float lut[kLutLds];
   lut_build(lut);
   if (blockIdx.x == 0 && table)
     for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) table[i] = lut[i];
   const int64_t units = H / 8;
   const int64_t rstride = gridDim.x;
-  uint32_t m = 0;
+  uint32_t m16 = 0;   // packed maxima of |bf16 a| (NaN patterns included)
+  auto unit = [&](int64_t r, int64_t u, u32x4 z1, u32x4 z2) {
+    const u32x4 aw = swiglu8_words(lut, z1, z2);
+#pragma unroll
+    for (int j = 0; j < 4; j++) m16 = pk_max_u16(m16, aw[j] & 0x7fff7fffu);
+    if (a) *reinterpret_cast<u32x4 *>(a + r * H + 8 * u) = aw;
+  };
   for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
     int64_t r = blockIdx.x;
     for (; r + (kRowsPer - 1) * rstride < M; r += kRowsPer * rstride) {
@@ -392,27 +419,27 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_amax_kernel(const uint16_
         z2[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u));
       }
 #pragma unroll
-      for (int k = 0; k < kRowsPer; k++) {
-        float v[8];
-        swiglu8(lut, z1[k], z2[k], v);
-#pragma unroll
-        for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(v[i]));
-        if (a)
-          *reinterpret_cast<u32x4 *>(a + (r + k * rstride) * H + 8 * u) =
-              u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
-      }
+      for (int k = 0; k < kRowsPer; k++) unit(r + k * rstride, u, z1[k], z2[k]);
     }
     for (; r < M; r += rstride) {
       const uint16_t *zr = z + r * sz;
-      float v[8];
-      swiglu8(lut, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u)),
-              __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u)), v);
-#pragma unroll
-      for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(v[i]));
-      if (a)
-        *reinterpret_cast<u32x4 *>(a + r * H + 8 * u) =
-            u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
+      unit(r, u, __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + 8 * u)),
+           __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(zr + H + 8 * u)));
     }
+  }
+  uint32_t m = max(m16 & 0xffffu, m16 >> 16);
+  if (m > 0x7f80u) {   // rare: a NaN among this thread's products; fold them again without it
+    m = 0;
+    for (int64_t u = threadIdx.x; u < units; u += blockDim.x)
+      for (int64_t r = blockIdx.x; r < M; r += rstride) {
+        const uint16_t *zr = z + r * sz;
+        float v[8];
+        swiglu8(lut, *reinterpret_cast<const u32x4 *>(zr + 8 * u), *reinterpret_cast<const u32x4 *>(zr + H + 8 * u), v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) m = max(m, absbits_nonan(v[i]));
+      }
+  } else {
+    m <<= 16;
   }
   m = block_max_u32(m);
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
@@ -423,7 +450,7 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_cast_kernel(const uint16_
                                                                     int nparts, uint8_t *__restrict__ q, int64_t sq,
                                                                     float *__restrict__ dequant,
                                                                     const float *__restrict__ table) {
-  __shared__ float lut[kLutSize];
+  __shared__ float lut[kLutLds];
   lut_load(lut, table);
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);
@@ -455,9 +482,12 @@ __device__ __forceinline__ void dz_words(const float *lut, u32x4 z1v, u32x4 z2v,
   sigmoid8(lut, z1v, z1, sg);
   float d1[8], d2[8];
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    d1[i] = dz1_of(z1[i], z2[i], dv[i], sg[i]);
-    d2[i] = dz2_of(z1[i], dv[i], sg[i]);
+  for (int i = 0; i < 8; i++) d1[i] = dz1_of(z1[i], z2[i], dv[i], sg[i]);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {   // dz2_of with the bf16(z1 * sg) of two values rounded by one instruction
+    const uint32_t sl = pack_bf16(z1[2 * j] * sg[2 * j], z1[2 * j + 1] * sg[2 * j + 1]);
+    d2[2 * j] = dv[2 * j] * bf16_lo(sl);
+    d2[2 * j + 1] = dv[2 * j + 1] * bf16_hi(sl);
   }
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -478,7 +508,7 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_kernel(const uint16_t
                                                                    int64_t sz, int64_t sda, uint16_t *__restrict__ dz,
                                                                    int64_t sdz, uint32_t *__restrict__ partial,
                                                                    float *__restrict__ table) {
-  __shared__ float lut[kLutSize];
+  __shared__ float lut[kLutLds];
   lut_build(lut);
   if (blockIdx.x == 0 && table)
     for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) table[i] = lut[i];
@@ -559,7 +589,7 @@ __global__ __launch_bounds__(kCastThreads) void swiglu_bwd_cast_kernel(const uin
                                                                         const float *__restrict__ table,
                                                                         uint8_t *__restrict__ dzq,
                                                                         float *__restrict__ dequant) {
-  __shared__ float lut[kLutSize];
+  __shared__ float lut[kLutLds];
   lut_load(lut, table);
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);
@@ -751,7 +781,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_cast_t_kernel(const uint16_t *
                                                                 const float *__restrict__ table, uint8_t *__restrict__ dzq,
                                                                 uint8_t *__restrict__ dzqt, int64_t ldt,
                                                                 float *__restrict__ dequant) {
-  __shared__ float lut[kLutSize];
+  __shared__ float lut[kLutLds];
   __shared__ uint32_t tile[kTT * kTPitch];
   lut_load(lut, table);
   float scale, deq;
