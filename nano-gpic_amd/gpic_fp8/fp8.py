@@ -1,6 +1,7 @@
 """Recipe dispatcher of the FP8 path (baselines/PixelGen/src/utils/fp8.py:13-56): "native" / "native2" convert the
-image blocks with convert_native (phase 1 / 2), "native3" with every GEMM in FP8 (phase 3). Any other recipe name is a
-torchao Float8Linear recipe in the reference; torchao is not part of this build and such a recipe raises ImportError.
+image blocks with convert_native (phase 1 / 2), "native3" with every GEMM in FP8 (phase 3), "native3+text" also the
+image blocks' kv_y and the text-refine blocks' linears (phase 3, convert_native(text=True)). Any other recipe name is
+a torchao Float8Linear recipe in the reference; torchao is not part of this build and such a recipe raises ImportError.
 """
 import os
 import sys
@@ -11,7 +12,7 @@ from .fp8_native import convert_native
 
 _PATH = os.environ.get("GPIC_TORCHAO_PATH", "")
 KEEP = ("adaLN_modulation",)
-NATIVE = {"native": 1, "native2": 2, "native3": 3}
+NATIVE = {"native": (1, False), "native2": (2, False), "native3": (3, False), "native3+text": (3, True)}
 
 
 def _torchao():
@@ -41,9 +42,11 @@ def convert_fp8(net, recipe):
     number of GEMMs (native recipes) or Linear layers (torchao recipes) converted."""
     if recipe in NATIVE:
         keys = set(net.state_dict())
-        n = convert_native(net, phase=NATIVE[recipe])
+        phase, text = NATIVE[recipe]
+        n = convert_native(net, phase=phase, text=text)
         assert set(net.state_dict()) == keys, "FP8 conversion changed the state-dict keys"
-        print(f"FP8 ({recipe}, MI355X native): {n} GEMMs of the image blocks converted", flush=True)
+        where = "image and text blocks" if text else "image blocks"
+        print(f"FP8 ({recipe}, MI355X native): {n} GEMMs of the {where} converted", flush=True)
         return n
     _torchao()
     from torchao.float8 import convert_to_float8_training, Float8LinearConfig

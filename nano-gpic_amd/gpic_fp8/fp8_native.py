@@ -519,37 +519,56 @@ class Fp8LinearF8(torch.nn.Linear):
         return fp8_linear_f8(x, self.weight, self.bias)
 
 
-def convert_native(net, phase=1):
+def _fp8_ok(lin):
+    """An nn.Linear the FP8 GEMM can take: in and out features multiples of 16 (fp8.py:35's rule)."""
+    return type(lin) is torch.nn.Linear and lin.in_features % 16 == 0 and lin.out_features % 16 == 0
+
+
+def _convert_block(blk, phase, attn_names):
+    """One block's attention linears `attn_names` and its SwiGLU MLP (w12, w3), as convert_native describes."""
+    n = 0
+    mlp = blk.mlp
+    mlp_ok = _fp8_ok(mlp.w12) and _fp8_ok(mlp.w3) and mlp.w12.out_features % 32 == 0
+    if phase >= 2:
+        lin_cls = Fp8LinearF8 if phase >= 3 else Fp8Linear
+        mlp_fn = fp8_mlp_f8 if phase >= 3 else fp8_mlp
+        for name in attn_names:
+            lin = getattr(blk.attn, name, None)
+            if _fp8_ok(lin):
+                lin.__class__ = lin_cls
+                n += 1
+        if mlp_ok and not getattr(mlp, "_fp8", False):
+            mlp._fp8 = True
+            mlp.forward = (lambda m, f: (lambda x: f(x, m.w12.weight, m.w3.weight)))(mlp, mlp_fn)
+            n += 2
+        return n
+    for parent, name in [(blk.attn, a) for a in attn_names] + [(mlp, "w12")]:
+        lin = getattr(parent, name, None)
+        if _fp8_ok(lin):
+            lin.__class__ = Fp8Linear
+            n += 1
+    if mlp_ok and not getattr(mlp, "_fp8", False):
+        mlp._fp8 = True
+        mlp.forward = (lambda m: (lambda x: fp8_swiglu_w3(m.w12(x), m.w3.weight)))(mlp)
+        n += 1
+    return n
+
+
+def convert_native(net, phase=1, text=False):
     """Phase 1: the image blocks' qkv_x, proj, w12 to Fp8Linear and their SwiGLU's w3 GEMM to the fused path. Phase 2:
     qkv_x and proj as in phase 1, the MLP as one fused FP8 function with FP8 dgrads. Phase 3: qkv_x and proj to
     Fp8LinearF8, the MLP as one function with every GEMM in FP8. Returns the count of GEMMs converted
-    (fp8_native.py:290-317)."""
+    (fp8_native.py:290-317).
+    text=True (an extension: the reference's native recipes convert the image blocks only, fp8_native.py:294, while its
+    torchao filter also takes the text-refine blocks, fp8.py:31) converts, in the same phase, the image blocks' kv_y
+    (over the text tokens) and the text-refine blocks' attention qkv, proj and SwiGLU MLP (JiT_T2I.py:131,227,231,274):
+    linears of M = batch x text tokens, which the same kernels serve."""
     n = 0
     for blk in getattr(net, "blocks", []):
-        if phase >= 2:
-            lin_cls = Fp8LinearF8 if phase >= 3 else Fp8Linear
-            mlp_fn = fp8_mlp_f8 if phase >= 3 else fp8_mlp
-            for name in ("qkv_x", "proj"):
-                lin = getattr(blk.attn, name)
-                if type(lin) is torch.nn.Linear:
-                    lin.__class__ = lin_cls
-                    n += 1
-            mlp = blk.mlp
-            if not getattr(mlp, "_fp8", False):
-                mlp._fp8 = True
-                mlp.forward = (lambda m, f: (lambda x: f(x, m.w12.weight, m.w3.weight)))(mlp, mlp_fn)
-                n += 2
-            continue
-        for parent, name in ((blk.attn, "qkv_x"), (blk.attn, "proj"), (blk.mlp, "w12")):
-            lin = getattr(parent, name)
-            if type(lin) is torch.nn.Linear:
-                lin.__class__ = Fp8Linear
-                n += 1
-        mlp = blk.mlp
-        if not getattr(mlp, "_fp8", False):
-            mlp._fp8 = True
-            mlp.forward = (lambda m: (lambda x: fp8_swiglu_w3(m.w12(x), m.w3.weight)))(mlp)
-            n += 1
+        n += _convert_block(blk, phase, ("qkv_x", "proj", "kv_y") if text else ("qkv_x", "proj"))
+    if text:
+        for blk in getattr(net, "text_refine_blocks", []):
+            n += _convert_block(blk, phase, ("qkv", "proj"))
     return n
 
 

@@ -41,11 +41,27 @@ class Block(nn.Module):
         self.adaLN_modulation = nn.Sequential(nn.Linear(d, 6 * d))
 
 
+class TextAttn(nn.Module):
+    """TextRefineAttention's linears (JiT_T2I.py:227,231)"""
+    def __init__(self, d):
+        super().__init__()
+        self.qkv = nn.Linear(d, 3 * d, bias=False)
+        self.proj = nn.Linear(d, d)
+
+
+class TextBlock(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.attn = TextAttn(d)
+        self.mlp = SwiGLU(d, 4 * d)
+        self.adaLN_modulation = nn.Sequential(nn.Linear(d, 6 * d))
+
+
 class Net(nn.Module):
     def __init__(self, d=32, n=3):
         super().__init__()
         self.blocks = nn.ModuleList(Block(d) for _ in range(n))
-        self.text_refine_blocks = nn.ModuleList(Block(d) for _ in range(1))
+        self.text_refine_blocks = nn.ModuleList(TextBlock(d) for _ in range(1))
 
 
 @pytest.mark.parametrize("phase,per_block", [(1, 4), (2, 4), (3, 4)])
@@ -62,13 +78,32 @@ def test_convert_native_counts_and_keys(phase, per_block):
         assert b.mlp._fp8
         assert (type(b.mlp.w12) is G.Fp8Linear) == (phase == 1)
     for b in net.text_refine_blocks:                          # image blocks only (fp8_native.py:294)
-        assert type(b.attn.qkv_x) is nn.Linear
+        assert type(b.attn.qkv) is nn.Linear and type(b.attn.proj) is nn.Linear and not getattr(b.mlp, "_fp8", False)
+
+
+@pytest.mark.parametrize("phase,per_block,per_text", [(1, 5, 4), (2, 5, 4), (3, 5, 4)])
+def test_convert_native_text_blocks(phase, per_block, per_text):
+    """text=True: the image blocks' kv_y and the text-refine blocks' qkv, proj and MLP as well, in the same phase;
+    state-dict keys unchanged; idempotent; adaLN untouched; a linear whose features are not multiples of 16 stays."""
+    net = Net()
+    net.text_refine_blocks[0].attn.odd = nn.Linear(32, 24)
+    keys = set(net.state_dict())
+    assert G.convert_native(net, phase=phase, text=True) == 3 * per_block + per_text
+    assert set(net.state_dict()) == keys
+    assert G.convert_native(net, phase=phase, text=True) == 0
+    lin = {1: G.Fp8Linear, 2: G.Fp8Linear, 3: G.Fp8LinearF8}[phase]
+    for b in net.blocks:
+        assert type(b.attn.qkv_x) is lin and type(b.attn.kv_y) is lin and type(b.adaLN_modulation[0]) is nn.Linear
+    t = net.text_refine_blocks[0]
+    assert type(t.attn.qkv) is lin and type(t.attn.proj) is lin and t.mlp._fp8
+    assert type(t.adaLN_modulation[0]) is nn.Linear and type(t.attn.odd) is nn.Linear
 
 
 def test_convert_fp8_recipes(capsys):
-    for recipe, n in (("native", 12), ("native2", 12), ("native3", 12)):
+    for recipe, n in (("native", 12), ("native2", 12), ("native3", 12), ("native3+text", 19)):
         assert G.convert_fp8(Net(), recipe) == n
-    assert "GEMMs of the image blocks converted" in capsys.readouterr().out
+    out = capsys.readouterr().out
+    assert "GEMMs of the image blocks converted" in out and "GEMMs of the image and text blocks converted" in out
     with pytest.raises(ImportError):
         G.convert_fp8(Net(), "tensorwise")
 

@@ -203,3 +203,84 @@ def test_convert_and_train_step(dev, recipe):
     for (n, p), (_, pr) in zip(net.named_parameters(), ref.named_parameters()):
         assert p.grad is not None and torch.isfinite(p.grad.float()).all(), n
         assert rel(p.grad, pr.grad) < 0.25, n
+
+
+class _XAttn(nn.Module):
+    """Image attention with the text cross-attention keys / values (qkv_x, kv_y, proj: JiT_T2I.py:130-136)."""
+    def __init__(self, d):
+        super().__init__()
+        self.qkv_x = nn.Linear(d, 3 * d, bias=False)
+        self.kv_y = nn.Linear(d, 2 * d, bias=False)
+        self.proj = nn.Linear(d, d)
+
+    def forward(self, x, y):
+        q, k, v = self.qkv_x(x).chunk(3, -1)
+        ky, vy = self.kv_y(y).chunk(2, -1)
+        k, v = torch.cat([k, ky], 1), torch.cat([v, vy], 1)
+        a = torch.softmax((q.float() @ k.float().transpose(-1, -2)) / q.shape[-1] ** 0.5, -1)
+        return self.proj((a @ v.float()).to(x.dtype))
+
+
+class _TAttn(_Attn):
+    """TextRefineAttention's linears are named qkv and proj (JiT_T2I.py:227,231)."""
+    def __init__(self, d):
+        super().__init__(d)
+        self.qkv = self.qkv_x
+        del self.qkv_x
+
+    def forward(self, x):
+        q, k, v = self.qkv(x).chunk(3, -1)
+        a = torch.softmax((q.float() @ k.float().transpose(-1, -2)) / q.shape[-1] ** 0.5, -1)
+        return self.proj((a @ v.float()).to(x.dtype))
+
+
+class _XBlock(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.attn = _XAttn(d)
+        self.mlp = _MLP(d)
+
+    def forward(self, x, y):
+        x = x + self.attn(x, y)
+        return x + self.mlp(x)
+
+
+class _TBlock(_Block):
+    def __init__(self, d):
+        super().__init__(d)
+        self.attn = _TAttn(d)
+
+
+class _TNet(nn.Module):
+    def __init__(self, d, n):
+        super().__init__()
+        self.blocks = nn.ModuleList(_XBlock(d) for _ in range(n))
+        self.text_refine_blocks = nn.ModuleList(_TBlock(d) for _ in range(1))
+
+    def forward(self, x, y):
+        for b in self.text_refine_blocks:
+            y = b(y)
+        for b in self.blocks:
+            x = b(x, y)
+        return x
+
+
+def test_convert_text_blocks_and_train_step(dev):
+    """Recipe native3+text: the image blocks' kv_y and the text-refine block's qkv, proj and MLP run on the FP8
+    kernels as well, at a text length (51 tokens, M = 204 rows) that is no multiple of 16; outputs and every
+    gradient close to the bf16 model's."""
+    torch.manual_seed(1)
+    net = _TNet(128, 2).to(dev).to(torch.bfloat16)
+    ref = _TNet(128, 2).to(dev).to(torch.bfloat16)
+    ref.load_state_dict(net.state_dict())
+    assert G.convert_fp8(net, "native3+text") == 2 * 5 + 4
+    assert type(net.blocks[0].attn.kv_y) is G.Fp8LinearF8 and type(net.text_refine_blocks[0].attn.qkv) is G.Fp8LinearF8
+    x = torch.randn(4, 64, 128, device=dev).to(torch.bfloat16)
+    y = torch.randn(4, 51, 128, device=dev).to(torch.bfloat16)
+    out, outr = net(x, y), ref(x, y)
+    assert rel(out, outr) < 0.1
+    out.float().square().mean().backward()
+    outr.float().square().mean().backward()
+    for (n, p), (_, pr) in zip(net.named_parameters(), ref.named_parameters()):
+        assert p.grad is not None and torch.isfinite(p.grad.float()).all(), n
+        assert rel(p.grad, pr.grad) < 0.25, n
