@@ -1,4 +1,7 @@
-// Scaled FP8 (e4m3fn) GEMM for gfx950, "TN" layout: C[M, N] = bf16(sa * sb * A[M, K] . B[N, K]^T) (+ bias).
+// Scaled FP8 (e4m3fn) GEMM for gfx950, "TN" layout: C[M, N] = bf16(sa * sb * A[M, K] . B[N, K]^T) (+ bias), and
+// its "MN-major" instance for the wgrad, C = bf16(sa * sb * A[K, M]^T . B[K, N]) from operands stored with K as their row
+// index: the same kernel, whose K tiles are then 128 K rows x 256 bytes in LDS and whose fragments are read with the
+// transposing ds_read_b64_tr_b8 (bit-identical to the TN instance on the transposed operands).
 //
 // Design (CDNA4):
 //  * Macro tile 256 x 256 x 128 per workgroup of 8 waves, two per SIMD. Wave w owns the 64 x 128 sub-tile
