@@ -61,7 +61,7 @@ def parse():
     return p.parse_args()
 
 
-def make_inputs(dev, seed=0, C=C, H=H, outliers=0.0):
+def make_inputs(dev, seed=0, C=C, H=H, outliers=0.0, M=M_TOK):
     """The block's inputs: X ~ N(0,1), W ~ N(0, 1/K), dY ~ N(0, 1e-2), bf16. With `outliers`, that fraction of the
     activation channels (the same columns in every X) is scaled by 50 before the bf16 rounding (config 5)."""
     import torch
@@ -72,7 +72,7 @@ def make_inputs(dev, seed=0, C=C, H=H, outliers=0.0):
         return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16)
 
     def act():
-        x = torch.randn(M_TOK, C, generator=g, device=dev)
+        x = torch.randn(M, C, generator=g, device=dev)
         x[:, cols] *= 50.0
         return x.to(torch.bfloat16)
 
@@ -80,7 +80,7 @@ def make_inputs(dev, seed=0, C=C, H=H, outliers=0.0):
         "x_qkv": act(), "x_proj": act(), "x_mlp": act(),
         "w_qkv": bf(3 * C, C, std=C ** -0.5), "w_proj": bf(C, C, std=C ** -0.5),
         "w12": bf(2 * H, C, std=C ** -0.5), "w3": bf(C, H, std=H ** -0.5),
-        "dy_qkv": bf(M_TOK, 3 * C, std=0.1), "dy_proj": bf(M_TOK, C, std=0.1), "dy_mlp": bf(M_TOK, C, std=0.1),
+        "dy_qkv": bf(M, 3 * C, std=0.1), "dy_proj": bf(M, C, std=0.1), "dy_mlp": bf(M, C, std=0.1),
     }
     for k in ("x_qkv", "x_proj", "x_mlp", "w_qkv", "w_proj", "w12", "w3"):
         t[k].requires_grad_(True)
@@ -296,6 +296,19 @@ def main():
     ms18 = time_region(run18, 5, 2)
     del t18
 
+    # ---- a text-refine block's linears (recipe native3+text): 128 captions x 51.5 tokens = 6592 rows, fwd + bwd
+    MT = 6592
+    tt = make_inputs(dev, seed=7, M=MT)
+
+    def run_text():
+        for v in tt.values():
+            v.grad = None
+        step(G, tt)
+
+    fl_t = flops(gemm_shapes(MT))
+    ms_t = time_region(run_text, 10, 3)
+    del tt
+
     # ---- comparator: hipBLASLt FP8 GEMM (torch._scaled_mm) on the same shapes
     hip = None
     if not args.no_compare:
@@ -351,6 +364,9 @@ def main():
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
                       "tflops": round(fl18 / ms18 / 1e9, 1)},
+        "text_block": {"workload": "text-refine block linears (qkv, proj, SwiGLU MLP) fwd+bwd, native3+text, "
+                                   f"M = {MT} (128 captions x 51.5 tokens)", "ms": round(ms_t, 4),
+                       "gemm_tflop": round(fl_t / 1e12, 4), "tflops": round(fl_t / ms_t / 1e9, 1)},
         "hipblaslt_compare": hip,
         "cpu_baseline": cpu,
     }
