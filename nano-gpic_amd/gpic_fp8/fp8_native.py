@@ -311,6 +311,16 @@ def fp8_gemm_mn(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Te
         raise ValueError(f"fp8_gemm_mn: a is [{K}, {M}] but b is {tuple(b.shape)}")
     if M % 16 or N % 16:
         raise ValueError(f"fp8_gemm_mn needs M % 16 == 0 and N % 16 == 0, got M={M} N={N} K={K}")
+    if K * max(a.stride(0), b.stride(0)) >= 2 ** 31:
+        # past the kernel's 32-bit load offsets: the K-major kernel on the transposed bytes (K padded with zeros to a
+        # multiple of 16) gives the same bits
+        k16 = (K + 15) // 16 * 16
+
+        def kmajor(t):
+            u = torch.zeros(t.shape[1], k16, dtype=torch.uint8, device=t.device)
+            u[:, :K] = t.view(torch.uint8).t()
+            return u.view(E4)
+        return fp8_gemm(kmajor(a), sa, kmajor(b), sb, bias, False)
     sa = sa.to(torch.float32).reshape(1)
     sb = sb.to(torch.float32).reshape(1)
     if bias is not None:

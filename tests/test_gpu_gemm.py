@@ -225,3 +225,18 @@ def test_mn_matches_tn(dev, M, N, K, bias, pad):
 
 def bits_t(t):
     return t.view(torch.int16)
+
+
+def test_mn_past_32bit_offsets_falls_back(dev):
+    """K x row stride >= 2^31 is past the MN-major kernel's 32-bit load offsets: the op routes through the K-major
+    kernel on the transposed bytes (same bits). Checked on a strided view: a [K, 32] slice of a [K, 65536] tensor,
+    K = 32768 (K x 65536 = 2^31)."""
+    K = 32768
+    g = torch.Generator(device=dev).manual_seed(77)
+    base = (torch.randn(K, 65536, generator=g, device=dev) * 8).clamp(-448, 448).to(E4)
+    a = base[:, :32]
+    b = (torch.randn(K, 48, generator=g, device=dev) * 8).clamp(-448, 448).to(E4)
+    s1 = torch.tensor([0.01], device=dev)
+    c = G.fp8_gemm_mn(a, s1, b, s1)
+    want = G.fp8_gemm_mn(a.contiguous(), s1, b, s1)
+    assert torch.equal(c.view(torch.int16), want.view(torch.int16))
