@@ -509,8 +509,10 @@ static int num_cus() {
 // The K split: the number of splits s (and K tiles per split) that minimises a model of the run time. Work items
 // (tiles x splits) run in rounds of one per CU; a round lasts as long as its items' K tiles plus a fixed cost per
 // item (prologue, epilogue); splitting adds the reduce, which reads s fp32 partials of C and writes C. Model constants
-// from measured d12 shapes: ~1.45 us per K tile, ~4 us per item (5 with fp32 partials), ~5 TB/s for the reduce.
-// Split-K also needs N < 2^21 (the partials' 32-bit buffer offsets).
+// from measured d12 and text-block shapes: a K tile takes ~1.45 us with every CU busy and less when a single round
+// leaves CUs idle (1.0 + 0.45 x the busy fraction: 1.03-1.18 us measured at 104 of 256), ~4 us per item (5 with fp32
+// partials), and the reduce ~4 us plus its bytes at ~5 TB/s. Split-K also needs N < 2^21 (the partials' 32-bit
+// buffer offsets).
 static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
   Plan p;
   p.tiles_m = (int)((M + kBM - 1) / kBM);
@@ -525,9 +527,11 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
     const int64_t per = (ktiles + s - 1) / s;          // K tiles per split
     const int64_t splits = (ktiles + per - 1) / per;   // splits actually needed
     if (splits != s) continue;
-    const int64_t rounds = (tiles * splits + cus - 1) / cus;
-    double t = (double)rounds * ((double)per * 1.45 + (splits > 1 ? 5.0 : 4.0));
-    if (splits > 1) t += ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
+    const int64_t items = tiles * splits;
+    const int64_t rounds = (items + cus - 1) / cus;
+    const double busy = rounds == 1 ? (double)items / (double)cus : 1.0;
+    double t = (double)rounds * ((double)per * (1.0 + 0.45 * busy) + (splits > 1 ? 5.0 : 4.0));
+    if (splits > 1) t += 4.0 + ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
     if (s == 1 || t < best) {
       best = t;
       best_per = per;
