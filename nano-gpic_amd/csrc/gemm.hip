@@ -445,20 +445,28 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
           }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
+        // all 8 rows read back first (their latencies overlap; a store between them would order them), then stored
+        st16_t wv[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           const int r = 4 * j + rr;
-          st16_t w = *(const GPIC_LDS st16_t *)(cst + r * 256 + 16 * (rc ^ (r & 15)));
-          if (kMN && r >= 16) w = st16_t{w[2], w[3], w[0], w[1]};   // halves exchanged (j >= 4: known here)
+          wv[j] = *(const GPIC_LDS st16_t *)(cst + r * 256 + 16 * (rc ^ (r & 15)));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
+        const int rl0 = wm * kWTM + mi * 32 + rr;   // row within the tile of j = 0; row j is rl0 + 4 j
+        int off = (rl0 * (int)ldc + n) * 2;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          st16_t w = wv[j];
+          if (kMN && j >= 4) w = st16_t{w[2], w[3], w[0], w[1]};   // rows 16..31: halves exchanged
           if (bias) {   // bf16(bf16(acc * s) + bias)
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
           }
-          const int rl = wm * kWTM + mi * 32 + r;   // row within the tile
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), rC,
-                                                 rl < rows_c && n < N ? (rl * (int)ldc + n) * 2 : kOOB, 0, 0);
+                                                 rl0 + 4 * j < rows_c && n < N ? off : kOOB, 0, 0);
+          off += 8 * (int)ldc;
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
       }
       pend = kStoresBF16;
     }
