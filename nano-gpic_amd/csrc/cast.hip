@@ -280,8 +280,8 @@ struct SrcSwiGLU {
     swiglu8(lut, z1, z2, v);
   }
 };
-// dz of one element (fp8_native.py:83-98), before its bf16 rounding: the z1 half da * z2 * sg * (1 + z1 * (1 - sg)),
-// the z2 half da * bf16(z1 * sg).
+// The z1 half of dz for one element (fp8_native.py:88-96), before its bf16 rounding: da * z2 * sg * (1 + z1 * (1 - sg)),
+// each operation rounded on its own (the z2 half, da * bf16(z1 * sg), is formed in dz_words).
 __device__ __forceinline__ float dz1_of(float z1, float z2, float dv, float sg) {
   const float t1 = 1.0f - sg;
   const float t2 = z1 * t1;
@@ -290,7 +290,6 @@ __device__ __forceinline__ float dz1_of(float z1, float z2, float dv, float sg) 
   const float pr = dv * z2;
   return pr * g;
 }
-__device__ __forceinline__ float dz2_of(float z1, float dv, float sg) { return dv * bf16_round(z1 * sg); }
 
 
 // src [rows, cols] (cols % 8 == 0) -> q [rows, cols] (row stride ldq; skipped when q == nullptr) and the transposed
@@ -484,7 +483,7 @@ __device__ __forceinline__ void dz_words(const float *lut, u32x4 z1v, u32x4 z2v,
 #pragma unroll
   for (int i = 0; i < 8; i++) d1[i] = dz1_of(z1[i], z2[i], dv[i], sg[i]);
 #pragma unroll
-  for (int j = 0; j < 4; j++) {   // dz2_of with the bf16(z1 * sg) of two values rounded by one instruction
+  for (int j = 0; j < 4; j++) {   // d2 = da * bf16(z1 * sg), the roundings of two values by one instruction
     const uint32_t sl = pack_bf16(z1[2 * j] * sg[2 * j], z1[2 * j + 1] * sg[2 * j + 1]);
     d2[2 * j] = dv[2 * j] * bf16_lo(sl);
     d2[2 * j + 1] = dv[2 * j + 1] * bf16_hi(sl);
