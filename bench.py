@@ -110,6 +110,42 @@ def time_region(fn, steps, warmup):
     return s.elapsed_time(e) / steps
 
 
+def time_device(fn, steps, warmup):
+    """ms per call of fn on the device alone: the calls are issued while filler work (elementwise passes over a
+    1 GiB buffer) holds the stream, and the events bracket the calls, so the host's issue time does not show -- the
+    time a host that issues ahead of the GPU would see. The filler is doubled until it outlasts the issuing (checked:
+    its event has not completed when the last call is issued); None if it never does."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fn()
+    issue_ms = (time.perf_counter() - t0) * 1e3
+    torch.cuda.synchronize()
+    buf = torch.empty(1 << 28, device="cuda")
+    buf.mul_(1.0)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    buf.mul_(1.0)
+    e.record()
+    torch.cuda.synchronize()
+    n = max(4, int(2.0 * steps * issue_ms / max(s.elapsed_time(e), 1e-3)) + 1)
+    for _ in range(4):
+        for _ in range(n):
+            buf.mul_(1.0)
+        s.record()
+        for _ in range(steps):
+            fn()
+        ahead = not s.query()
+        e.record()
+        torch.cuda.synchronize()
+        if ahead:
+            return s.elapsed_time(e) / steps
+        n *= 2
+    return None
+
+
 def gemm_operands(G, dev, shapes):
     """e4m3 operands of each shape in the layout the step gives them: forward and dgrad GEMMs K-major (a [M, K],
     b [N, K]: fp8_gemm); wgrads MN-major, the untransposed output gradient and input over the tokens (a [K, M],
@@ -307,6 +343,9 @@ def main():
 
     fl_t = flops(gemm_shapes(MT))
     ms_t = time_region(run_text, 10, 3)
+    # Its kernels are short (12-60 us GEMMs): Python's autograd issues a step in about as long as the GPU runs it, so
+    # the wall time above depends on the host CPU; the device time is measured with the launches queued ahead.
+    ms_t_dev = time_device(run_text, 10, 0)
     del tt
 
     # ---- comparator: hipBLASLt FP8 GEMM (torch._scaled_mm) on the same shapes
@@ -366,7 +405,9 @@ def main():
                       "tflops": round(fl18 / ms18 / 1e9, 1)},
         "text_block": {"workload": "text-refine block linears (qkv, proj, SwiGLU MLP) fwd+bwd, native3+text, "
                                    f"M = {MT} (128 captions x 51.5 tokens)", "ms": round(ms_t, 4),
-                       "gemm_tflop": round(fl_t / 1e12, 4), "tflops": round(fl_t / ms_t / 1e9, 1)},
+                       "gemm_tflop": round(fl_t / 1e12, 4), "tflops": round(fl_t / ms_t / 1e9, 1),
+                       "device_ms": round(ms_t_dev, 4) if ms_t_dev else None,
+                       "device_tflops": round(fl_t / ms_t_dev / 1e9, 1) if ms_t_dev else None},
         "hipblaslt_compare": hip,
         "cpu_baseline": cpu,
     }

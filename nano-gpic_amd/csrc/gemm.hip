@@ -8,23 +8,27 @@
 //    (rows 64 * (w >> 1), columns 128 * (w & 1)) as 2 x 4 MFMA tiles of v_mfma_f32_32x32x64_f8f6f4 (both operands
 //    e4m3, fp32 accumulators in VGPRs: 239 of the 256 a wave of two per SIMD may hold, so the epilogue's VALU
 //    work reads them without AGPR copies; measured 0.5% faster than accumulators in AGPRs).
+//  * A narrow class, 256 x 128 (K-major operands only), for shapes whose 256 x 256 tiles leave CUs idle: each wave
+//    then owns 64 x 64, the B K tile is 16 KiB; the host picks the width per shape (same bits either way).
 //  * Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share the SIMDs pairwise and run one phase apart. In each
-//    phase one group issues its 16 MFMAs of a K tile while the other reads its fragments of the next K tile from LDS
-//    (and, for group 0, sends the following K tile to LDS); a workgroup barrier separates phases. The MFMA pipe of
-//    every SIMD sees the two groups' MFMA blocks back to back.
-//  * Global -> LDS with buffer_load_dwordx4 ... lds (no VGPR round trip), issued by group 0: one wave instruction
-//    fills 1 KiB of LDS = 8 rows x 128 bytes of K. Rows past M / N read as zeros through the buffer descriptor's range
-//    check; the last, partial K tile masks its chunks the same way, so any M and any K % 16 == 0 need no branches in
-//    the main loop. Per-lane offsets are computed once; the K position travels in the scalar soffset.
+//    phase one group issues its 16 MFMAs of a K tile while the other reads its 12 fragments of that K tile from LDS,
+//    with its share of a later K tile's loads between the reads (group 0 sends B one K tile ahead, group 1 sends A
+//    two ahead); a workgroup barrier separates phases. The MFMA pipe of every SIMD sees the two groups' MFMA blocks
+//    back to back. LDS: 3 A stages and 2 B stages of 32 KiB, all of gfx950's 160 KiB.
+//  * Global -> LDS with buffer_load_dwordx4 ... lds (no VGPR round trip): one wave instruction fills 1 KiB of LDS =
+//    8 rows x 128 bytes of K. Rows past M / N read as zeros through the buffer descriptor's range check; the last,
+//    partial K tile masks its chunks the same way, so any M and any K % 16 == 0 need no branches in the main loop.
+//    Per-lane offsets are computed once; the K position travels in the scalar soffset.
 //  * LDS rows are XOR-swizzled: 16-byte chunk c of row r lives in slot c ^ ((r >> 1) & 7). gfx950's LDS serves
 //    256 B per clock to 16 lanes at a time; the fragment reads of 16 consecutive rows at one chunk then hit 16
 //    different 16-byte bank groups (measured: no SQ_LDS_BANK_CONFLICT cycles).
-//  * Two LDS stages: K tile t is read by group 0 in phase 2t and by group 1 in phase 2t + 1; group 0 sends tile t + 1
-//    into the other stage during phase 2t and waits for it at the end of its MFMA phase 2t + 1.
-//  * The MFMA is issued as B-fragment x A-fragment, so each lane's accumulators hold runs of 4 consecutive columns
-//    n of one row m of C: the epilogue writes 8-byte (bf16) or 16-byte (fp32 partial) chunks.
-//  * Tile order: workgroups are dealt to the 8 XCDs round robin; the id is remapped so each XCD walks a contiguous
-//    range of tiles in groups of kGroupM tile rows (neighbouring workgroups share A and B panels in that XCD's L2).
+//  * The MFMA is issued as B-fragment x A-fragment with B's rows permuted in LDS (col_of), so each lane's
+//    accumulators hold runs of 8 consecutive columns of one row of C. The bf16 epilogue rounds them, passes each
+//    32-row block through LDS and stores 16 bytes per lane, whole 256-byte row segments per 16 lanes; split-K
+//    partials go out as 16-byte fp32 stores straight from the accumulators.
+//  * Persistent grid: work items (tile, K split) are dealt to the workgroups round robin and the id is remapped so
+//    each XCD walks a contiguous range of tiles in groups of kGroupM tile rows (neighbouring workgroups share A and B
+//    panels in that XCD's L2). The next item's first loads are issued before the current item's epilogue.
 //  * Split-K (for the small-output wgrad shapes): each split writes fp32 partials; a second kernel sums them in
 //    split order (deterministic) and applies scale, bias and the bf16 rounding.
 #include <algorithm>
@@ -72,8 +76,6 @@ __device__ __forceinline__ int mn_swz(int r) { return (r & 7) << 1; }
 // 16 (v / 8) + 8 (l / 32) + v % 8, i.e. two runs of 8 consecutive columns. An involution that keeps every aligned
 // group of 16 rows, so with N % 16 == 0 the rows past N stay past N.
 __host__ __device__ constexpr int col_of(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
-constexpr int kCStageBytes = 32 * 256;                 // per wave: a 32 x 128 bf16 block of C on its way out
-static_assert(kThreads / 2 / 64 * kCStageBytes == kHalfBytes, "each group's C blocks fill one half stage");
 static_assert(col_of(13) == 13 && col_of(8) == 4 && col_of(4) == 8 && col_of(17) == 17 && col_of(col_of(22)) == 22,
               "col_of swaps bits 2 and 3");
 
@@ -124,14 +126,24 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
 // ldb), C[m, n] = bf16(sa * sb * sum_k A[k, m] B[k, n]) -- the FP8 wgrad reading the untransposed e4m3 activations
 // and gradients. A K tile of an operand is then 128 rows (K) x 256 bytes (MN) in LDS and its fragments are read with
 // the transposing ds_read_b64_tr_b8.
-template <bool kTail, bool kMN>
+// kBNt: the tile's width, 256 or (K-major instance only) 128 -- the narrow tile class for shapes whose 256 x 256 tiles
+// leave CUs idle or end on a partial round: each wave then owns 64 x 64 of C, a B K tile is 16 KiB.
+template <bool kTail, bool kMN, int kBNt>
 __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
                                                             const uint8_t *__restrict__ B, int ldb,
                                                             const float *__restrict__ sa, const float *__restrict__ sb,
                                                             const uint16_t *__restrict__ bias, uint16_t *__restrict__ C,
                                                             int64_t ldc, float *__restrict__ P, int M, int N, int K,
                                                             int ksplit, int tiles_m, int tiles_n, int splits) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+  static_assert(kBNt == 256 || (kBNt == 128 && !kMN), "tile widths: 256, or 128 for the K-major instance");
+  constexpr int kWTNt = kBNt / 2;                 // wave tile columns
+  constexpr int kTNt = kWTNt / 32;                // 32-column MFMA tiles per wave: 4 or 2
+  constexpr int kHalfB = kBNt * kBK;              // one B K tile: 32 or 16 KiB
+  constexpr int kLoadsB = kBNt / 8 / kLoaders;    // B loads per wave per K tile: 8 or 4
+  constexpr int kRowB = kWTNt * 2;                // bytes of a row of a wave's bf16 C block: 256 or 128
+  constexpr int kCStage = 32 * kRowB;             // a wave's 32-row C block on its way out
+  static_assert(4 * kCStage <= kHalfBytes && 4 * kCStage <= kHalfB, "each group's C blocks fit one stage");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kAStages * kHalfBytes + kBStages * kHalfB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = wave >> 2;
@@ -174,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const int first_m = (tile / per_group) * kGroupM;
     const int gsz = min(tiles_m - first_m, kGroupM);
     w.m0 = (first_m + (tile % per_group) % gsz) * kBM;
-    w.n0 = ((tile % per_group) / gsz) * kBN;
+    w.n0 = ((tile % per_group) / gsz) * kBNt;
     w.kbeg = w.split * ksplit;
     w.kend = min(K, w.kbeg + ksplit);
     w.nk = (w.kend - w.kbeg + kBK - 1) / kBK;
@@ -185,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       w.voB = w.n0 + 16 * mchunk < N ? baseB : kOOB;
     } else {
       w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
-      w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBN) * ldb);
+      w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBNt) * ldb);
       w.voA = w.voB = 0;
     }
     return w;
@@ -215,14 +227,14 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     }
   };
   auto a_half = [](int stage) { return stage * kHalfBytes; };
-  auto b_half = [](int stage) { return kBBase + stage * kHalfBytes; };
+  auto b_half = [](int stage) { return kBBase + stage * kHalfB; };
   // Group 0 sends an item's first loads: A(0), B(0) and, with a second K tile, A(1) (16 + 8 per wave).
   auto send_prologue = [&](const Item &w) {
     if (w.nk > 0) {
 #pragma unroll
       for (int i = 0; i < kLoads; i++) load(w, true, a_half(0), w.kbeg, i);
 #pragma unroll
-      for (int i = 0; i < kLoads; i++) load(w, false, b_half(0), w.kbeg, i);
+      for (int i = 0; i < kLoadsB; i++) load(w, false, b_half(0), w.kbeg, i);
     }
     if (w.nk > 1) {
 #pragma unroll
@@ -232,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 
   // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5).
   // Fragment j = 6 * step + f: f < kTM is A fragment f, otherwise B fragment f - kTM; two ds_read_b128 each.
-  v8i fa[2][kTM], fb[2][kTN];
+  v8i fa[2][kTM], fb[2][kTNt];
   const int frow = lane & 31;
   const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
   const int c0 = 2 * (lane >> 5);
@@ -247,9 +259,9 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int tr_off = tr_row * 256 + 8 * (tr_s & 1);
   const int tr_x = 16 * ((tr_g & 1) | mn_swz(tr_row));
   auto read_frag = [&](int ast, int bst, int j) {
-    const int step = j / (kTM + kTN), f = j % (kTM + kTN);
+    const int step = j / (kTM + kTNt), f = j % (kTM + kTNt);
     if constexpr (kMN) {
-      const int mnb = f < kTM ? wm * kWTM + f * 32 : wn * kWTN + (f - kTM) * 32;
+      const int mnb = f < kTM ? wm * kWTM + f * 32 : wn * kWTNt + (f - kTM) * 32;
       const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem + (f < kTM ? a_half(ast) : b_half(bst)) +
                                   step * 64 * 256 + tr_off + (mnb ^ tr_x);
       v2i r[4];
@@ -263,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
     const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem +
                                 (f < kTM ? a_half(ast) + (wm * kWTM + f * 32 + frow) * kBK
-                                         : b_half(bst) + (wn * kWTN + (f - kTM) * 32 + frow) * kBK);
+                                         : b_half(bst) + (wn * kWTNt + (f - kTM) * 32 + frow) * kBK);
     const u32x4 x0 = *(const GPIC_LDS u32x4 *)(p + lo), x1 = *(const GPIC_LDS u32x4 *)(p + hi);
     const v8i v{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
     if (f < kTM) fa[step][f] = v;
@@ -272,15 +284,33 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // A memory phase: the wave's 12 fragment reads of K tile (ast, bst), with its 8 loads of one operand's later K
   // tile between them when `send`. A load issue waits while the texture unit's queue is full; with the reads in
   // between, the LDS works through the reads during those waits.
-  static_assert(2 * (kTM + kTN) == 12 && kLoads == 8, "interleave pattern: 3 fragments per 2 loads");
+  // (The narrow tile: 8 fragment reads, with the 8 A or 4 B loads spread evenly between them.)
   auto mem_phase = [&](const Item &w, int ast, int bst, bool send, bool isA, int dst, int k0) {
+    if constexpr (kBNt == 256) {
+      static_assert(2 * (kTM + kTNt) == 12 && kLoads == 8 && kLoadsB == 8, "interleave pattern: 3 fragments per 2 loads");
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      read_frag(ast, bst, 3 * j);
-      if (send) load(w, isA, dst, k0, 2 * j);
-      read_frag(ast, bst, 3 * j + 1);
-      read_frag(ast, bst, 3 * j + 2);
-      if (send) load(w, isA, dst, k0, 2 * j + 1);
+      for (int j = 0; j < 4; j++) {
+        read_frag(ast, bst, 3 * j);
+        if (send) load(w, isA, dst, k0, 2 * j);
+        read_frag(ast, bst, 3 * j + 1);
+        read_frag(ast, bst, 3 * j + 2);
+        if (send) load(w, isA, dst, k0, 2 * j + 1);
+      }
+    } else {
+      constexpr int R = 2 * (kTM + kTNt);
+#pragma unroll
+      for (int j = 0; j < R; j++) {
+        read_frag(ast, bst, j);
+        if (send) {
+          if (isA) {
+#pragma unroll
+            for (int i = j * kLoads / R; i < (j + 1) * kLoads / R; i++) load(w, true, dst, k0, i);
+          } else {
+#pragma unroll
+            for (int i = j * kLoadsB / R; i < (j + 1) * kLoadsB / R; i++) load(w, false, dst, k0, i);
+          }
+        }
+      }
     }
   };
 
@@ -303,7 +333,10 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     if (pend == 0) {
       if (two) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else if (pend == 16) {
+    } else if (kBNt == 128 && pend == 8) {   // (the narrow tile's pend is 0, 8 or 16; the wide one's 0, 16 or 32)
+      if (two) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    } else if (kBNt == 128 || pend == 16) {
       if (two) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     } else {
@@ -311,17 +344,17 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
     }
   };
-  constexpr int kStoresBF16 = kTM * kTN * 2;         // bf16 epilogue: 16 buffer stores per wave, always issued
-  constexpr int kStoresF32 = kTN * kTM * 4;          // split-K partials: 32
+  constexpr int kStoresBF16 = kTM * kTNt * 2;         // bf16 epilogue: 16 (narrow: 8) buffer stores per wave, always issued
+  constexpr int kStoresF32 = kTNt * kTM * 4;          // split-K partials: 32 (narrow: 16)
 
   int it = blockIdx.x;
   Item cur = item(it);
   if (group == 0) send_prologue(cur);
   int pend = 0;   // stores group 0 issued after the current item's prologue loads
   for (;;) {
-    v16f acc[kTN][kTM];
+    v16f acc[kTNt][kTM];
 #pragma unroll
-    for (int i = 0; i < kTN; i++)
+    for (int i = 0; i < kTNt; i++)
 #pragma unroll
       for (int j = 0; j < kTM; j++) acc[i][j] = v16f{};
 
@@ -358,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 #pragma unroll
       for (int step = 0; step < 2; step++)
 #pragma unroll
-        for (int ni = 0; ni < kTN; ni++)
+        for (int ni = 0; ni < kTNt; ni++)
 #pragma unroll
           for (int mi = 0; mi < kTM; mi++)
             acc[ni][mi] =
@@ -388,13 +421,13 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(P + ((int64_t)cur.split * M + cur.m0) * N), 0, rows_c * N * 4, kBufferFlags);
 #pragma unroll
-      for (int ni = 0; ni < kTN; ni++)
+      for (int ni = 0; ni < kTNt; ni++)
 #pragma unroll
         for (int mi = 0; mi < kTM; mi++)
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             const int r = wm * kWTM + mi * 32 + wr;
-            const int n = cur.n0 + wn * kWTN + ni * 32 +
+            const int n = cur.n0 + wn * kWTNt + ni * 32 +
                           (kMN ? 8 * q + 4 * wh : 16 * (q >> 1) + 8 * wh + 4 * (q & 1));
             const v16f &v = acc[ni][mi];
             __builtin_amdgcn_raw_buffer_store_b128(
@@ -410,12 +443,16 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       // both ways). Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. The next item's
       // prologue loads go to A stages 0, 1 and B stage 0; the first loads into A stage 2 and B stage 1 come after the
       // next item's first barrier, which group 1 reaches only when its epilogue is done.
+      // The narrow tile's block rows are 128 bytes (8 chunks): chunk c of row r sits in slot c ^ ((r / 2) & 7), so the
+      // 16 lanes of a write (rows r..r+15 at one chunk) or of a read-back (two rows) cover all 64 banks.
       GPIC_LDS uint8_t *cst =
-          (GPIC_LDS uint8_t *)smem + (group == 0 ? a_half(2) : b_half(1)) + (wave & 3) * kCStageBytes;
+          (GPIC_LDS uint8_t *)smem + (group == 0 ? a_half(2) : b_half(1)) + (wave & 3) * kCStage;
       const __amdgpu_buffer_rsrc_t rC =
           __builtin_amdgcn_make_buffer_rsrc((void *)(C + (int64_t)cur.m0 * ldc), 0, rows_c * (int)ldc * 2, kBufferFlags);
-      const int rr = el >> 4, rc = el & 15;        // read-back: rows 4 j + rr, chunk rc
-      const int n = cur.n0 + wn * kWTN + 8 * rc;   // the read-back lane's 8 columns
+      constexpr int kLPR = kRowB / 16, kRPI = 64 / kLPR;   // read-back: lanes per row, rows per instruction
+      auto slot = [](int c, int r) { return kBNt == 256 ? c ^ (r & 15) : c ^ ((r >> 1) & 7); };
+      const int rr = (unsigned)el / kLPR, rc = (unsigned)el % kLPR;   // read-back: rows kRPI j + rr, chunk rc
+      const int n = cur.n0 + wn * kWTNt + 8 * rc;   // the read-back lane's 8 columns
       uint32_t b[4] = {0, 0, 0, 0};
       if (bias && n < N) {
         const u32x2 b0 = *reinterpret_cast<const u32x2 *>(bias + n), b1 = *reinterpret_cast<const u32x2 *>(bias + n + 4);
@@ -424,14 +461,14 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 #pragma unroll
       for (int mi = 0; mi < kTM; mi++) {
 #pragma unroll
-        for (int ni = 0; ni < kTN; ni++) {
+        for (int ni = 0; ni < kTNt; ni++) {
           const v16f &v = acc[ni][mi];
           if constexpr (kMN) {
             // natural column order: runs of 4 (columns 32 ni + 8 q + 4 wh + [0, 4)), 8 bytes each, into half
             // wh ^ (wr / 16) of the chunk (rows wr and wr + 16 share a slot: the halves keep them apart)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-              *(GPIC_LDS st8_t *)(cst + wr * 256 + 16 * ((4 * ni + q) ^ (wr & 15)) + 8 * (wh ^ (wr >> 4))) =
+              *(GPIC_LDS st8_t *)(cst + wr * kRowB + 16 * slot(4 * ni + q, wr) + 8 * (wh ^ (wr >> 4))) =
                   st8_t{pack_bf16(v[4 * q] * s, v[4 * q + 1] * s), pack_bf16(v[4 * q + 2] * s, v[4 * q + 3] * s)};
           } else {
 #pragma unroll
@@ -440,23 +477,24 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 #pragma unroll
               for (int e = 0; e < 4; e++)
                 w[e] = pack_bf16(v[8 * hh + 2 * e] * s, v[8 * hh + 2 * e + 1] * s);
-              *(GPIC_LDS st16_t *)(cst + wr * 256 + 16 * ((4 * ni + 2 * hh + wh) ^ (wr & 15))) = w;
+              *(GPIC_LDS st16_t *)(cst + wr * kRowB + 16 * slot(4 * ni + 2 * hh + wh, wr)) = w;
             }
           }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the block is complete before any lane reads it back
         // all 8 rows read back first (their latencies overlap; a store between them would order them), then stored
-        st16_t wv[8];
+        constexpr int kNI = 32 / kRPI;   // read-back instructions per block: 8 (narrow: 4)
+        st16_t wv[kNI];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int r = 4 * j + rr;
-          wv[j] = *(const GPIC_LDS st16_t *)(cst + r * 256 + 16 * (rc ^ (r & 15)));
+        for (int j = 0; j < kNI; j++) {
+          const int r = kRPI * j + rr;
+          wv[j] = *(const GPIC_LDS st16_t *)(cst + r * kRowB + 16 * slot(rc, r));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
-        const int rl0 = wm * kWTM + mi * 32 + rr;   // row within the tile of j = 0; row j is rl0 + 4 j
+        const int rl0 = wm * kWTM + mi * 32 + rr;   // row within the tile of j = 0; row j is rl0 + kRPI j
         int off = (rl0 * (int)ldc + n) * 2;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < kNI; j++) {
           st16_t w = wv[j];
           if (kMN && j >= 4) w = st16_t{w[2], w[3], w[0], w[1]};   // rows 16..31: halves exchanged
           if (bias) {   // bf16(bf16(acc * s) + bias)
@@ -464,8 +502,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
             for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
           }
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), rC,
-                                                 rl0 + 4 * j < rows_c && n < N ? off : kOOB, 0, 0);
-          off += 8 * (int)ldc;
+                                                 rl0 + kRPI * j < rows_c && n < N ? off : kOOB, 0, 0);
+          off += 2 * kRPI * (int)ldc;
         }
       }
       pend = kStoresBF16;
@@ -501,7 +539,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 // ------------------------------------------------------------------------------------------- host side
 
 struct Plan {
-  int tiles_m, tiles_n, splits, ksplit;
+  int tiles_m, tiles_n, splits, ksplit, bn;   // bn: the tile width, 256 or 128
 };
 
 static int num_cus() {
@@ -521,13 +559,27 @@ static int num_cus() {
 // leaves CUs idle (1.0 + 0.45 x the busy fraction: 1.03-1.18 us measured at 104 of 256), ~4 us per item (5 with fp32
 // partials), and the reduce ~4 us plus its bytes at ~5 TB/s. Split-K also needs N < 2^21 (the partials' 32-bit
 // buffer offsets).
-static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
-  Plan p;
-  p.tiles_m = (int)((M + kBM - 1) / kBM);
-  p.tiles_n = (int)((N + kBN - 1) / kBN);
-  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+// Then the tile width at that split count (K-major operands only): the 256 x 128 tile does half the work per item at
+// ~0.59 of the time per K tile (measured over full rounds of d12 shapes: 0.57-0.60) and ~3 us per item, so it wins
+// where it fills CUs that 256 x 256 tiles leave idle (text-block shapes: 104 tiles of 256 x 256 on 256 CUs) or
+// evens out a partial last round. It is taken only for a predicted gain of 10% or more: the model treats a partial
+// last round of several as a full one, and near-ties went either way when measured (text qkv.fwd: 3 narrow rounds vs
+// 2 wide ones, 29.4 vs 30.0 us on one box, 33.3 vs 31.1 on another). The split count does not depend on the width,
+// so both operand layouts sum the same partials in the same order: their results are the same bits.
+constexpr double kNarrowKTile = 0.59, kNarrowItem = 3.0, kNarrowGain = 0.9;
+static Plan plan_gemm(int64_t M, int64_t N, int64_t K, bool narrow_ok) {
   const int64_t ktiles = (K + kBK - 1) / kBK;
   const int64_t cus = num_cus();
+  const int64_t tiles_m = (M + kBM - 1) / kBM;
+  auto model = [&](int bn, int64_t per, int64_t splits) {
+    const int64_t items = tiles_m * ((N + bn - 1) / bn) * splits;
+    const int64_t rounds = (items + cus - 1) / cus;
+    const double busy = rounds == 1 ? (double)items / (double)cus : 1.0;
+    const double ktile = bn == 256 ? 1.0 : kNarrowKTile, fixed = bn == 256 ? 4.0 : kNarrowItem;
+    double t = (double)rounds * ((double)per * ktile * (1.0 + 0.45 * busy) + fixed + (splits > 1 ? 1.0 : 0.0));
+    if (splits > 1) t += 4.0 + ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
+    return t;
+  };
   const int64_t max_splits = N < (1 << 21) ? std::min<int64_t>(ktiles, 64) : 1;
   double best = 0.0;
   int64_t best_per = ktiles;
@@ -535,19 +587,18 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
     const int64_t per = (ktiles + s - 1) / s;          // K tiles per split
     const int64_t splits = (ktiles + per - 1) / per;   // splits actually needed
     if (splits != s) continue;
-    const int64_t items = tiles * splits;
-    const int64_t rounds = (items + cus - 1) / cus;
-    const double busy = rounds == 1 ? (double)items / (double)cus : 1.0;
-    double t = (double)rounds * ((double)per * (1.0 + 0.45 * busy) + (splits > 1 ? 5.0 : 4.0));
-    if (splits > 1) t += 4.0 + ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
+    const double t = model(256, per, splits);
     if (s == 1 || t < best) {
       best = t;
       best_per = per;
     }
   }
+  Plan p;
+  p.tiles_m = (int)tiles_m;
   p.ksplit = (int)(best_per * kBK);
-  p.splits = (int)((ktiles + best_per - 1) / best_per);
-  if (ktiles == 0) p.splits = 1;
+  p.splits = ktiles == 0 ? 1 : (int)((ktiles + best_per - 1) / best_per);
+  p.bn = narrow_ok && ktiles > 0 && model(128, best_per, p.splits) < kNarrowGain * best ? 128 : 256;
+  p.tiles_n = (int)((N + p.bn - 1) / p.bn);
   return p;
 }
 
@@ -559,7 +610,8 @@ static int launch_gemm(const uint8_t *A, int64_t lda, const float *sa, const uin
   if (M == 0 || N == 0) return GPIC_OK;
   if (K > 0 && (!A || !B)) return GPIC_EINVAL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && ((uintptr_t)bias & 7u))) return GPIC_EALIGN;
-  const Plan p = K > 0 ? plan_gemm(M, N, K) : Plan{(int)((M + kBM - 1) / kBM), (int)((N + kBN - 1) / kBN), 1, kBK};
+  const Plan p =
+      K > 0 ? plan_gemm(M, N, K, !kMN) : Plan{(int)((M + kBM - 1) / kBM), (int)((N + kBN - 1) / kBN), 1, kBK, kBN};
   float *P = nullptr;
   if (p.splits > 1) {
     const size_t need = (size_t)p.splits * M * N * sizeof(float);
@@ -572,7 +624,9 @@ static int launch_gemm(const uint8_t *A, int64_t lda, const float *sa, const uin
   const int slots = num_cus() & ~7;
   const int grid = work <= slots || slots < 8 ? work : slots;
   // the partial-K-tile load path is compiled only into the instance that needs it
-  auto *kernel = K % kBK ? gemm_tn_kernel<true, kMN> : gemm_tn_kernel<false, kMN>;
+  auto *kernel = K % kBK ? gemm_tn_kernel<true, kMN, 256> : gemm_tn_kernel<false, kMN, 256>;
+  if constexpr (!kMN)
+    if (p.bn == 128) kernel = K % kBK ? gemm_tn_kernel<true, false, 128> : gemm_tn_kernel<false, false, 128>;
   kernel<<<grid, kThreads, 0, st>>>(
       A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
       p.splits);
@@ -593,7 +647,7 @@ extern "C" {
 
 size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const Plan p = plan_gemm(M, N, K);
+  const Plan p = plan_gemm(M, N, K, false);   // (the split count does not depend on the tile width)
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 

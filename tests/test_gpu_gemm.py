@@ -161,12 +161,12 @@ def test_d12_shapes(dev, name, M, N, K):
 @pytest.mark.parametrize("M,N,K,bias,lda_pad", [
     (9000, 4000, 512, False, 0),      # 36 x 16 = 576 work items: 3 rounds per CU, ragged last row / column of tiles
     (4999, 2992, 1040, True, 16),     # partial K tile (K % 128 = 16), bias, padded leading dimension of A
-    (700, 528, 9984, False, 0),       # few tiles: split K, the last split shorter
+    (700, 528, 9984, False, 0),       # few tiles: split K, the last split shorter; 256 x 128 tiles
     (33, 4112, 2048, True, 0),        # one tile row, many columns, bias
     (6000, 256, 4096, False, 48),     # one tile column, split K may or may not apply
     (257, 257 // 16 * 16 + 16, 160, True, 0),   # tiny K, two splits with a partial tile
     (1024, 1024, 6592, False, 0),     # text-block proj wgrad: K = 128 images x 51.5 tokens, many splits, tail tile
-    (6592, 1024, 3072, True, 0),      # text-block qkv dgrad: 104 tiles, split K
+    (6592, 1024, 3072, True, 0),      # text-block qkv dgrad: 208 tiles of 256 x 128 (104 wide ones idle CUs)
 ])
 def test_shape_sweep(dev, M, N, K, bias, lda_pad):
     """Shapes that put several work items on each CU, partial tiles in M, N and K, split-K with a short last split,
@@ -198,11 +198,15 @@ def test_shape_sweep(dev, M, N, K, bias, lda_pad):
     (16, 16, 1, False, 0),           # one K row
     (4112, 2992, 1040, True, 32),    # padded leading dimensions, bias, partial K tile
     (9008, 4000, 512, False, 16),    # several work items per CU
+    (6592, 1024, 4096, True, 0),     # text-block w3 fwd shape: the K-major call takes 256 x 128 tiles, ragged M, bias
+    (704, 528, 9984, False, 0),      # 256 x 128 tiles with 16 K splits on the K-major side
 ])
 def test_mn_matches_tn(dev, M, N, K, bias, pad):
     """gpic_fp8_gemm_mn (both operands with K as the row index, the untransposed bytes of the wgrad) gives the same
     bits as gpic_fp8_gemm on the transposed operands: the MFMA sees the same values at every position (K padded
-    with zeros to a multiple of 16 for the TN call). Elementwise against the float64 product as well."""
+    with zeros to a multiple of 16 for the TN call). Where the K-major call picks the 256 x 128 tile (the small
+    shapes here and the last two cases; the MN-major kernel has only 256 x 256 tiles), this is also the check that the
+    two tile widths give the same bits. Elementwise against the float64 product as well."""
     g = torch.Generator(device=dev).manual_seed(M * 7 + N * 3 + K)
     a = (torch.randn(K, M + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :M]
     b = (torch.randn(K, N + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :N]
