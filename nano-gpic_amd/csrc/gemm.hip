@@ -8,8 +8,8 @@
 //    (rows 64 * (w >> 1), columns 128 * (w & 1)) as 2 x 4 MFMA tiles of v_mfma_f32_32x32x64_f8f6f4 (both operands
 //    e4m3, fp32 accumulators in VGPRs: 239 of the 256 a wave of two per SIMD may hold, so the epilogue's VALU
 //    work reads them without AGPR copies; measured 0.5% faster than accumulators in AGPRs).
-//  * A narrow class, 256 x 128 (K-major operands only), for shapes whose 256 x 256 tiles leave CUs idle: each wave
-//    then owns 64 x 64, the B K tile is 16 KiB; the host picks the width per shape (same bits either way).
+//  * A narrow class, 256 x 128, for shapes whose 256 x 256 tiles leave CUs idle: each wave then owns 64 x 64, the B
+//    K tile is 16 KiB; the host picks the width and the K split per shape, the same for both operand layouts.
 //  * Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share the SIMDs pairwise and run one phase apart. In each
 //    phase one group issues its 16 MFMAs of a K tile while the other reads its 12 fragments of that K tile from LDS,
 //    with its share of a later K tile's loads between the reads (group 0 sends B one K tile ahead, group 1 sends A
@@ -70,6 +70,10 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 // takes two adjacent chunks (2c', 2c' + 1) of 8 consecutive rows; the XOR with 2 (r & 7) sends those 16 chunks to 16
 // different slots, i.e. all 64 banks.
 __device__ __forceinline__ int mn_swz(int r) { return (r & 7) << 1; }
+// The narrow tile's MN-major B K tile has rows of 128 bytes (8 chunks): chunk c of K row r lives in slot
+// c ^ mn_swz_n(r). Two rows share a 256-byte bank window, so the 8 rows x 2 chunks of a transposing read hit 16
+// different 16-byte slots when the 4 rows of each parity XOR the chunk pair with 4 different even masks.
+__device__ __forceinline__ int mn_swz_n(int r) { return ((r >> 1) & 3) << 1; }
 
 // The column of C that MFMA output row i (0..31) of a 32 x 32 tile stands for: i with bits 2 and 3 exchanged. Lane l
 // holds output rows 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15; through this map those are the columns
@@ -126,8 +130,8 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
 // ldb), C[m, n] = bf16(sa * sb * sum_k A[k, m] B[k, n]) -- the FP8 wgrad reading the untransposed e4m3 activations
 // and gradients. A K tile of an operand is then 128 rows (K) x 256 bytes (MN) in LDS and its fragments are read with
 // the transposing ds_read_b64_tr_b8.
-// kBNt: the tile's width, 256 or (K-major instance only) 128 -- the narrow tile class for shapes whose 256 x 256 tiles
-// leave CUs idle or end on a partial round: each wave then owns 64 x 64 of C, a B K tile is 16 KiB.
+// kBNt: the tile's width, 256 or 128 -- the narrow tile class for shapes whose 256 x 256 tiles leave CUs idle or end
+// on a partial round: each wave then owns 64 x 64 of C, a B K tile is 16 KiB (MN-major: 128 K rows x 128 bytes).
 template <bool kTail, bool kMN, int kBNt>
 __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
                                                             const uint8_t *__restrict__ B, int ldb,
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
                                                             const uint16_t *__restrict__ bias, uint16_t *__restrict__ C,
                                                             int64_t ldc, float *__restrict__ P, int M, int N, int K,
                                                             int ksplit, int tiles_m, int tiles_n, int splits) {
-  static_assert(kBNt == 256 || (kBNt == 128 && !kMN), "tile widths: 256, or 128 for the K-major instance");
+  static_assert(kBNt == 256 || kBNt == 128, "tile widths: 256 or 128");
   constexpr int kWTNt = kBNt / 2;                 // wave tile columns
   constexpr int kTNt = kWTNt / 32;                // 32-column MFMA tiles per wave: 4 or 2
   constexpr int kHalfB = kBNt * kBK;              // one B K tile: 32 or 16 KiB
@@ -163,8 +167,13 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // row & 7 = mrow & 7 only.
   const int mrow = (wave & 3) * 4 + (lane >> 4);
   const int mchunk = (lane & 15) ^ mn_swz(mrow);
+  // MN-major B of the narrow tile: instruction i fills K rows [R0, R0 + 8), R0 = (i * 4 + wave % 4) * 8 =
+  // 32 i + mrowB - lane / 8; lane j writes slot j & 7 of row 32 i + mrowB, i.e. MN chunk (j & 7) ^ mn_swz_n(row), and
+  // mn_swz_n depends on (row / 2) & 3 = (mrowB / 2) & 3 only.
+  const int mrowB = kBNt == 256 ? mrow : (wave & 3) * 8 + (lane >> 3);
+  const int mchunkB = kBNt == 256 ? mchunk : (lane & 7) ^ mn_swz_n(mrowB);
   const int baseA = kMN ? mrow * lda + 16 * mchunk : lrow * lda + kchunk;
-  const int baseB = kMN ? mrow * ldb + 16 * mchunk : col_of(lrow) * ldb + kchunk;
+  const int baseB = kMN ? mrowB * ldb + 16 * mchunkB : col_of(lrow) * ldb + kchunk;
   const float s = sa[0] * sb[0];
 
   // ---- persistent: work item `it` (a tile and a K split) goes to workgroup it % gridDim.x. The grid is a multiple
@@ -194,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       w.rA = buffer_rsrc(A + w.m0, K * lda - w.m0);
       w.rB = buffer_rsrc(B + w.n0, K * ldb - w.n0);
       w.voA = w.m0 + 16 * mchunk < M ? baseA : kOOB;
-      w.voB = w.n0 + 16 * mchunk < N ? baseB : kOOB;
+      w.voB = w.n0 + 16 * mchunkB < N ? baseB : kOOB;
     } else {
       w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
       w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBNt) * ldb);
@@ -208,6 +217,16 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // register held across the loop for each load. In the last, partial K tile (kTail instance only), chunks at or past
   // kend read zeros.
   auto load = [&](const Item &w, bool isA, int dst, int k0, int i) {
+    if constexpr (kMN && kBNt == 128) {
+      if (!isA) {   // the narrow B K tile: K rows k0 + 32 i + mrowB, 128 bytes each
+        const int R0 = (i * kLoaders + (wave & 3)) * 8;
+        const int vo = w.voB + i * opaque(32 * ldb);
+        const uint32_t to = lds_addr(smem) + dst + R0 * 128;
+        if (!kTail || k0 + kBK <= w.kend) lds_dma16(w.rB, vo, k0 * ldb, to);
+        else lds_dma16(w.rB, k0 + 32 * i + mrowB < w.kend ? vo + k0 * ldb : kOOB, 0, to);
+        return;
+      }
+    }
     if constexpr (kMN) {
       // K rows k0 + 16 i + mrow; the K position goes to the scalar offset (k0 * ld), the row within the tile and the
       // chunk to the lane's; lanes whose chunk lies past M / N start from kOOB
@@ -258,15 +277,22 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int tr_row = 32 * (tr_g >> 1) + (tr_s >> 1);
   const int tr_off = tr_row * 256 + 8 * (tr_s & 1);
   const int tr_x = 16 * ((tr_g & 1) | mn_swz(tr_row));
+  // (the narrow tile's B: rows of 128 bytes, chunk (mnb / 16 + g % 2) ^ mn_swz_n(row), mn_swz_n even as well)
+  const int tr_offB = kBNt == 256 ? tr_off : tr_row * 128 + 8 * (tr_s & 1);
+  const int tr_xB = kBNt == 256 ? tr_x : 16 * ((tr_g & 1) | mn_swz_n(tr_row));
   auto read_frag = [&](int ast, int bst, int j) {
     const int step = j / (kTM + kTNt), f = j % (kTM + kTNt);
     if constexpr (kMN) {
       const int mnb = f < kTM ? wm * kWTM + f * 32 : wn * kWTNt + (f - kTM) * 32;
-      const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem + (f < kTM ? a_half(ast) : b_half(bst)) +
-                                  step * 64 * 256 + tr_off + (mnb ^ tr_x);
+      const int rowb = f < kTM ? 256 : kBNt;   // bytes per K row of the operand's K tile
+      const GPIC_LDS uint8_t *p =
+          kBNt == 256 ? (const GPIC_LDS uint8_t *)smem + (f < kTM ? a_half(ast) : b_half(bst)) + step * 64 * 256 +
+                            tr_off + (mnb ^ tr_x)
+                      : (const GPIC_LDS uint8_t *)smem + step * 64 * rowb +
+                            (f < kTM ? a_half(ast) + tr_off + (mnb ^ tr_x) : b_half(bst) + tr_offB + (mnb ^ tr_xB));
       v2i r[4];
 #pragma unroll
-      for (int q = 0; q < 4; q++) r[q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GPIC_LDS v2i *)(p + q * 8 * 256));
+      for (int q = 0; q < 4; q++) r[q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GPIC_LDS v2i *)(p + q * 8 * rowb));
       const v8i v{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
       if (f < kTM) fa[step][f] = v;
       else fb[step][f - kTM] = v;
@@ -496,7 +522,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
 #pragma unroll
         for (int j = 0; j < kNI; j++) {
           st16_t w = wv[j];
-          if (kMN && j >= 4) w = st16_t{w[2], w[3], w[0], w[1]};   // rows 16..31: halves exchanged
+          if (kMN && kRPI * j >= 16) w = st16_t{w[2], w[3], w[0], w[1]};   // rows 16..31: halves exchanged
           if (bias) {   // bf16(bf16(acc * s) + bias)
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
@@ -552,54 +578,51 @@ static int num_cus() {
   return cus;
 }
 
-// The K split: the number of splits s (and K tiles per split) that minimises a model of the run time. Work items
+// The plan: for each tile width, the number of K splits s (and K tiles per split) that minimises a model of the run
+// time; then the width. Work items
 // (tiles x splits) run in rounds of one per CU; a round lasts as long as its items' K tiles plus a fixed cost per
 // item (prologue, epilogue); splitting adds the reduce, which reads s fp32 partials of C and writes C. Model constants
 // from measured d12 and text-block shapes: a K tile takes ~1.45 us with every CU busy and less when a single round
 // leaves CUs idle (1.0 + 0.45 x the busy fraction: 1.03-1.18 us measured at 104 of 256), ~4 us per item (5 with fp32
 // partials), and the reduce ~4 us plus its bytes at ~5 TB/s. Split-K also needs N < 2^21 (the partials' 32-bit
 // buffer offsets).
-// Then the tile width at that split count (K-major operands only): the 256 x 128 tile does half the work per item at
-// ~0.59 of the time per K tile (measured over full rounds of d12 shapes: 0.57-0.60) and ~3 us per item, so it wins
-// where it fills CUs that 256 x 256 tiles leave idle (text-block shapes: 104 tiles of 256 x 256 on 256 CUs) or
-// evens out a partial last round. It is taken only for a predicted gain of 10% or more: the model treats a partial
-// last round of several as a full one, and near-ties went either way when measured (text qkv.fwd: 3 narrow rounds vs
-// 2 wide ones, 29.4 vs 30.0 us on one box, 33.3 vs 31.1 on another). The split count does not depend on the width,
-// so both operand layouts sum the same partials in the same order: their results are the same bits.
+// The tile width: the 256 x 128 tile does half the work per item at ~0.59 of the time per K tile (measured over
+// full rounds of d12 shapes: 0.57-0.60) and ~3 us per item, so it wins where it fills CUs that 256 x 256 tiles leave
+// idle (text-block shapes: 104 tiles of 256 x 256 on 256 CUs), evens out a partial last round, or needs fewer K
+// splits. The best narrow plan (over its own split counts) is taken only for a predicted gain of 10% or more over the
+// best wide one: the model treats a partial last round of several as a full one, and near-ties went either way when
+// measured (text qkv.fwd: 3 narrow rounds vs 2 wide ones, 29.4 vs 30.0 us on one box, 33.3 vs 31.1 on another). Both
+// operand layouts use the same plan, so they sum the same partials in the same order: their results are the same bits.
 constexpr double kNarrowKTile = 0.59, kNarrowItem = 3.0, kNarrowGain = 0.9;
-static Plan plan_gemm(int64_t M, int64_t N, int64_t K, bool narrow_ok) {
+static Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
   const int64_t ktiles = (K + kBK - 1) / kBK;
   const int64_t cus = num_cus();
   const int64_t tiles_m = (M + kBM - 1) / kBM;
-  auto model = [&](int bn, int64_t per, int64_t splits) {
-    const int64_t items = tiles_m * ((N + bn - 1) / bn) * splits;
-    const int64_t rounds = (items + cus - 1) / cus;
-    const double busy = rounds == 1 ? (double)items / (double)cus : 1.0;
-    const double ktile = bn == 256 ? 1.0 : kNarrowKTile, fixed = bn == 256 ? 4.0 : kNarrowItem;
-    double t = (double)rounds * ((double)per * ktile * (1.0 + 0.45 * busy) + fixed + (splits > 1 ? 1.0 : 0.0));
-    if (splits > 1) t += 4.0 + ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
-    return t;
-  };
   const int64_t max_splits = N < (1 << 21) ? std::min<int64_t>(ktiles, 64) : 1;
-  double best = 0.0;
-  int64_t best_per = ktiles;
-  for (int64_t s = 1; s <= max_splits; s++) {
-    const int64_t per = (ktiles + s - 1) / s;          // K tiles per split
-    const int64_t splits = (ktiles + per - 1) / per;   // splits actually needed
-    if (splits != s) continue;
-    const double t = model(256, per, splits);
-    if (s == 1 || t < best) {
-      best = t;
-      best_per = per;
+  Plan best[2];
+  double tbest[2] = {0.0, 0.0};
+  for (int c = 0; c < 2; c++) {
+    const int bn = c == 0 ? 256 : 128;
+    const double ktile = c == 0 ? 1.0 : kNarrowKTile, fixed = c == 0 ? 4.0 : kNarrowItem;
+    const int64_t tiles = tiles_m * ((N + bn - 1) / bn);
+    best[c] = Plan{(int)tiles_m, (int)((N + bn - 1) / bn), 1, (int)(std::max<int64_t>(ktiles, 1) * kBK), bn};
+    for (int64_t s = 1; s <= max_splits; s++) {
+      const int64_t per = (ktiles + s - 1) / s;          // K tiles per split
+      const int64_t splits = (ktiles + per - 1) / per;   // splits actually needed
+      if (splits != s) continue;
+      const int64_t items = tiles * splits;
+      const int64_t rounds = (items + cus - 1) / cus;
+      const double busy = rounds == 1 ? (double)items / (double)cus : 1.0;
+      double t = (double)rounds * ((double)per * ktile * (1.0 + 0.45 * busy) + fixed + (splits > 1 ? 1.0 : 0.0));
+      if (splits > 1) t += 4.0 + ((double)splits * 4.0 + 2.0) * (double)M * (double)N / 5.0e6;
+      if (s == 1 || t < tbest[c]) {
+        tbest[c] = t;
+        best[c].splits = (int)splits;
+        best[c].ksplit = (int)(per * kBK);
+      }
     }
   }
-  Plan p;
-  p.tiles_m = (int)tiles_m;
-  p.ksplit = (int)(best_per * kBK);
-  p.splits = ktiles == 0 ? 1 : (int)((ktiles + best_per - 1) / best_per);
-  p.bn = narrow_ok && ktiles > 0 && model(128, best_per, p.splits) < kNarrowGain * best ? 128 : 256;
-  p.tiles_n = (int)((N + p.bn - 1) / p.bn);
-  return p;
+  return ktiles > 0 && tbest[1] < kNarrowGain * tbest[0] ? best[1] : best[0];
 }
 
 // The launch shared by both operand layouts (arguments checked by the entry points).
@@ -610,8 +633,7 @@ static int launch_gemm(const uint8_t *A, int64_t lda, const float *sa, const uin
   if (M == 0 || N == 0) return GPIC_OK;
   if (K > 0 && (!A || !B)) return GPIC_EINVAL;
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && ((uintptr_t)bias & 7u))) return GPIC_EALIGN;
-  const Plan p =
-      K > 0 ? plan_gemm(M, N, K, !kMN) : Plan{(int)((M + kBM - 1) / kBM), (int)((N + kBN - 1) / kBN), 1, kBK, kBN};
+  const Plan p = K > 0 ? plan_gemm(M, N, K) : Plan{(int)((M + kBM - 1) / kBM), (int)((N + kBN - 1) / kBN), 1, kBK, kBN};
   float *P = nullptr;
   if (p.splits > 1) {
     const size_t need = (size_t)p.splits * M * N * sizeof(float);
@@ -624,9 +646,8 @@ static int launch_gemm(const uint8_t *A, int64_t lda, const float *sa, const uin
   const int slots = num_cus() & ~7;
   const int grid = work <= slots || slots < 8 ? work : slots;
   // the partial-K-tile load path is compiled only into the instance that needs it
-  auto *kernel = K % kBK ? gemm_tn_kernel<true, kMN, 256> : gemm_tn_kernel<false, kMN, 256>;
-  if constexpr (!kMN)
-    if (p.bn == 128) kernel = K % kBK ? gemm_tn_kernel<true, false, 128> : gemm_tn_kernel<false, false, 128>;
+  auto *kernel = p.bn == 128 ? (K % kBK ? gemm_tn_kernel<true, kMN, 128> : gemm_tn_kernel<false, kMN, 128>)
+                              : (K % kBK ? gemm_tn_kernel<true, kMN, 256> : gemm_tn_kernel<false, kMN, 256>);
   kernel<<<grid, kThreads, 0, st>>>(
       A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
       p.splits);
@@ -647,7 +668,7 @@ extern "C" {
 
 size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const Plan p = plan_gemm(M, N, K, false);   // (the split count does not depend on the tile width)
+  const Plan p = plan_gemm(M, N, K);
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 

@@ -198,15 +198,16 @@ def test_shape_sweep(dev, M, N, K, bias, lda_pad):
     (16, 16, 1, False, 0),           # one K row
     (4112, 2992, 1040, True, 32),    # padded leading dimensions, bias, partial K tile
     (9008, 4000, 512, False, 16),    # several work items per CU
-    (6592, 1024, 4096, True, 0),     # text-block w3 fwd shape: the K-major call takes 256 x 128 tiles, ragged M, bias
-    (704, 528, 9984, False, 0),      # 256 x 128 tiles with 16 K splits on the K-major side
+    (6592, 1024, 4096, True, 0),     # text-block w3 fwd shape: 256 x 128 tiles, ragged M, bias
+    (704, 528, 9984, False, 0),      # 256 x 128 tiles with 13 K splits, a partial last column of tiles (N = 528)
+    (1056, 528, 2000, True, 48),     # 256 x 128 tiles, padded leading dimensions, bias, partial K tile
 ])
 def test_mn_matches_tn(dev, M, N, K, bias, pad):
     """gpic_fp8_gemm_mn (both operands with K as the row index, the untransposed bytes of the wgrad) gives the same
     bits as gpic_fp8_gemm on the transposed operands: the MFMA sees the same values at every position (K padded
-    with zeros to a multiple of 16 for the TN call). Where the K-major call picks the 256 x 128 tile (the small
-    shapes here and the last two cases; the MN-major kernel has only 256 x 256 tiles), this is also the check that the
-    two tile widths give the same bits. Elementwise against the float64 product as well."""
+    with zeros to a multiple of 16 for the TN call). Both layouts get the same plan (tile width and K split); the
+    small shapes here, the text proj wgrad and the last three cases take the 256 x 128 tile, the others 256 x 256.
+    Elementwise against the float64 product as well."""
     g = torch.Generator(device=dev).manual_seed(M * 7 + N * 3 + K)
     a = (torch.randn(K, M + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :M]
     b = (torch.randn(K, N + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :N]
