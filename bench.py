@@ -56,6 +56,9 @@ def parse():
                    help="only copy a 1 GiB buffer (the known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE)")
     p.add_argument("--traffic", action="store_true",
                    help="only run each of the 12 GEMM shapes once, in the printed order (one counter row per shape)")
+    p.add_argument("--cast-traffic", action="store_true",
+                   help="only run the casts once each, in the printed order (one counter row per dispatch): config 2 "
+                        "warm and with L2 / MALL flushed, an fp32 weight-shaped cast, the d12 SwiGLU casts")
     p.add_argument("--step-only", type=int, default=0, metavar="N",
                    help="only run the d12 step N times (for a kernel-by-kernel trace of one step)")
     return p.parse_args()
@@ -93,6 +96,39 @@ def step(G, t):
     y2 = G.fp8_linear_f8(t["x_proj"], t["w_proj"])
     y3 = G.fp8_mlp_f8(t["x_mlp"], t["w12"], t["w3"])
     torch.autograd.backward([y1, y2, y3], [t["dy_qkv"], t["dy_proj"], t["dy_mlp"]])
+
+
+def config2_input(dev):
+    """Config 2: X [32768 x 1024] fp32 N(0,1) (seed 1), 1% of the columns x50, rounded once to bf16."""
+    import torch
+    gx = torch.Generator().manual_seed(1)
+    xc = torch.randn(M_TOK, C, generator=gx)
+    cols = torch.randperm(C, generator=gx)[:round(0.01 * C)]
+    xc[:, cols] *= 50.0
+    return xc.to(torch.bfloat16).to(dev)
+
+
+def cast_traffic(G, dev):
+    """Each cast once, for counter collection (one row per dispatch, in this order): config 2 (a warm-up call, then a
+    warm one, then one after a 512 MB write that flushes L2 / MALL), an fp32 weight [3072 x 1024] (DDP weights are
+    fp32), and the d12 SwiGLU casts of the step: the product cast of z [32768 x 8192] and the backward's dz cast."""
+    import torch
+    xc = config2_input(dev)
+    flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev).manual_seed(3)
+    w32 = torch.randn(3 * C, C, generator=g, device=dev) * C ** -0.5
+    z = torch.randn(M_TOK, 2 * H, generator=g, device=dev).to(torch.bfloat16)
+    da = (torch.randn(M_TOK, H, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    order = []
+    for name, fn in (("config2 warm-up", lambda: G.tcast(xc)), ("config2 warm", lambda: G.tcast(xc)),
+                     ("flush", lambda: flush.fill_(1)), ("config2 flushed", lambda: G.tcast(xc)),
+                     ("fp32 weight [3072 x 1024]", lambda: G.tcast(w32)),
+                     ("swiglu product cast z [32768 x 8192]", lambda: G.swiglu_tcast(z)),
+                     ("swiglu backward dz cast", lambda: G.swiglu_bwd_q(z, da))):
+        fn()
+        torch.cuda.synchronize()
+        order.append(name)
+    print(json.dumps({"cast_order": order}), flush=True)
 
 
 def time_region(fn, steps, warmup):
@@ -255,6 +291,10 @@ def main():
         print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4, "launches": 3}), flush=True)
         return
 
+    if args.cast_traffic:
+        cast_traffic(G, dev)
+        return
+
     if args.traffic:
         shapes = gemm_shapes()
         ops = gemm_operands(G, dev, shapes)
@@ -298,11 +338,7 @@ def main():
                            "tflops": round(2.0 * m * n * k / tm / 1e9, 1)}
 
     # ---- config 2: the cast alone
-    gx = torch.Generator().manual_seed(1)
-    xc = torch.randn(M_TOK, C, generator=gx)
-    cols = torch.randperm(C, generator=gx)[:round(0.01 * C)]
-    xc[:, cols] *= 50.0
-    xc = xc.to(torch.bfloat16).to(dev)
+    xc = config2_input(dev)
     cast_ms = time_region(lambda: G.tcast(xc), 50, 10)
     cast_bytes = xc.numel() * 3 + 4
     # the same with L2 / MALL flushed before each call (a 512 MB write between the timed launches)
