@@ -50,17 +50,15 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 #define GPIC_LDS __attribute__((address_space(3)))
 
-constexpr int kBM = 256, kBN = 256, kBK = 128;
+constexpr int kBM = 256, kBN = 256, kBK = 128;         // the wide tile (the narrow one is 256 x 128: kBNt)
 constexpr int kThreads = 512;                          // 8 waves: 2 groups x 4
-constexpr int kWTM = 64, kWTN = 128;                   // wave tile
-constexpr int kTM = kWTM / 32, kTN = kWTN / 32;        // 32 x 32 MFMA tiles per wave: 2 x 4
-constexpr int kHalfBytes = kBM * kBK;                  // 32 KiB: one operand's K tile (kBM == kBN)
+constexpr int kWTM = 64;                               // wave tile rows (columns: kWTNt, 128 or 64)
+constexpr int kTM = kWTM / 32;                         // 32 x 32 MFMA tiles per wave in M: 2
+constexpr int kHalfBytes = kBM * kBK;                  // 32 KiB: an A K tile (and a wide tile's B K tile)
 constexpr int kAStages = 3, kBStages = 2;              // A is sent two K tiles ahead, B one
-constexpr int kBBase = kAStages * kHalfBytes;          // B stages follow the A stages
-constexpr int kLdsBytes = (kAStages + kBStages) * kHalfBytes;   // 160 KiB, all of gfx950's LDS
-static_assert(kBM == kBN, "A and B K tiles have the same size");
+constexpr int kBBase = kAStages * kHalfBytes;          // B stages follow the A stages (160 KiB in all for the wide tile)
 constexpr int kLoaders = 4;                            // waves of a group
-constexpr int kLoads = kBM / 8 / kLoaders;             // 8 wave-instructions (1 KiB each) per operand K tile per wave
+constexpr int kLoads = kBM / 8 / kLoaders;             // 8 wave-instructions (1 KiB each) per A K tile per wave
 constexpr int kGroupM = 4;
 constexpr int kBufferFlags = 0x00020000;               // raw buffer descriptor word 3 for gfx9-family targets
 constexpr int kOOB = (int)0x80000000;                  // an offset past any descriptor's range: reads zeros
@@ -154,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- loads. A K tile of one operand is 256 rows x 128 bytes = 32 wave-instructions of 1 KiB, 8 per wave of a
-  // group. Instruction i of a wave fills rows [R0, R0 + 8), R0 = (i * 4 + wave % 4) * 8; lane j writes slot j & 7
+  // group (the narrow tile's B K tile: 128 rows, 4 per wave). Instruction i of a wave fills rows [R0, R0 + 8), R0 = (i * 4 + wave % 4) * 8; lane j writes slot j & 7
   // of row R0 + j / 8, i.e. K chunk (j & 7) ^ swz(row). swz(row) does not depend on i, so every instruction's offset
   // is a per-lane base plus i * 32 rows. Row offsets stay in the VGPR offset (the part the descriptor
   // range-checks); only the K position goes to the scalar offset.
