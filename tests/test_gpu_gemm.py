@@ -245,3 +245,43 @@ def test_mn_past_32bit_offsets_falls_back(dev):
     c = G.fp8_gemm_mn(a, s1, b, s1)
     want = G.fp8_gemm_mn(a.contiguous(), s1, b, s1)
     assert torch.equal(c.view(torch.int16), want.view(torch.int16))
+
+
+def _sweep_shapes():
+    """A seeded list of ragged problems (M any size, every other one a multiple of 16; N and K multiples of 16),
+    spread over both tile widths, unsplit and split K, with partial last tiles in every dimension."""
+    rng = np.random.default_rng(20261201)
+    out = []
+    for i in range(40):
+        m = int(rng.integers(1, 5000)) if i % 4 else int(rng.integers(1, 300))
+        if i % 2 == 0:
+            m = (m + 15) // 16 * 16      # half the cases also run the MN-major layout
+        n = 16 * int(rng.integers(1, 260))
+        k = 16 * int(rng.integers(1, 700)) if i % 3 else 16 * int(rng.integers(700, 2200))
+        out.append((m, n, k, bool(i % 2), int(rng.integers(0, 3)) * 16))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,bias,pad", _sweep_shapes())
+def test_random_shape_sweep(dev, M, N, K, bias, pad):
+    """Seeded ragged shapes through the planner's choices (tile width, K split): the K-major GEMM within the
+    elementwise bound of the float64 product and the bias added after the bf16 rounding; where M % 16 == 0, the
+    MN-major GEMM on the transposed bytes gives the same bits."""
+    g = torch.Generator(device=dev).manual_seed(M * 31 + N * 7 + K)
+    a = (torch.randn(M, K + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :K]
+    b = (torch.randn(N, K + pad, generator=g, device=dev) * 20).clamp(-448, 448).to(E4)[:, :K]
+    sa = torch.tensor([0.013], device=dev)
+    sb = torch.tensor([0.019], device=dev)
+    bv = (torch.randn(N, generator=g, device=dev) * 0.5).to(torch.bfloat16) if bias else None
+    c0 = G.fp8_gemm(a, sa, b, sb)
+    if M * N * K <= 1 << 33:
+        assert_elementwise(c0, a, 0.013, b, 0.019)
+    else:
+        assert rel(c0, ref_fp32(a, sa, b, sb)) < 4e-3
+    if bias:
+        c = G.fp8_gemm(a, sa, b, sb, bv)
+        assert torch.equal(c, (c0.float() + bv.float()).to(torch.bfloat16))
+    if M % 16 == 0:
+        at = a.t().contiguous()
+        bt = b.t().contiguous()
+        assert torch.equal(bits_t(G.fp8_gemm_mn(at, sa, bt, sb)), bits_t(c0))
