@@ -355,6 +355,20 @@ def main():
     cast_cold_ms = sorted(cold)[len(cold) // 2]
     del flush
 
+    # ---- the other casts: an fp32 weight-shaped tensor (DDP keeps fp32 weights) and the d12 SwiGLU casts of the step,
+    # as device time (short kernels: Python's issue time would show in a back-to-back loop)
+    gc = torch.Generator(device=dev).manual_seed(3)
+    w32 = torch.randn(3 * C, C, generator=gc, device=dev) * C ** -0.5
+    w32_ms = time_device(lambda: G.tcast(w32), 20, 3)
+    z = torch.randn(M_TOK, 2 * H, generator=gc, device=dev).to(torch.bfloat16)
+    da = (torch.randn(M_TOK, H, generator=gc, device=dev) * 0.1).to(torch.bfloat16)
+    sw_ms = time_device(lambda: G.swiglu_tcast(z), 10, 2)
+    swb_ms = time_device(lambda: G.swiglu_bwd_q(z, da), 10, 2)
+    del z, da
+    w32_bytes = w32.numel() * 5 + 4
+    sw_min, sw_moved = M_TOK * H * 5, M_TOK * H * 9               # min: read z, write q; as built: + write a, read a
+    swb_min, swb_moved = M_TOK * H * 8, M_TOK * H * 14            # min: read z, da, write dzq; as built: z, da twice
+
     # ---- config 5: the d18 block (C = 1792, H = 7168) with 1% outlier activation channels, fwd + bwd
     C18, H18 = 1792, 7168
     t18 = make_inputs(dev, seed=5, C=C18, H=H18, outliers=0.01)
@@ -436,6 +450,19 @@ def main():
                  "frac": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4),
                  "algorithmic_bytes": cast_bytes, "us_l2_flushed": round(cast_cold_ms * 1e3, 2),
                  "frac_l2_flushed": round(cast_bytes / cast_cold_ms / 1e6 / PEAK_HBM_GBS, 4)},
+        "cast_fp32_weight": {"workload": "fp32 [3072 x 1024] -> e4m3 + amax + scale (a DDP weight)",
+                             "us": round(w32_ms * 1e3, 2) if w32_ms else None, "algorithmic_bytes": w32_bytes,
+                             "achieved_GBs": round(w32_bytes / w32_ms / 1e6, 1) if w32_ms else None},
+        "swiglu": {"workload": "d12 SwiGLU casts: product cast of z [32768 x 8192] and the backward's dz cast "
+                               "(z, da [32768 x 4096]), device time",
+                   "fwd_us": round(sw_ms * 1e3, 1) if sw_ms else None, "fwd_min_bytes": sw_min,
+                   "fwd_moved_bytes": sw_moved,
+                   "fwd_GBs_moved": round(sw_moved / sw_ms / 1e6, 1) if sw_ms else None,
+                   "fwd_frac_min": round(sw_min / sw_ms / 1e6 / PEAK_HBM_GBS, 4) if sw_ms else None,
+                   "bwd_us": round(swb_ms * 1e3, 1) if swb_ms else None, "bwd_min_bytes": swb_min,
+                   "bwd_moved_bytes": swb_moved,
+                   "bwd_GBs_moved": round(swb_moved / swb_ms / 1e6, 1) if swb_ms else None,
+                   "bwd_frac_min": round(swb_min / swb_ms / 1e6 / PEAK_HBM_GBS, 4) if swb_ms else None},
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
                       "tflops": round(fl18 / ms18 / 1e9, 1)},
