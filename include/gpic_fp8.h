@@ -13,10 +13,13 @@
  *   - `stream` is a hipStream_t (void * here so this header needs no HIP headers). Work is enqueued on it; nothing
  *     synchronises with the host, nothing is allocated, and scales stay on the device.
  *   - `ws` is a caller-provided device workspace of at least the size the matching *_workspace_bytes() returns,
- *     16-byte aligned. The cast workspace is zeroed once when it is created and then kept for the cast calls: the
- *     single-pass casts tag their partial maxima with a call number, and a stale word from an earlier call never
- *     matches a later one; nothing else carries over between calls. Two calls that may run concurrently (different
- *     streams) need different workspaces.
+ *     16-byte aligned. The cast workspace carries state from call to call and must be zeroed once, when it is created
+ *     (by any means; it is never to be cleared again while it is in use): the single-pass casts tag their partial
+ *     maxima with a call number kept in the workspace itself (an epoch word that each call's last workgroup advances
+ *     on the device), so a stale word from an earlier call never matches a later one. Because the number lives on the
+ *     device, a cast captured in a HIP graph takes a new number on every replay. Calls that may run at the same time
+ *     (different streams, or graphs replayed concurrently) need different workspaces; calls ordered on one stream may
+ *     share one. The GEMM workspace (split-K partials) is scratch of one call.
  *   - Tensor data pointers are 16-byte aligned; leading dimensions are in elements.
  *   - Return value: 0 on success, a negative GPIC_E* code for invalid arguments (nothing was launched), or a positive
  *     hipError_t from the launch.
@@ -49,8 +52,8 @@ const char *gpic_fp8_status_string(int status);
  * the single-pass casts' tagged partials). */
 size_t gpic_fp8_cast_workspace_bytes(void);
 
-/* Tuning and test knob (process-wide, not synchronised with calls in flight; no counterpart in the reference, whose
- * casts are always two Triton launches). gpic_fp8_tcast and gpic_fp8_tcast_t cast a bf16 (or, flat, fp32) tensor
+/* Tuning and test knob (process-wide; a call made on another thread at the same time sees the old or the new
+ * setting; no counterpart in the reference, whose casts are always two Triton launches). gpic_fp8_tcast and gpic_fp8_tcast_t cast a bf16 (or, flat, fp32) tensor
  * that fits in the chip's registers in one launch (x read once) and larger ones in two (amax pass, then cast pass).
  * enabled = 0 forces the two-pass path; wait_us bounds how long a workgroup of the single pass waits for another's
  * partial maximum before computing it from x itself (< 0: the default, 200 us; 0 makes every missing partial a direct
@@ -132,7 +135,7 @@ size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
  *   C[m, n] = bf16(sa * sb * sum_k A[m, k] * B[n, k]);  if bias: C[m, n] = bf16(C[m, n] + bias[n])
  *   A [M, K] e4m3, row stride lda;  B [N, K] e4m3, row stride ldb;  C [M, N] bf16, row stride ldc
  *   sa, sb   device fp32 scalars (the dequantization scales);  bias: [N] bf16 or NULL
- *   K % 16 == 0, N % 16 == 0, lda / ldb % 16 == 0, ldc % 8 == 0; any M.
+ *   K % 16 == 0, N % 16 == 0, lda / ldb % 16 == 0, ldc % 8 == 0; lda, ldb < 2^23, ldc < 2^22; any M.
  *   fast_accum is accepted for interface parity with use_fast_accum: MFMA accumulates in fp32 either way.
  * The fp32 accumulation is the MFMA's; the result matches the scaled matmul of the same operands within the
  * relative Frobenius error the path promises (1e-2), and is deterministic (split-K partials are summed in a fixed
@@ -147,7 +150,7 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
  * untransposed e4m3 bytes of the layer's output gradient and input.
  *   C[m, n] = bf16(sa * sb * sum_k A[k, m] * B[k, n]);  if bias: C[m, n] = bf16(C[m, n] + bias[n])
  *   A [K, M] e4m3, row stride lda;  B [K, N] e4m3, row stride ldb;  C [M, N] bf16, row stride ldc
- *   M % 16 == 0, N % 16 == 0, lda / ldb % 16 == 0, ldc % 8 == 0, K * lda and K * ldb < 2^31; any K.
+ *   M % 16 == 0, N % 16 == 0, lda / ldb % 16 == 0, ldc % 8 == 0, K * lda and K * ldb < 2^31, ldc < 2^22; any K.
  * Bit-identical to gpic_fp8_gemm on the transposed operands (A^T [M, K], B^T [N, K]): the same products summed in
  * the same order, with the same workspace (gpic_fp8_gemm_workspace_bytes(M, N, K)).
  * No counterpart in the reference (its wgrads are bf16, fp8_native.py:202, 264-265); the FP8-wgrad extension.

@@ -1,12 +1,19 @@
 // Per-tensor current-amax e4m3 casts for gfx950: the flat cast (tcast), the cast with a transposed copy (for the
 // dgrad / wgrad operands), the SwiGLU product cast and the SwiGLU backward.
 //
-// Every cast is two stream-ordered launches with no state between calls:
-//   1. an amax pass: each workgroup reduces its share to one partial maximum (|x| bit patterns, NaN ignored) and
-//      writes it to partial[blockIdx.x] -- no atomics, so nothing has to be zeroed beforehand;
-//   2. a cast pass: each workgroup folds all partials (<= kMaxParts words, served from L2), derives the scale with
-//      IEEE division and streams its share: 128-bit loads, 128-bit e4m3 stores.
-// Workgroup 0 of pass 2 writes the dequantization scale.
+// Two designs, chosen per call by size:
+//  * Single pass (bf16 tensors of at most 64 MiB, fp32 of 48 MiB; hybrids up to 8x that): ONE launch. Each workgroup
+//    holds its share of x in registers, publishes a partial maximum tagged with the call's number, folds every
+//    workgroup's partial and casts from its registers (3 B/elem moved for bf16). The call number lives in the
+//    workspace (an epoch word the last workgroup of each call advances), so the workspace carries state from call to
+//    call: it is zeroed once when created, and calls that may run at the same time (different streams) need
+//    different workspaces. Graph capture is fine: a replayed launch reads the epoch the previous call left.
+//  * Two passes (larger tensors, the SwiGLU kernels, fp32 transposing casts): two stream-ordered launches,
+//      1. an amax pass: each workgroup reduces its share to one partial maximum (|x| bit patterns, NaN ignored) and
+//         writes it to partial[blockIdx.x] -- no atomics, so nothing has to be zeroed beforehand;
+//      2. a cast pass: each workgroup folds all partials (<= kMaxParts words, served from L2), derives the scale with
+//         IEEE division and streams its share: 128-bit loads, 128-bit e4m3 stores.
+//    Workgroup 0 of pass 2 writes the dequantization scale. The partials are scratch of the call in the workspace.
 #include <algorithm>
 #include <atomic>
 
@@ -840,9 +847,12 @@ static void launch_cast_t(SrcBF16 src, int64_t rows, int64_t cols, int nparts, u
 // registers, reduces it to a partial maximum and publishes it, takes the maximum of all workgroups' partials, and
 // casts from its registers. x is read once: 3 B/elem moved for bf16 instead of 5.
 //
-// Partials: one 64-bit word per workgroup, (call tag << 32) | amax bits, in the workspace. The tag is a host-side call
-// counter passed to the kernel, so a word left by any earlier call (or by a late workgroup of one) never matches; the
-// workspace is zeroed once, when it is created, and tag 0 is never used.
+// Partials: one 64-bit word per workgroup, (call tag << 32) | amax bits, in the workspace. The tag is the workspace's
+// epoch + 1 (0 skipped): every workgroup reads the epoch at its fold, and the last workgroup of the call to finish its
+// fold (a counter in the workspace reaches the grid size) stores the tag as the new epoch and clears the counter. So
+// the next call on the workspace -- stream-ordered after this one, or the next replay of a captured graph -- uses the
+// next tag, and a word left by an earlier call never matches. The workspace is zeroed once, when it is created, and
+// tag 0 is never used; the tag repeats after 2^32 calls on one workspace.
 // No workgroup waits on another without a bound: a partial that has not appeared within the wait bound (kOnceWaitUs by
 // default, about 8x a whole call) is computed by the waiting workgroup itself, from that workgroup's share of x, and
 // published for the other waiters. So the launch needs no co-residency guarantee (a plain launch; the cooperative one
@@ -851,8 +861,10 @@ static void launch_cast_t(SrcBF16 src, int64_t rows, int64_t cols, int nparts, u
 constexpr int kMaxOnceBlocks = 1024;
 constexpr size_t kOnceTagged = 28 * 1024;                         // uint64_t[kMaxOnceBlocks] tagged partials
 constexpr size_t kOnceFallback = kOnceTagged + 8 * kMaxOnceBlocks;  // uint32_t: partials computed by a waiter
+constexpr size_t kOnceEpoch = kOnceFallback + 4;                    // uint32_t: the tag of the last call
+constexpr size_t kOnceDone = kOnceFallback + 8;                     // uint32_t: workgroups of this call done folding
 static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kOnceTagged, "two-pass scratch overlaps the single-pass words");
-static_assert(kOnceFallback + 4 <= kCastWorkspaceBytes, "cast workspace too small");
+static_assert(kOnceDone + 4 <= kCastWorkspaceBytes, "cast workspace too small");
 template <typename T>
 constexpr int kOnceWords = sizeof(T) == 2 ? 16 : 12;   // 16-byte words a thread of the flat kernel holds (fp32: 12,
                                                         // which its wider narrowing code needs to fit 128 VGPRs)
@@ -919,21 +931,29 @@ __device__ __forceinline__ uint32_t words_amax(const u32x4 (&w)[W]) {
   return m;
 }
 
-// Publishes this workgroup's maximum m (held by every thread) as call `tag`'s partial, then returns the maximum over
+// Publishes this workgroup's maximum m (held by every thread) as this call's partial, then returns the maximum over
 // all G partials to every thread. share_max(c) must return (to every thread of the workgroup) workgroup c's maximum
-// computed from x; it runs only for a partial that did not appear within wait_ticks.
+// computed from x; it runs only for a partial that did not appear within wait_ticks. The call's tag comes from the
+// workspace's epoch; the last workgroup to finish its fold advances the epoch (see above).
 template <class ShareMax>
-__device__ __forceinline__ uint32_t once_fold(uint32_t m, uint32_t tag, void *ws, uint32_t wait_ticks,
-                                              ShareMax share_max) {
+__device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wait_ticks, ShareMax share_max) {
   __shared__ int missing[kMaxOnceBlocks];
   __shared__ int nmissing;
+  __shared__ uint32_t stag;
   uint64_t *tagged = reinterpret_cast<uint64_t *>((char *)ws + kOnceTagged);
+  uint32_t *epoch = reinterpret_cast<uint32_t *>((char *)ws + kOnceEpoch);
+  uint32_t *done = reinterpret_cast<uint32_t *>((char *)ws + kOnceDone);
   const int G = gridDim.x;
   if (threadIdx.x == 0) {
-    __hip_atomic_store(tagged + blockIdx.x, ((uint64_t)tag << 32) | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the epoch cannot change before this workgroup has counted itself done (below)
+    uint32_t t = __hip_atomic_load(epoch, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    t = t ? t : 1u;
+    stag = t;
+    __hip_atomic_store(tagged + blockIdx.x, ((uint64_t)t << 32) | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     nmissing = 0;
   }
   __syncthreads();
+  const uint32_t tag = stag;
   uint32_t g = m;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   for (int i = threadIdx.x; i < G; i += blockDim.x) {
@@ -974,6 +994,13 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, uint32_t tag, void *ws
       __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)computed,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  // Done with the partials (every thread has passed the barriers above after its last read of them). The last of the
+  // G workgroups to get here ends the call's use of the words: the next call takes the next tag.
+  if (threadIdx.x == 0 &&
+      __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)G - 1u) {
+    __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(epoch, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
   return g;
 }
 
@@ -985,7 +1012,7 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, uint32_t tag, void *ws
 template <typename T>
 __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__ x, int64_t n, int wpt,
                                                            int64_t sgroups, uint8_t *__restrict__ q,
-                                                           float *__restrict__ dequant, void *ws, uint32_t tag,
+                                                           float *__restrict__ dequant, void *ws,
                                                            uint32_t wait_ticks) {
   constexpr int kE = 16 / sizeof(T);   // elements per word
   const int64_t nw = n / kE;
@@ -1031,7 +1058,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
   uint32_t m0 = max(words_amax<T, kW>(w), tail_amax());
   if (sgroups > 0) m0 = max(m0, stream_amax(blockIdx.x));
   const uint32_t m = block_max_u32(m0);
-  const uint32_t g = once_fold(m, tag, ws, wait_ticks, [&](int c) {
+  const uint32_t g = once_fold(m, ws, wait_ticks, [&](int c) {
     uint32_t a = tail_amax();
     for (int j = 0; j < wpt; j++) {
       const int64_t i = word(c, j);
@@ -1087,7 +1114,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
 __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows,
                                                              int64_t cols, uint8_t *__restrict__ q, int64_t ldq,
                                                              uint8_t *__restrict__ qt, int64_t ldt,
-                                                             float *__restrict__ dequant, void *ws, uint32_t tag,
+                                                             float *__restrict__ dequant, void *ws,
                                                              uint32_t wait_ticks) {
   static_assert(kOnceTiles == 2, "two tiles per workgroup");
   __shared__ uint32_t tile[kTT * kTPitch];
@@ -1112,7 +1139,7 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
     load_tile_bf16(x, ld, rows, cols, r0_of(t), c0_of(t), S);
     m = max(m, words_amax<uint16_t, kTPer>(S));
   }
-  const uint32_t g = once_fold(block_max_u32(m), tag, ws, wait_ticks, [&](int c) {
+  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int c) {
     uint32_t a = 0;
     for (int64_t t = c; t < tiles; t += G) {
       const int64_t r0 = r0_of(t), c0 = c0_of(t);
@@ -1149,66 +1176,62 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
 }
 
 // Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and
-// the wait bound in microseconds.
-static int g_once_enabled = 1;
-static int g_once_wait_us = kOnceWaitUs;
-static std::atomic<uint32_t> g_once_calls{0};
+// the wait bound in microseconds. Atomic: a call on another thread reads either the old or the new setting.
+static std::atomic<int> g_once_enabled{1};
+static std::atomic<int> g_once_wait_us{kOnceWaitUs};
 
-static uint32_t once_next_tag() {
-  uint32_t t = ++g_once_calls;
-  while (t == 0) t = ++g_once_calls;   // 0 is the zeroed workspace's tag
-  return t;
-}
-
-// Workgroups of `kernel` (256 threads) that the device holds at once; computed once per kernel (`cache`).
-static int once_capacity(const void *kernel, int *cache) {
-  if (*cache < 0) {
-    int dev = 0, per = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess)
-      per = 0;
+// Workgroups of `kernel` (256 threads) the current device holds at once, capped at kMaxOnceBlocks; cached per device
+// in `cache` (one per kernel, slots initialised to -1).
+static int once_capacity(const void *kernel, DeviceCache &cache) {
+  return per_device(cache, [kernel](int dev) {
+    int per = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess) per = 0;
     (void)hipGetLastError();
-    *cache = std::min(per * cus, kMaxOnceBlocks);
-  }
-  return *cache;
+    return std::min(per * device_cus(dev), kMaxOnceBlocks);
+  });
 }
 
 // s_memrealtime counts at 100 MHz on this target
-static uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us) * 100u; }
+static uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(std::memory_order_relaxed)) * 100u; }
+
+static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t;
+struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
+  DeviceCacheInit() {
+    for (int i = 0; i < kMaxDevices; i++) g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = -1;
+  }
+};
+static DeviceCacheInit g_device_cache_init;
 
 // The single-pass flat cast when x fits, as a hybrid up to kHybridFlat times that (false, nothing launched, above).
 template <typename T>
 static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant, void *ws, hipStream_t st) {
-  static int cache = -1;
-  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T>), &cache);
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T>),
+                                sizeof(T) == 2 ? g_cap_flat_bf16 : g_cap_flat_f32);
   constexpr int kE = 16 / sizeof(T);
   const int64_t nw = n / kE;
   const int64_t held = (int64_t)kOnceWords<T> * 256 * cap;   // words the grid holds in registers
-  if (!g_once_enabled || cap <= 0 || n <= 0 || nw > kHybridFlat * held) return false;
+  if (!g_once_enabled.load(std::memory_order_relaxed) || cap <= 0 || n <= 0 || nw > kHybridFlat * held) return false;
   if (nw > held) {   // hybrid: every workgroup holds its full share, the rest is streamed
     const int64_t sgroups = (nw - held + 255) / 256;
-    cast_once_kernel<T><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_next_tag(),
-                                             once_wait_ticks());
+    cast_once_kernel<T><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_wait_ticks());
     return true;
   }
   const int64_t groups = std::max<int64_t>(1, (nw + 255) / 256);   // 256-word groups
   const int grid = (int)std::min<int64_t>(groups, cap);
   const int wpt = (int)((groups + grid - 1) / grid);
-  cast_once_kernel<T><<<grid, 256, 0, st>>>(x, n, wpt, 0, q, dequant, ws, once_next_tag(), once_wait_ticks());
+  cast_once_kernel<T><<<grid, 256, 0, st>>>(x, n, wpt, 0, q, dequant, ws, once_wait_ticks());
   return true;
 }
 
 // The single-pass transposing cast of a bf16 source when it fits (false, nothing launched, otherwise).
 static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,
                                 float *dequant, void *ws, hipStream_t st) {
-  static int cache = -1;
-  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), &cache);
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), g_cap_t);
   const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
-  if (!g_once_enabled || cap <= 0 || tiles <= 0 || tiles > (int64_t)kHybridTiles * cap) return false;
+  if (!g_once_enabled.load(std::memory_order_relaxed) || cap <= 0 || tiles <= 0 || tiles > (int64_t)kHybridTiles * cap)
+    return false;
   const int grid = (int)std::min<int64_t>(tiles, cap);
-  cast_t_once_kernel<<<grid, 256, 0, st>>>(x, cols, rows, cols, q, cols, qt, ldt, dequant, ws, once_next_tag(),
-                                           once_wait_ticks());
+  cast_t_once_kernel<<<grid, 256, 0, st>>>(x, cols, rows, cols, q, cols, qt, ldt, dequant, ws, once_wait_ticks());
   return true;
 }
 
@@ -1224,8 +1247,8 @@ extern "C" {
 size_t gpic_fp8_cast_workspace_bytes(void) { return kCastWorkspaceBytes; }
 
 void gpic_fp8_set_single_pass(int enabled, int wait_us) {
-  g_once_enabled = enabled != 0;
-  g_once_wait_us = wait_us < 0 ? kOnceWaitUs : wait_us;
+  g_once_enabled.store(enabled != 0, std::memory_order_relaxed);
+  g_once_wait_us.store(wait_us < 0 ? kOnceWaitUs : wait_us, std::memory_order_relaxed);
 }
 
 int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *ws, void *stream) {

@@ -566,15 +566,15 @@ struct Plan {
   int tiles_m, tiles_n, splits, ksplit, bn;   // bn: the tile width, 256 or 128
 };
 
-static int num_cus() {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+// Compute units of the current device (cached per device).
+static DeviceCache g_cus;
+struct CusInit {
+  CusInit() {
+    for (int i = 0; i < kMaxDevices; i++) g_cus[i] = -1;
   }
-  return cus;
-}
+};
+static CusInit g_cus_init;
+static int num_cus() { return per_device(g_cus, device_cus); }
 
 // The plan: for each tile width, the number of K splits s (and K tiles per split) that minimises a model of the run
 // time; then the width. Work items
@@ -676,7 +676,8 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
   (void)fast_accum;
   if (M < 0 || N < 0 || K < 0 || !sa || !sb || (M > 0 && N > 0 && !C)) return GPIC_EINVAL;
   if (K % 16 != 0 || N % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldc % 8 != 0) return GPIC_ESHAPE;
-  if (lda < K || ldb < K || ldc < N || lda >= (1 << 23) || ldb >= (1 << 23) || M >= (1 << 30) || N >= (1 << 30))
+  // (the epilogue's C offsets, row within the tile x ldc x 2 bytes, are 32-bit: ldc < 2^22)
+  if (lda < K || ldb < K || ldc < N || lda >= (1 << 23) || ldb >= (1 << 23) || ldc >= (1 << 22) || M >= (1 << 30))
     return GPIC_ESHAPE;
   return launch_gemm<false>(A, lda, sa, B, ldb, sb, bias, C, ldc, M, N, K, ws, ws_bytes, (hipStream_t)stream);
 }
@@ -686,9 +687,9 @@ int gpic_fp8_gemm_mn(const uint8_t *A, int64_t lda, const float *sa, const uint8
                      size_t ws_bytes, void *stream) {
   if (M < 0 || N < 0 || K < 0 || !sa || !sb || (M > 0 && N > 0 && !C)) return GPIC_EINVAL;
   if (M % 16 != 0 || N % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldc % 8 != 0) return GPIC_ESHAPE;
-  // every load offset (K row x row stride) is a 32-bit buffer offset
+  // every load offset (K row x row stride) is a 32-bit buffer offset, and so is every C offset (ldc < 2^22)
   if (lda < M || ldb < N || ldc < N || K * lda >= (int64_t(1) << 31) || K * ldb >= (int64_t(1) << 31) ||
-      M >= (1 << 30) || N >= (1 << 30))
+      ldc >= (1 << 22) || M >= (1 << 30))
     return GPIC_ESHAPE;
   return launch_gemm<true>(A, lda, sa, B, ldb, sb, bias, C, ldc, M, N, K, ws, ws_bytes, (hipStream_t)stream);
 }

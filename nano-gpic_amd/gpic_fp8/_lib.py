@@ -7,6 +7,7 @@ torch is imported before the library is opened, so libgpic_fp8.so binds to the H
 """
 import ctypes
 import os
+import threading
 
 import torch
 
@@ -80,7 +81,7 @@ def aligned(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-_WORKSPACES = {}
+_WORKSPACES = {}   # (device index, stream handle) -> the cast workspace of that stream
 
 
 def set_single_pass(enabled=True, wait_us=-1):
@@ -89,14 +90,45 @@ def set_single_pass(enabled=True, wait_us=-1):
     lib().gpic_fp8_set_single_pass(int(bool(enabled)), int(wait_us))
 
 
+def _new_workspace(index, nbytes):
+    """Device memory for a cast workspace, outside any CUDA-graph memory pool where that is possible. During a
+    cudagraph-tree warm-up, torch serves every allocation of the current thread from the graph's private pool, and a
+    workspace kept in this module's cache there would be live storage the trees do not account for (they refuse it).
+    So it is allocated by a short-lived helper thread, whose allocations come from the ordinary pool. While the
+    current stream is capturing (a first cast inside a torch.cuda.graph capture) a fresh device allocation elsewhere
+    could break the capture, so the capture's own pool serves it and the graph keeps it alive."""
+    dev = torch.device("cuda", index)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    out = {}
+
+    def alloc():
+        try:
+            out["ws"] = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+        except BaseException as e:   # re-raised on the caller's thread
+            out["err"] = e
+
+    t = threading.Thread(target=alloc, name="gpic_fp8-workspace")
+    t.start()
+    t.join()
+    if "err" in out:
+        raise out["err"]
+    return out["ws"]
+
+
 def cast_workspace(device):
     """The cast workspace of `device`'s current stream: partial maxima, the SwiGLU sigmoid table and the single-pass
-    casts' call counter. Created zeroed once per (device, stream) and kept: the counter must survive between calls,
-    and casts on different streams, which may overlap, get different workspaces."""
+    casts' tagged partials with their call counter (an epoch word the kernels advance on the device). Created once per
+    (device, stream) and kept: the counter must survive from call to call, and casts on different streams, which may
+    overlap, get different workspaces. It is zeroed with a fill kernel on the stream that uses it, so under graph
+    capture the fill is part of the graph (clearing it again on every replay, which the epoch scheme allows) and no
+    memset node is recorded."""
     device = torch.device(device)
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_ptr(device))
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(index).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None:
-        n = lib().gpic_fp8_cast_workspace_bytes()
-        ws = _WORKSPACES[key] = torch.zeros(n // 4, dtype=torch.int32, device=device)
+        ws = _new_workspace(index, lib().gpic_fp8_cast_workspace_bytes())
+        ws.zero_()
+        _WORKSPACES[key] = ws
     return ws

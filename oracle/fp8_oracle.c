@@ -9,7 +9,10 @@
  * against closed forms (tests/test_oracle.py) and then used to check the HIP kernels bit for bit.
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off: every multiply and add is rounded on its own unless the code
- * calls fmaf explicitly, which is what the device code does too).
+ * calls fmaf explicitly, which is what the device code does too). The element loops are split over threads with
+ * OpenMP (-fopenmp; OMP_NUM_THREADS sets how many): each element's arithmetic is the same scalar code whatever thread
+ * runs it, and the maxima are reduced with max, which does not depend on order, so the results do not depend on the
+ * thread count.
  */
 #include <math.h>
 #include <stdint.h>
@@ -51,6 +54,7 @@ uint8_t gpo_e4m3(float f) {
 }
 
 void gpo_e4m3_n(const float *x, int64_t n, uint8_t *q) {
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; i++) q[i] = gpo_e4m3(x[i]);
 }
 
@@ -69,6 +73,7 @@ float gpo_e4m3_to_f32(uint8_t b) {
  * so NaN elements take no part (an all-NaN tensor has amax 0). */
 uint32_t gpo_amax_bf16(const uint16_t *x, int64_t n) {
     uint32_t m = 0;
+#pragma omp parallel for schedule(static) reduction(max : m)
     for (int64_t i = 0; i < n; i++) {
         uint32_t a = ((uint32_t)(x[i] & 0x7fffu)) << 16;
         if (a > 0x7f800000u) continue;
@@ -79,6 +84,7 @@ uint32_t gpo_amax_bf16(const uint16_t *x, int64_t n) {
 
 uint32_t gpo_amax_f32(const float *x, int64_t n) {
     uint32_t m = 0;
+#pragma omp parallel for schedule(static) reduction(max : m)
     for (int64_t i = 0; i < n; i++) {
         uint32_t a = f2u(x[i]) & 0x7fffffffu;
         if (a > 0x7f800000u) continue;
@@ -106,10 +112,12 @@ static inline uint8_t cast1(float x, float scale) {
 }
 
 void gpo_cast_bf16(const uint16_t *x, int64_t n, float scale, uint8_t *q) {
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; i++) q[i] = cast1(gpo_bf16_to_f32(x[i]), scale);
 }
 
 void gpo_cast_f32(const float *x, int64_t n, float scale, uint8_t *q) {
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; i++) q[i] = cast1(x[i], scale);
 }
 
@@ -167,6 +175,7 @@ uint16_t gpo_swiglu1(uint16_t z1h, uint16_t z2h) {
 void gpo_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, float *dequant,
                       uint32_t *amax_out) {
     uint32_t m = 0;
+#pragma omp parallel for schedule(static) reduction(max : m)
     for (int64_t r = 0; r < M; r++)
         for (int64_t k = 0; k < H; k++) {
             uint32_t a = ((uint32_t)(gpo_swiglu1(z[r * sz + k], z[r * sz + H + k]) & 0x7fffu)) << 16;
@@ -175,6 +184,7 @@ void gpo_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8
         }
     float scale;
     gpo_scales(m, &scale, dequant);
+#pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < M; r++)
         for (int64_t k = 0; k < H; k++)
             q[r * sq + k] = cast1(gpo_bf16_to_f32(gpo_swiglu1(z[r * sz + k], z[r * sz + H + k])), scale);
@@ -201,11 +211,13 @@ void gpo_swiglu_bwd1(uint16_t z1h, uint16_t z2h, uint16_t dah, uint16_t *d1, uin
 
 void gpo_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                     uint16_t *dz, int64_t sdz, uint8_t *dzq, float *dequant, uint32_t *amax_out) {
+#pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < M; r++)
         for (int64_t k = 0; k < H; k++)
             gpo_swiglu_bwd1(z[r * sz + k], z[r * sz + H + k], da[r * sda + k], &dz[r * sdz + k], &dz[r * sdz + H + k]);
     /* _cast_flat over the contiguous dz [M, 2H] */
     uint32_t m = 0;
+#pragma omp parallel for schedule(static) reduction(max : m)
     for (int64_t r = 0; r < M; r++)
         for (int64_t k = 0; k < 2 * H; k++) {
             uint32_t a = ((uint32_t)(dz[r * sdz + k] & 0x7fffu)) << 16;
@@ -214,6 +226,7 @@ void gpo_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H,
         }
     float scale;
     gpo_scales(m, &scale, dequant);
+#pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < M; r++)
         for (int64_t k = 0; k < 2 * H; k++)
             dzq[r * 2 * H + k] = cast1(gpo_bf16_to_f32(dz[r * sdz + k]), scale);

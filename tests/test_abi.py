@@ -73,6 +73,9 @@ def test_validation_codes():
     assert g(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 24, 4, 24, 32, 1, None, 0, None) == -3
     assert g(wsp, 16, wsp, wsp, 32, wsp, None, wsp, 16, 4, 16, 32, 1, None, 0, None) == -3
     assert g(wsp, 32, None, wsp, 32, wsp, None, wsp, 16, 4, 16, 32, 1, None, 0, None) == -1
+    # the epilogue's C offsets are 32-bit: ldc < 2^22 (a larger one would wrap them)
+    assert g(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 1 << 22, 4, 16, 32, 1, None, 0, None) == -3
+    assert g(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 1 << 30, 4, 16, 32, 1, None, 0, None) == -3
     # empty output: nothing to do
     assert g(None, 32, wsp, None, 32, wsp, None, None, 16, 0, 16, 32, 1, None, 0, None) == 0
     # MN-major GEMM: M % 16, N % 16, lda >= M, ldb >= N, K * ld < 2^31, null scales, misaligned operand
@@ -84,6 +87,7 @@ def test_validation_codes():
     assert mn(wsp, 32, None, wsp, 32, wsp, None, wsp, 32, 32, 32, 5, None, 0, None) == -1
     assert mn(wsp + 8, 32, wsp, wsp, 32, wsp, None, wsp, 32, 32, 32, 5, None, 0, None) == -4
     assert mn(None, 32, wsp, None, 32, wsp, None, None, 32, 0, 32, 5, None, 0, None) == 0
+    assert mn(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 1 << 22, 32, 32, 5, None, 0, None) == -3
 
 
 def test_single_pass_knob_is_host_only():

@@ -104,8 +104,14 @@ def test_convert_fp8_recipes(capsys):
         assert G.convert_fp8(Net(), recipe) == n
     out = capsys.readouterr().out
     assert "GEMMs of the image blocks converted" in out and "GEMMs of the image and text blocks converted" in out
-    with pytest.raises(ImportError):
-        G.convert_fp8(Net(), "tensorwise")
+    net = Net()
+    keys = {k: v.clone() for k, v in net.state_dict().items()}
+    for recipe in ("tensorwise", "rowwise", "native4"):
+        with pytest.raises(ValueError, match="native"):
+            G.convert_fp8(net, recipe)
+    # a refused recipe leaves the model untouched
+    assert all(type(m) is nn.Linear for m in net.modules() if isinstance(m, nn.Linear))
+    assert all(torch.equal(v, keys[k]) for k, v in net.state_dict().items())
 
 
 def test_fp8_filter():

@@ -131,16 +131,146 @@ def test_mlp_phase3_grads_match_quantized_formula(dev):
     assert torch.equal(w12.grad, G.fp8_gemm(G.swiglu_bwd_t(z, da)[2], sdz, G.tcast_t(x.detach())[1], sx))
 
 
-def test_swiglu_w3_phase1(dev):
-    M, C, H = 256, 128, 512
-    z = (torch.randn(M, 2 * H, device=dev) * 2).to(torch.bfloat16).requires_grad_()
-    w3 = (torch.randn(C, H, device=dev) / H ** 0.5).requires_grad_()
+def _np_bf16(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _np_q(t):
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def _bf16_matmul64(a, b):
+    """bf16(a @ b) with a, b float arrays, the product in float64: the reference's bf16 GEMMs (fp8_native.py:202,225,
+    264-265) up to their accumulation order."""
+    from oracle import oracle as O
+    return O.bf16_to_f32(O.f32_to_bf16((np.asarray(a, np.float64) @ np.asarray(b, np.float64)).astype(np.float32)))
+
+
+def _deq(q, s):
+    from oracle import oracle as O
+    return O.e4m3_to_f32(q).astype(np.float64) * np.float64(s)
+
+
+def _orel(x, ref):
+    from oracle import oracle as O
+    return O.rel_fro(x.detach().float().cpu().numpy(), ref)
+
+
+def test_swiglu_w3_phase1_against_oracle(dev):
+    """_SwiGLUw3 (fp8_native.py:207-232). Forward: the product cast and w3's cast are the oracle's bytes and scales
+    (the kernels reproduce them bit for bit) and y is within the elementwise bound of the oracle's float64 scaled
+    product of those bytes. Backward: exactly the reference's eager formulas (:221-232) on the saved tensors, and
+    within 1e-2 of the oracle's float64 restatement (dz within one bf16 ulp of the oracle's swiglu_bwd, whose
+    sigmoid is this build's)."""
+    from oracle import oracle as O
+    M, C, H = 512, 256, 1024
+    g = torch.Generator(device=dev).manual_seed(31)
+    z = (torch.randn(M, 2 * H, generator=g, device=dev) * 2).to(torch.bfloat16).requires_grad_()
+    w3 = (torch.randn(C, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16).requires_grad_()
+    dy = (torch.randn(M, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
     y = G.fp8_swiglu_w3(z, w3)
-    z1, z2 = z.detach().float().chunk(2, -1)
-    yref = (torch.nn.functional.silu(z1) * z2) @ w3.detach().t()
-    assert rel(y, yref) < 0.1
-    y.backward(torch.ones_like(y))
-    assert z.grad.shape == z.shape and w3.grad.dtype == torch.float32 and torch.isfinite(z.grad.float()).all()
+    zb, w3b = _np_bf16(z), _np_bf16(w3)
+    oaq, osa, _ = O.swiglu_tcast(zb)
+    o3q, os3, _ = O.tcast(w3b)
+    aq, sa = G.swiglu_tcast(z.detach())
+    w3q, s3 = G.tcast(w3.detach())
+    assert np.array_equal(_np_q(aq), oaq) and sa.item() == osa
+    assert np.array_equal(_np_q(w3q), o3q) and s3.item() == os3
+    ref = O.mm64(oaq, osa, o3q, os3)
+    assert _orel(y, ref) < 4e-3
+    from parity import assert_elementwise
+    assert_elementwise(y, aq, sa.item(), w3q, s3.item())
+    y.backward(dy)
+    # the reference's eager backward, written out (fp8_native.py:221-232)
+    zd, w3d = z.detach(), w3.detach()
+    da = dy @ w3d.to(torch.bfloat16)
+    dw3 = (dy.t() @ (aq.to(torch.float32) * sa).to(torch.bfloat16)).to(w3.dtype)
+    z1, z2 = zd.chunk(2, dim=-1)
+    z1f = z1.float()
+    sg = torch.sigmoid(z1f)
+    dz2 = da * (z1f * sg).to(torch.bfloat16)
+    dz1 = (da.float() * z2.float() * (sg * (1 + z1f * (1 - sg)))).to(torch.bfloat16)
+    assert torch.equal(z.grad, torch.cat([dz1, dz2], dim=-1))
+    assert torch.equal(w3.grad, dw3)
+    # against the oracle: da, dw3 in float64, dz from the oracle's swiglu_bwd of that da
+    dyf = O.bf16_to_f32(_np_bf16(dy))
+    oda = O.f32_to_bf16(_bf16_matmul64(dyf, O.bf16_to_f32(w3b)))
+    assert np.abs(O.bf16_to_f32(_np_bf16(da)) - O.bf16_to_f32(oda)).max() <= 2.0 ** -7 * np.abs(O.bf16_to_f32(oda)).max()
+    odz, _, _, _ = O.swiglu_bwd(zb, _np_bf16(da))
+    diff = np.abs(_np_bf16(z.grad).astype(np.int32) - odz.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.99
+    odw3 = _bf16_matmul64(dyf.T, _deq(oaq, osa))
+    assert _orel(w3.grad, odw3) < 1e-2
+
+
+@pytest.mark.parametrize("phase", [2, 3])
+def test_mlp_against_oracle_chain(dev, phase):
+    """_Fp8MLP (phase 2, fp8_native.py:235-266) and the all-FP8 _Fp8MLPF8 (phase 3): output and every gradient
+    within 1e-2 relative Frobenius of the oracle's chain on the same inputs -- tcast, mm, swiglu_tcast, mm forward;
+    tcast(dy), tcast(w3^T), mm (da), swiglu_bwd, tcast(w12^T), mm (dx) backward; the wgrads as the reference's bf16
+    products (phase 2) or as float64 scaled products of the e4m3 bytes (phase 3). Every intermediate is the
+    oracle's own."""
+    from oracle import oracle as O
+    M, C, H = 512, 256, 512
+    g = torch.Generator(device=dev).manual_seed(32 + phase)
+    x = torch.randn(M, C, generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    w12 = (torch.randn(2 * H, C, generator=g, device=dev) / C ** 0.5).to(torch.bfloat16).requires_grad_()
+    w3 = (torch.randn(C, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16).requires_grad_()
+    dy = (torch.randn(M, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    y = (G.fp8_mlp if phase == 2 else G.fp8_mlp_f8)(x, w12, w3)
+    y.backward(dy)
+    xb, w12b, w3b, dyb = _np_bf16(x), _np_bf16(w12), _np_bf16(w3), _np_bf16(dy)
+    # forward chain
+    oxq, osx, _ = O.tcast(xb)
+    o12q, os12, _ = O.tcast(w12b)
+    oz = O.mm(oxq, osx, o12q, os12)                                  # [M, 2H] bf16
+    oaq, osa, _ = O.swiglu_tcast(oz)
+    o3q, os3, _ = O.tcast(w3b)
+    assert _orel(y, O.mm64(oaq, osa, o3q, os3)) < 1e-2
+    # backward chain
+    odyq, osdy, _ = O.tcast(dyb)
+    o3tq, os3t, _ = O.tcast(np.ascontiguousarray(w3b.T))            # [H, C]
+    oda = O.mm(odyq, osdy, o3tq, os3t)                               # [M, H]
+    odz, odzq, osdz, _ = O.swiglu_bwd(oz, oda)
+    o12tq, os12t, _ = O.tcast(np.ascontiguousarray(w12b.T))         # [C, 2H]
+    assert _orel(x.grad, O.mm64(odzq, osdz, o12tq, os12t)) < 1e-2
+    if phase == 2:
+        odw12 = _bf16_matmul64(O.bf16_to_f32(odz).T, O.bf16_to_f32(xb))
+        odw3 = _bf16_matmul64(O.bf16_to_f32(dyb).T, _deq(oaq, osa))
+    else:
+        odw12 = _deq(odzq, osdz).T @ _deq(oxq, osx)
+        odw3 = _deq(odyq, osdy).T @ _deq(oaq, osa)
+    assert _orel(w12.grad, odw12) < 1e-2
+    assert _orel(w3.grad, odw3) < 1e-2
+
+
+def test_mlp_phase2_wiring_exact(dev):
+    """Phase 2's backward, operation by operation (fp8_native.py:255-266), recomputed from the same kernels on the
+    same tensors: dx is the FP8 dgrad of swiglu_bwd's dzq with w12's transposed bytes, dw12 the bf16 product dz^T x,
+    dw3 the bf16 product dy^T bf16(aq sa) -- all bit for bit."""
+    M, C, H = 512, 256, 512
+    g = torch.Generator(device=dev).manual_seed(35)
+    x = torch.randn(M, C, generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    w12 = (torch.randn(2 * H, C, generator=g, device=dev) / C ** 0.5).to(torch.bfloat16).requires_grad_()
+    w3 = (torch.randn(C, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16).requires_grad_()
+    dy = (torch.randn(M, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    G.fp8_mlp(x, w12, w3).backward(dy)
+    xd, w12d, w3d = x.detach(), w12.detach(), w3.detach()
+    xq, sx = G.tcast(xd)
+    w12q, s12 = G.tcast(w12d)
+    z = G.fp8_gemm(xq, sx, w12q, s12)
+    aq, sa = G.swiglu_tcast(z)
+    dyq, sdy = G.tcast(dy)
+    _, w3tq, s3t = G.tcast_t(w3d, False)
+    da = G.fp8_gemm(dyq, sdy, w3tq, s3t, None, False)
+    dz, dzq, sdz = G.swiglu_bwd(z, da)
+    _, w12tq, s12t = G.tcast_t(w12d, False)
+    assert torch.equal(x.grad, G.fp8_gemm(dzq, sdz, w12tq, s12t, None, False))
+    assert torch.equal(w12.grad, (dz.t() @ xd).to(w12.dtype))
+    assert torch.equal(w3.grad, (dy.t() @ (aq.to(torch.float32) * sa).to(torch.bfloat16)).to(w3.dtype))
+    # the transposed bytes are the reference's tcast(w.t().contiguous()) (fp8_native.py:259,262)
+    q3t, s3t2 = G.tcast(w3d.t().contiguous())
+    assert torch.equal(q3t.view(torch.uint8), w3tq.view(torch.uint8)) and s3t2.item() == s3t.item()
 
 
 class _Attn(nn.Module):

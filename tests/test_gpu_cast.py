@@ -172,15 +172,20 @@ def test_other_float_dtypes_widen(dev):
 
 
 # The single-pass casts write their tagged partial maxima from byte 28672 of the cast workspace (one 64-bit word per
-# workgroup, the call tag in the high half) and count partials a workgroup had to compute from x itself at byte 36864
-# (cast.hip: kOnceTagged, kOnceFallback).
-ONCE_WORD0, ONCE_FALLBACK = 28672 // 8, 36864 // 4
+# workgroup, the call tag in the high half), count partials a workgroup had to compute from x itself at byte 36864,
+# keep the last call's tag (the epoch) at byte 36868 and the workgroups of a call that are done folding at byte 36872
+# (cast.hip: kOnceTagged, kOnceFallback, kOnceEpoch, kOnceDone).
+ONCE_WORD0, ONCE_FALLBACK, ONCE_EPOCH, ONCE_DONE = 28672 // 8, 36864 // 4, 36868 // 4, 36872 // 4
 
 
 def once_state(dev):
     ws = L.cast_workspace(dev)
     torch.cuda.synchronize()
-    return int(ws.view(torch.int64)[ONCE_WORD0].item()), int(ws[ONCE_FALLBACK].item())
+    w0 = int(ws.view(torch.int64)[ONCE_WORD0].item())
+    # after a single-pass call the epoch holds its tag (the high half of workgroup 0's word) and the counter is back to 0
+    assert int(ws[ONCE_DONE].item()) == 0
+    assert int(ws[ONCE_EPOCH].item()) & 0xffffffff == (w0 >> 32) & 0xffffffff or w0 == 0
+    return w0, int(ws[ONCE_FALLBACK].item())
 
 
 @pytest.fixture
