@@ -71,6 +71,18 @@ void gpic_fp8_set_single_pass(int enabled, int wait_us);
 int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *ws, void *stream);
 
 /*
+ * gpic_fp8_tcast without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). No counterpart in the reference. It allocates
+ * nothing: its workspace is a static 40 KiB device array of the library, one per GPU, held until the process ends,
+ * set up on the first call on each device (its address taken, and the array cleared by a kernel on `stream`). The
+ * array's size does not depend on n, so every n gpic_fp8_tcast takes is accepted; a build whose cast workspace
+ * outgrew the array would return GPIC_EWORKSPACE. The same bytes and scale as gpic_fp8_tcast. Every call on one GPU
+ * shares the array and keeps the state the last call left there: calls that overlap on one GPU (several streams, or
+ * a captured graph replayed beside other such calls) race; calls ordered on one stream do not.
+ */
+int gpic_fp8_tcast_noalloc(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *stream);
+
+/*
  * The same cast of x [rows, cols] (row-major, cols % 16 == 0), writing q [rows, cols] (skipped when q is NULL) and
  * the transposed bytes qt [cols, ldt] (ldt % 16 == 0, ldt >= rows; columns rows..ldt-1 are written as zero bytes).
  * Replaces the reference's tcast(w.t().contiguous()) (fp8_native.py:259,262), which has the same amax and therefore

@@ -16,6 +16,7 @@
 //    Workgroup 0 of pass 2 writes the dequantization scale. The partials are scratch of the call in the workspace.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "gpic_device.h"
 #include "gpic_launch.h"
@@ -1235,6 +1236,48 @@ static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, u
   return true;
 }
 
+// ------------------------------------------------------------------------------------------- allocation-free cast
+//
+// gpic_fp8_tcast_noalloc: gpic_fp8_tcast with its workspace in this file's static device array `scratch` (one copy per
+// GPU, held until the process ends) instead of a caller's buffer, for callers that cannot allocate. The host name
+// `scratch` is only a stand-in for the device array: its device address is taken once per device with
+// hipGetSymbolAddress (below) and only that address is ever passed to a kernel. The cast workspace has a fixed size
+// (kCastWorkspaceBytes, whatever n is), which the array holds. Every call on one GPU shares the array and keeps what
+// the last call left in it (the single-pass casts' epoch and tagged partials: state they expect to persist); calls
+// that overlap on one GPU (several streams, or a graph replayed beside other casts on that GPU) race.
+constexpr size_t kScratchBytes = kCastWorkspaceBytes;   // 40 KiB per GPU
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static_assert(kCastWorkspaceBytes <= kScratchBytes, "the cast workspace must fit the static scratch array");
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];   // the array's device address per device (guarded by g_scratch_mu)
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *__restrict__ p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+// The current device's scratch address, set up on the first call on that device: the symbol's address, then a
+// clearing of the array on `st` (a fill kernel, not a memset: a caller may be capturing a graph) so that the
+// single-pass state starts at zero, stream-ordered before the cast that follows on `st`.
+static int scratch_address(hipStream_t st, void **out) {
+  const int dev = current_device();
+  if (dev < 0 || dev >= kMaxDevices) return GPIC_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr || !aligned16(ptr)) return GPIC_EALIGN;
+    zero_words_kernel<<<(int)(kScratchBytes / 4 + 255) / 256, 256, 0, st>>>(static_cast<uint32_t *>(ptr),
+                                                                          (int)(kScratchBytes / 4));
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GPIC_OK;
+}
+
 // SwiGLU kernels: rows strided over at most kSwigluBlocks workgroups (each builds its 24 KiB sigmoid table once).
 static inline int swiglu_grid(int64_t M) { return (int)(M < 1 ? 1 : (M > kSwigluBlocks ? kSwigluBlocks : M)); }
 
@@ -1265,6 +1308,18 @@ int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequa
   const float *xf = static_cast<const float *>(x);
   if (launch_tcast_once(xf, n, q, dequant, ws, st)) return (int)hipGetLastError();
   return launch_tcast(xf, n, q, dequant, partial, st);
+}
+
+int gpic_fp8_tcast_noalloc(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *stream) {
+  // the arguments gpic_fp8_tcast checks, before the first call on a device sets its scratch up
+  if (n < 0 || !dequant || (n > 0 && (!x || !q))) return GPIC_EINVAL;
+  if (dtype != GPIC_DTYPE_BF16 && dtype != GPIC_DTYPE_F32) return GPIC_EDTYPE;
+  if (!aligned16(x) || !aligned16(q)) return GPIC_EALIGN;
+  if (gpic_fp8_cast_workspace_bytes() > kScratchBytes) return GPIC_EWORKSPACE;
+  void *ws = nullptr;
+  const int rc = scratch_address((hipStream_t)stream, &ws);
+  if (rc != GPIC_OK) return rc;
+  return gpic_fp8_tcast(x, dtype, n, q, dequant, ws, stream);
 }
 
 int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,

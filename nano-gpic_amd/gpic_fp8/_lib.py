@@ -25,6 +25,7 @@ SIGNATURES = {
     "gpic_fp8_cast_workspace_bytes": (_sz, []),
     "gpic_fp8_set_single_pass": (None, [_int, _int]),
     "gpic_fp8_tcast": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _vp]),
+    "gpic_fp8_tcast_noalloc": (_int, [_vp, _int, _i64, _vp, _vp, _vp]),
     "gpic_fp8_tcast_t": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_swiglu_tcast": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_swiglu_tcast_t": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),

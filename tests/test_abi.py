@@ -50,6 +50,12 @@ def test_validation_codes():
     assert lib.gpic_fp8_tcast(wsp, 7, 16, wsp, wsp, wsp, None) == -2
     # misaligned input
     assert lib.gpic_fp8_tcast(wsp + 2, 0, 16, wsp, wsp, wsp, None) == -4
+    # the allocation-free cast checks the same arguments before it sets anything up
+    na = lib.gpic_fp8_tcast_noalloc
+    assert na(None, 0, -1, None, wsp, None) == -1
+    assert na(wsp, 0, 16, wsp, None, None) == -1
+    assert na(wsp, 7, 16, wsp, wsp, None) == -2
+    assert na(wsp + 2, 0, 16, wsp, wsp, None) == -4
     # transposing cast: columns must be a multiple of 16, ldt >= rows
     assert lib.gpic_fp8_tcast_t(wsp, 0, 4, 24, wsp, wsp, 16, wsp, wsp, None) == -3
     assert lib.gpic_fp8_tcast_t(wsp, 0, 40, 32, wsp, wsp, 32, wsp, wsp, None) == -3
