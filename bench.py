@@ -207,69 +207,122 @@ def run_gemm(G, op):
     return G.fp8_gemm(aq, sa, bq, sb, None, False)
 
 
-def cpu_baseline():
-    """The oracle on the host: the d12 block's casts (C restatement, one thread) and its 12 GEMMs as float32 numpy
-    matmuls of the dequantized operands (BLAS threads), on a bounded sample of 2048 of the 32768 tokens."""
-    import numpy as np
-    from oracle import oracle as O
+def gemm_source_sha():
+    import hashlib
+    with open(os.path.join(ROOT, "nano-gpic_amd", "csrc", "gemm.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def gemm_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/gemm_d12_traffic.json), or None when that summary was measured on another version of the GEMM source
+    than the one built here (its recorded hash differs): a stale figure is not reported."""
+    tpath = os.path.join(ROOT, "profiles", "gemm_d12_traffic.json")
+    if not os.path.exists(tpath):
+        return None
+    with open(tpath) as f:
+        t = json.load(f)
+    if t.get("gemm_source_sha") != gemm_source_sha():
+        return None
+    return t.get("traffic_bytes_per_launch")
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on, capped by OMP_NUM_THREADS where the host sets
+    it (the GPU boxes grant each job a share of their cores and set it to that share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model():
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    Ms = 2048
-    rng = np.random.default_rng(0)
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
-    def bf(shape, std=1.0):
-        return O.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
 
-    def dq(q, s):
-        return O.e4m3_to_f32(q) * np.float32(s)
+def median_s(fn, runs):
+    """Median wall time in seconds of `runs` calls of fn after one warm-up call."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
 
-    x = {k: bf((Ms, C)) for k in ("qkv", "proj", "mlp")}
-    w = {"qkv": bf((3 * C, C), C ** -0.5), "proj": bf((C, C), C ** -0.5)}
-    w12, w3 = bf((2 * H, C), C ** -0.5), bf((C, H), H ** -0.5)
-    dy = {"qkv": bf((Ms, 3 * C), 0.1), "proj": bf((Ms, C), 0.1), "mlp": bf((Ms, C), 0.1)}
 
-    def one():
+def cpu_baseline(runs=5, sample_tokens=8192):
+    """The reference path on the host's cores in torch CPU ops (the oracle's torch restatement: reference()'s fp32
+    product of dequantized e4m3 operands, the casts with IEEE scales, the eager SwiGLU expressions): config 1 at full
+    size, and the d12 block step of this benchmark (every GEMM in FP8, as on the GPU) on `sample_tokens` of the 32768
+    tokens; median of `runs` timed runs after a warm-up, with all the threads this process is granted."""
+    import torch
+    from oracle import oracle as O
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+
+    g = torch.Generator().manual_seed(0)                    # config 1 (SURVEY 8d): X [4096 x 768], W [768 x 768]
+    X = torch.randn(4096, 768, generator=g).to(torch.bfloat16)
+    W = (torch.randn(768, 768, generator=g) / 768 ** 0.5).to(torch.bfloat16)
+
+    def config1():
+        xq, sx = O.torch_tcast(X)
+        wq, sw = O.torch_tcast(W)
+        return O.torch_mm(xq, sx, wq, sw)
+    c1 = median_s(config1, max(runs, 7))
+
+    Ms = sample_tokens
+    g = torch.Generator().manual_seed(0)
+
+    def bf(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16)
+
+    x = {k: bf(Ms, C) for k in ("qkv", "proj", "mlp")}
+    w = {"qkv": bf(3 * C, C, std=C ** -0.5), "proj": bf(C, C, std=C ** -0.5)}
+    w12, w3 = bf(2 * H, C, std=C ** -0.5), bf(C, H, std=H ** -0.5)
+    dy = {"qkv": bf(Ms, 3 * C, std=0.1), "proj": bf(Ms, C, std=0.1), "mlp": bf(Ms, C, std=0.1)}
+    mm, tc = O.torch_mm, O.torch_tcast
+
+    def step():
         for k in ("qkv", "proj"):
-            xq, sx, _ = O.tcast(x[k])
-            wq, sw, _ = O.tcast(w[k])
-            dxq = dq(xq, sx)
-            dwq = dq(wq, sw)
-            _ = dxq @ dwq.T                                   # forward
-            dyq, sdy, _ = O.tcast(dy[k])
-            ddy = dq(dyq, sdy)
-            _ = ddy @ dwq                                     # dgrad
-            _ = ddy.T @ dxq                                   # wgrad
-        xq, sx, _ = O.tcast(x["mlp"])
-        w12q, s12, _ = O.tcast(w12)
-        w3q, s3, _ = O.tcast(w3)
-        dxq, dw12, dw3 = dq(xq, sx), dq(w12q, s12), dq(w3q, s3)
-        z = O.f32_to_bf16(dxq @ dw12.T)
-        aq, sa, _ = O.swiglu_tcast(z)
-        da_ = dq(aq, sa)
-        _ = da_ @ dw3.T
-        dyq, sdy, _ = O.tcast(dy["mlp"])
-        ddy = dq(dyq, sdy)
-        da = O.f32_to_bf16(ddy @ dw3)
-        _ = ddy.T @ da_
-        dz, dzq, sdz, _ = O.swiglu_bwd(z, da)
-        ddz = dq(dzq, sdz)
-        _ = ddz @ dw12
-        _ = ddz.T @ dxq
+            xq, sx = tc(x[k])
+            wq, sw = tc(w[k])
+            mm(xq, sx, wq, sw)                                   # forward
+            dyq, sdy = tc(dy[k])
+            mm(dyq, sdy, wq.t(), sw)                             # dgrad (w's bytes transposed)
+            mm(dyq.t(), sdy, xq.t(), sx)                         # wgrad
+        xq, sx = tc(x["mlp"])
+        w12q, s12 = tc(w12)
+        w3q, s3 = tc(w3)
+        z = mm(xq, sx, w12q, s12)
+        aq, sa = O.torch_swiglu_tcast(z)
+        mm(aq, sa, w3q, s3)
+        dyq, sdy = tc(dy["mlp"])
+        da = mm(dyq, sdy, w3q.t(), s3)
+        mm(dyq.t(), sdy, aq.t(), sa)                             # dw3
+        _, dzq, sdz = O.torch_swiglu_bwd(z, da)
+        mm(dzq, sdz, w12q.t(), s12)                              # dx
+        mm(dzq.t(), sdz, xq.t(), sx)                             # dw12
 
-    one()                                                     # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while reps < 2 or time.perf_counter() - t0 < 10.0:
-        one()
-        reps += 1
-    sec = (time.perf_counter() - t0) / reps
+    sec = median_s(step, runs)
     fl = flops(gemm_shapes(M=Ms))
-    return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": f"d12 block fwd+bwd FP8 linear path on {Ms} of the {M_TOK} tokens (oracle casts in C, 1 thread; "
-                      f"GEMMs as float32 numpy matmuls of dequantized e4m3 operands); {reps} reps, "
-                      f"{sec * 1e3:.0f} ms per sample step", "ms_per_sample_step": round(sec * 1e3, 1)}
+    return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"d12 block fwd+bwd FP8 linear path (the step of this benchmark, every GEMM FP8) on {Ms} of the "
+                      f"{M_TOK} tokens in torch CPU ops (reference()'s fp32 product of dequantized e4m3 operands, "
+                      f"IEEE-scaled casts, eager SwiGLU); median of {runs} runs after a warm-up",
+            "ms_per_sample_step": round(sec * 1e3, 1), "gemm_tflop_per_sample_step": round(fl / 1e12, 4),
+            "config1_ms": round(c1 * 1e3, 2),
+            "config1_workload": "X [4096 x 768] . W [768 x 768] seed 0: two casts + fp32 product -> bf16 (4.83 GFLOP)",
+            "config1_gflops": round(2.0 * 4096 * 768 * 768 / c1 / 1e9, 1),
+            "threads": threads, "os_cpu_count": os.cpu_count(), "cpu_model": cpu_model()}
 
 
 def main():
@@ -417,11 +470,7 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline()
     gemm_tflops = fl / gemm_ms / 1e9
-    traffic = None          # HBM bytes per GEMM launch, from the committed FETCH_SIZE / WRITE_SIZE summary
-    tpath = os.path.join(ROOT, "profiles", "gemm_d12_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
+    traffic = gemm_traffic()
     out = {
         "metric": METRIC,
         "value": round(fl / ms / 1e9, 2),
@@ -445,11 +494,12 @@ def main():
                      "launches_per_step": len(shapes),
                      "avg_launch_us": round(gemm_ms * 1e3 / len(shapes), 1), "gemm_ms_per_step": round(gemm_ms, 4),
                      "per_shape": per_shape},
-        "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale", "us": round(cast_ms * 1e3, 2),
-                 "achieved_GBs": round(cast_bytes / cast_ms / 1e6, 1), "peak_GBs": PEAK_HBM_GBS,
-                 "frac": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4),
-                 "algorithmic_bytes": cast_bytes, "us_l2_flushed": round(cast_cold_ms * 1e3, 2),
-                 "frac_l2_flushed": round(cast_bytes / cast_cold_ms / 1e6 / PEAK_HBM_GBS, 4)},
+        "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale, L2 / MALL flushed before each "
+                             "call (a 512 MB write; median of 20); the warm figures are back-to-back calls",
+                 "us": round(cast_cold_ms * 1e3, 2), "achieved_GBs": round(cast_bytes / cast_cold_ms / 1e6, 1),
+                 "peak_GBs": PEAK_HBM_GBS, "frac": round(cast_bytes / cast_cold_ms / 1e6 / PEAK_HBM_GBS, 4),
+                 "algorithmic_bytes": cast_bytes, "us_warm": round(cast_ms * 1e3, 2),
+                 "frac_warm": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4)},
         "cast_fp32_weight": {"workload": "fp32 [3072 x 1024] -> e4m3 + amax + scale (a DDP weight)",
                              "us": round(w32_ms * 1e3, 2) if w32_ms else None, "algorithmic_bytes": w32_bytes,
                              "achieved_GBs": round(w32_bytes / w32_ms / 1e6, 1) if w32_ms else None},

@@ -73,7 +73,7 @@ int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequa
 /*
  * gpic_fp8_tcast without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation). No counterpart in the reference. It allocates
- * nothing: its workspace is a static 40 KiB device array of the library, one per GPU, held until the process ends,
+ * nothing: its workspace is a static 44 KiB device array of the library, one per GPU, held until the process ends,
  * set up on the first call on each device (its address taken, and the array cleared by a kernel on `stream`). The
  * array's size does not depend on n, so every n gpic_fp8_tcast takes is accepted; a build whose cast workspace
  * outgrew the array would return GPIC_EWORKSPACE. The same bytes and scale as gpic_fp8_tcast. Every call on one GPU

@@ -863,9 +863,15 @@ constexpr int kMaxOnceBlocks = 1024;
 constexpr size_t kOnceTagged = 28 * 1024;                         // uint64_t[kMaxOnceBlocks] tagged partials
 constexpr size_t kOnceFallback = kOnceTagged + 8 * kMaxOnceBlocks;  // uint32_t: partials computed by a waiter
 constexpr size_t kOnceEpoch = kOnceFallback + 4;                    // uint32_t: the tag of the last call
-constexpr size_t kOnceDone = kOnceFallback + 8;                     // uint32_t: workgroups of this call done folding
+constexpr size_t kOnceDone = kOnceFallback + 8;                     // uint32_t: groups of this call done folding
+// Per group of kDoneGroup workgroups, the count of its workgroups done folding, each on its own 128-byte line: a single
+// counter taking one atomic from each of 1024 workgroups measured ~10 us per call (they serialise on one address).
+constexpr int kDoneGroup = 32;
+constexpr size_t kOnceGroupDone = 40 * 1024;                        // uint32_t at kOnceGroupDone + 128 g
 static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kOnceTagged, "two-pass scratch overlaps the single-pass words");
-static_assert(kOnceDone + 4 <= kCastWorkspaceBytes, "cast workspace too small");
+static_assert(kOnceDone + 4 <= kOnceGroupDone, "single-pass words overlap");
+static_assert(kOnceGroupDone + 128 * ((kMaxOnceBlocks + kDoneGroup - 1) / kDoneGroup) <= kCastWorkspaceBytes,
+              "cast workspace too small");
 template <typename T>
 constexpr int kOnceWords = sizeof(T) == 2 ? 16 : 12;   // 16-byte words a thread of the flat kernel holds (fp32: 12,
                                                         // which its wider narrowing code needs to fit 128 VGPRs)
@@ -946,8 +952,10 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wai
   uint32_t *done = reinterpret_cast<uint32_t *>((char *)ws + kOnceDone);
   const int G = gridDim.x;
   if (threadIdx.x == 0) {
-    // the epoch cannot change before this workgroup has counted itself done (below)
-    uint32_t t = __hip_atomic_load(epoch, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    // The epoch cannot change before this workgroup has counted itself done (below). Relaxed atomics throughout: the
+    // epoch is read by the next call, which starts after this kernel has completed, and an acquire / release at
+    // agent scope would write back or invalidate whole caches on this multi-XCD part in each of the 1024 workgroups.
+    uint32_t t = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     t = t ? t : 1u;
     stag = t;
     __hip_atomic_store(tagged + blockIdx.x, ((uint64_t)t << 32) | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -995,12 +1003,23 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wai
       __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)computed,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // Done with the partials (every thread has passed the barriers above after its last read of them). The last of the
-  // G workgroups to get here ends the call's use of the words: the next call takes the next tag.
-  if (threadIdx.x == 0 &&
-      __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)G - 1u) {
-    __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(epoch, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  // Done with the partials: every value this workgroup read from them has been consumed before the barriers above,
+  // so no read of them is outstanding. The last of the G workgroups to get here ends the call's use of the words: the
+  // next call takes the next tag. Counted in two levels: the last workgroup of each group of kDoneGroup counts its
+  // group done (atomic read-modify-writes of one address are totally ordered, so exactly one workgroup sees each
+  // count complete); every counter is back at zero when the call ends.
+  if (threadIdx.x == 0) {
+    const int grp = blockIdx.x / kDoneGroup;
+    const uint32_t gsize = (uint32_t)min(kDoneGroup, G - grp * kDoneGroup);
+    uint32_t *gdone = reinterpret_cast<uint32_t *>((char *)ws + kOnceGroupDone + 128 * grp);
+    if (__hip_atomic_fetch_add(gdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1u) {
+      __hip_atomic_store(gdone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t groups = (uint32_t)((G + kDoneGroup - 1) / kDoneGroup);
+      if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1u) {
+        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
   return g;
 }
@@ -1245,7 +1264,7 @@ static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, u
 // (kCastWorkspaceBytes, whatever n is), which the array holds. Every call on one GPU shares the array and keeps what
 // the last call left in it (the single-pass casts' epoch and tagged partials: state they expect to persist); calls
 // that overlap on one GPU (several streams, or a graph replayed beside other casts on that GPU) race.
-constexpr size_t kScratchBytes = kCastWorkspaceBytes;   // 40 KiB per GPU
+constexpr size_t kScratchBytes = kCastWorkspaceBytes;   // 44 KiB per GPU
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 static_assert(kCastWorkspaceBytes <= kScratchBytes, "the cast workspace must fit the static scratch array");
 

@@ -16,8 +16,9 @@ constexpr int kSwigluBlocks = 512;                    // workgroups of a SwiGLU 
 constexpr int kMaxCastBlocks = 8192;                  // workgroups of a streaming cast pass
 constexpr int kCastTBlocks = 1024;                    // workgroups of a (persistent) transposing cast pass
 constexpr int kSwigluCastTBlocks = 768;               // workgroups of the SwiGLU backward's recomputing cast (3 per CU)
-constexpr size_t kCastWorkspaceBytes = 40 * 1024;     // partial maxima (4 KiB), the SwiGLU sigmoid table (24 KiB),
-                                                      // the single-pass tagged partials (8 KiB) and call counter
+constexpr size_t kCastWorkspaceBytes = 44 * 1024;     // partial maxima (4 KiB), the SwiGLU sigmoid table (24 KiB),
+                                                      // the single-pass tagged partials (8 KiB), their epoch and
+                                                      // counters (4 KiB + 4 KiB)
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 

@@ -250,3 +250,47 @@ def linear_forward(x, w, bias=None):
     xq, sx, _ = tcast(x)
     wq, sw, _ = tcast(w)
     return mm(xq, sx, wq, sw, bias)
+
+
+# ---------------------------------------------------------------- the same path in torch CPU ops (the CPU baseline)
+#
+# A restatement of the reference's plain-torch path (fp8_native.py:320-331, reference()) with the production cast's
+# division rule (fp8_native.py:40-49: IEEE 448 / amax via torch.div, never the eager 448.0 / a), the SwiGLU product
+# and backward as the reference's eager expressions (fp8_native.py:55-58, 226-231, torch.sigmoid), on torch CPU
+# tensors: what bench.py times on the host's cores as the CPU baseline. Inputs are NaN-free (torch's amax propagates
+# NaN, the kernels' ignores it). Pinned against the C restatement above (tests/test_oracle.py): the same bytes and
+# scales for the casts and the product cast, dz within one bf16 ulp.
+
+def torch_tcast(x):
+    """tcast on a CPU tensor: (e4m3 tensor, dequant [1] fp32)."""
+    import torch
+    a = x.float().abs().amax().clamp_min(TINY).reshape(1)
+    fmax = torch.tensor([FMAX], dtype=torch.float32)
+    q = (x.float() * torch.div(fmax, a)).clamp(-FMAX, FMAX).to(torch.float8_e4m3fn)
+    return q, torch.div(a, fmax)
+
+
+def torch_mm(aq, sa, bq, sb):
+    """_mm on CPU tensors as reference() computes it: the fp32 product of the dequantized operands, rounded to bf16."""
+    import torch
+    return ((aq.float() * sa) @ (bq.float() * sb).t()).to(torch.bfloat16)
+
+
+def torch_swiglu_tcast(z):
+    """swiglu_tcast on a CPU bf16 tensor z [M, 2H]: a = bf16(bf16(z1 sigmoid(z1)) z2), then its tcast."""
+    import torch
+    z1, z2 = z.float().chunk(2, dim=-1)
+    sl = (z1 * torch.sigmoid(z1)).to(torch.bfloat16)
+    return torch_tcast((sl.float() * z2).to(torch.bfloat16))
+
+
+def torch_swiglu_bwd(z, da):
+    """swiglu_bwd on CPU bf16 tensors (the eager backward of fp8_native.py:226-231): (dz, dzq, dequant)."""
+    import torch
+    z1, z2 = z.float().chunk(2, dim=-1)
+    sg = torch.sigmoid(z1)
+    dz2 = da * (z1 * sg).to(torch.bfloat16)
+    dz1 = (da.float() * z2 * (sg * (1 + z1 * (1 - sg)))).to(torch.bfloat16)
+    dz = torch.cat([dz1, dz2], dim=-1)
+    dzq, s = torch_tcast(dz)
+    return dz, dzq, s

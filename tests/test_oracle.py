@@ -257,3 +257,53 @@ def test_linear_forward_golden(gold):
     y = O.linear_forward(gold["lin_x"], gold["lin_w"], gold["lin_b"])
     ref = O.bf16_to_f32(gold["lin_y"])
     assert O.rel_fro(O.bf16_to_f32(y), ref) < 5e-3
+
+
+# ---------------------------------------------------------------- the torch-CPU restatement (the CPU baseline)
+
+def _u16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_torch_tcast_equals_c_oracle(dtype):
+    """The CPU baseline's cast (torch ops, torch.div scales) gives the C oracle's bytes and scale, outliers included."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3000, 1024, generator=g)
+    x[:, :10] *= 50.0
+    x = x.to(dtype)
+    q, s = O.torch_tcast(x)
+    oq, od, _ = O.tcast(_u16(x) if dtype == torch.bfloat16 else x.numpy())
+    assert s.item() == od and np.array_equal(q.view(torch.uint8).numpy(), oq)
+
+
+def test_torch_mm_equals_reference_formula_and_c_oracle(gold):
+    """The baseline's GEMM is reference()'s fp32 product of the dequantized bytes: on the exact integer golden GEMM it
+    gives the golden bf16 bits, and on random bytes it is within 1e-2 of the oracle's float64 product."""
+    a = torch.from_numpy(gold["gemm_a"]).view(E4)
+    b = torch.from_numpy(gold["gemm_b"]).view(E4)
+    c = O.torch_mm(a, torch.tensor(gold["gemm_sa"]), b, torch.tensor(gold["gemm_sb"]))
+    assert np.array_equal(_u16(c), gold["gemm_c"])
+    g = torch.Generator().manual_seed(8)
+    a = (torch.randn(300, 512, generator=g) * 30).clamp(-448, 448).to(E4)
+    b = (torch.randn(200, 512, generator=g) * 30).clamp(-448, 448).to(E4)
+    c = O.torch_mm(a, torch.tensor(0.01), b, torch.tensor(0.02))
+    ref = O.mm64(a.view(torch.uint8).numpy(), np.float32(0.01), b.view(torch.uint8).numpy(), np.float32(0.02))
+    assert O.rel_fro(c.float().numpy(), ref) < 4e-3
+
+
+def test_torch_swiglu_equals_c_oracle():
+    """The baseline's SwiGLU product cast equals the C oracle's bytes (sl = bf16(z1 sigmoid(z1)) agrees with torch's
+    for every finite bf16 input); its backward's dz is within one bf16 ulp of the oracle's (sigmoid definitions)."""
+    g = torch.Generator().manual_seed(9)
+    z = (torch.randn(256, 2048, generator=g) * 3).to(torch.bfloat16)
+    da = (torch.randn(256, 1024, generator=g) * 0.1).to(torch.bfloat16)
+    q, s = O.torch_swiglu_tcast(z)
+    oq, od, _ = O.swiglu_tcast(_u16(z))
+    assert s.item() == od and np.array_equal(q.view(torch.uint8).numpy(), oq)
+    dz, dzq, sdz = O.torch_swiglu_bwd(z, da)
+    odz, _, _, _ = O.swiglu_bwd(_u16(z), _u16(da))
+    diff = np.abs(_u16(dz).astype(np.int32) - odz.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.99
+    q2, s2 = O.torch_tcast(dz)
+    assert s2.item() == sdz.item() and torch.equal(q2.view(torch.uint8), dzq.view(torch.uint8))
