@@ -207,6 +207,41 @@ def run_gemm(G, op):
     return G.fp8_gemm(aq, sa, bq, sb, None, False)
 
 
+def norm_sites(G, dev, B=128, N=256, eps=1e-6):
+    """The two norm sites of a d12 block over one GPU's 32768 tokens: fused (the norm kernel writes h's e4m3 bytes
+    and scale; h never exists in bf16) against unfused (the norm writes bf16 h, then tcast reads it), device time, with
+    the bytes each design moves (HBM minimum: x, a read, x_new, h / hq written; 4 bytes of rstd per row)."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(B, N, C, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(B, N, C, generator=g, device=dev).to(torch.bfloat16)
+    mod = (torch.randn(B, 1, 6 * C, generator=g, device=dev) * 0.2).to(torch.bfloat16)
+    sh, sc, gate = mod[..., :C], mod[..., C:2 * C], mod[..., 2 * C:3 * C]
+    w = 1 + 0.1 * torch.randn(C, generator=g, device=dev)
+    q = G.res_mod_rmsnorm_q
+    t = {
+        "site1_fused": time_device(lambda: q(x, x, x, w, sh, sc, eps, False, False), 20, 3),
+        "site1_unfused": time_device(lambda: G.tcast(q(x, x, x, w, sh, sc, eps, False, True, False)[1]), 20, 3),
+        "site2_fused": time_device(lambda: q(x, a, gate, w, sh, sc, eps, True, False), 20, 3),
+        "site2_unfused": time_device(lambda: G.tcast(q(x, a, gate, w, sh, sc, eps, True, True, False)[1]), 20, 3),
+    }
+    n, rows = B * N * C, B * N
+    by = {"site1_fused": n * 3 + rows * 4, "site1_unfused": n * 7 + rows * 4,
+          "site2_fused": n * 7 + rows * 4, "site2_unfused": n * 11 + rows * 4}
+    out = {"workload": f"d12 norm sites over {rows} tokens (C {C}): site 1 RMSNorm + modulation, site 2 residual add + "
+                       "RMSNorm + modulation; fused: h's e4m3 + scale from the norm kernel, unfused: the norm writes bf16 "
+                       "h, tcast reads it (device time)"}
+    for k, ms in t.items():
+        out[k + "_us"] = round(ms * 1e3, 2) if ms else None
+        out[k + "_bytes"] = by[k]
+        out[k + "_GBs"] = round(by[k] / ms / 1e6, 1) if ms else None
+    for site in ("site1", "site2"):
+        if t[site + "_fused"] and t[site + "_unfused"]:
+            out[site + "_speedup"] = round(t[site + "_unfused"] / t[site + "_fused"], 3)
+            out[site + "_fused_frac_hbm"] = round(by[site + "_fused"] / t[site + "_fused"] / 1e6 / PEAK_HBM_GBS, 4)
+    return out
+
+
 def gemm_source_sha():
     import hashlib
     with open(os.path.join(ROOT, "nano-gpic_amd", "csrc", "gemm.hip"), "rb") as f:
@@ -422,6 +457,11 @@ def main():
     sw_min, sw_moved = M_TOK * H * 5, M_TOK * H * 9               # min: read z, write q; as built: + write a, read a
     swb_min, swb_moved = M_TOK * H * 8, M_TOK * H * 14            # min: read z, da, write dzq; as built: z, da twice
 
+    # ---- the norm sites' producer with the cast folded in: site 1 (RMSNorm + modulation -> qkv_x) and site 2 (x + gate
+    # * a, RMSNorm + modulation -> the MLP) at d12, h's e4m3 bytes from the norm kernel (fused) against the norm
+    # writing bf16 h and tcast(h) reading it back (unfused), device time
+    norm = norm_sites(G, dev)
+
     # ---- config 5: the d18 block (C = 1792, H = 7168) with 1% outlier activation channels, fwd + bwd
     C18, H18 = 1792, 7168
     t18 = make_inputs(dev, seed=5, C=C18, H=H18, outliers=0.01)
@@ -513,6 +553,7 @@ def main():
                    "bwd_moved_bytes": swb_moved,
                    "bwd_GBs_moved": round(swb_moved / swb_ms / 1e6, 1) if swb_ms else None,
                    "bwd_frac_min": round(swb_min / swb_ms / 1e6 / PEAK_HBM_GBS, 4) if swb_ms else None},
+        "norm_sites": norm,
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
                       "tflops": round(fl18 / ms18 / 1e9, 1)},

@@ -20,6 +20,7 @@
 
 #include "gpic_device.h"
 #include "gpic_launch.h"
+#include "gpic_once.h"
 
 namespace gpic {
 
@@ -848,30 +849,8 @@ static void launch_cast_t(SrcBF16 src, int64_t rows, int64_t cols, int nparts, u
 // registers, reduces it to a partial maximum and publishes it, takes the maximum of all workgroups' partials, and
 // casts from its registers. x is read once: 3 B/elem moved for bf16 instead of 5.
 //
-// Partials: one 64-bit word per workgroup, (call tag << 32) | amax bits, in the workspace. The tag is the workspace's
-// epoch + 1 (0 skipped): every workgroup reads the epoch at its fold, and the last workgroup of the call to finish its
-// fold (a counter in the workspace reaches the grid size) stores the tag as the new epoch and clears the counter. So
-// the next call on the workspace -- stream-ordered after this one, or the next replay of a captured graph -- uses the
-// next tag, and a word left by an earlier call never matches. The workspace is zeroed once, when it is created, and
-// tag 0 is never used; the tag repeats after 2^32 calls on one workspace.
-// No workgroup waits on another without a bound: a partial that has not appeared within the wait bound (kOnceWaitUs by
-// default, about 8x a whole call) is computed by the waiting workgroup itself, from that workgroup's share of x, and
-// published for the other waiters. So the launch needs no co-residency guarantee (a plain launch; the cooperative one
-// costs ~17 us per call here), never deadlocks when other work holds CUs, and the amax is exact either way. The
-// workspace's fallback word counts such direct computations (0 in normal runs).
-constexpr int kMaxOnceBlocks = 1024;
-constexpr size_t kOnceTagged = 28 * 1024;                         // uint64_t[kMaxOnceBlocks] tagged partials
-constexpr size_t kOnceFallback = kOnceTagged + 8 * kMaxOnceBlocks;  // uint32_t: partials computed by a waiter
-constexpr size_t kOnceEpoch = kOnceFallback + 4;                    // uint32_t: the tag of the last call
-constexpr size_t kOnceDone = kOnceFallback + 8;                     // uint32_t: groups of this call done folding
-// Per group of kDoneGroup workgroups, the count of its workgroups done folding, each on its own 128-byte line: a single
-// counter taking one atomic from each of 1024 workgroups measured ~10 us per call (they serialise on one address).
-constexpr int kDoneGroup = 32;
-constexpr size_t kOnceGroupDone = 40 * 1024;                        // uint32_t at kOnceGroupDone + 128 g
+// The partials' layout and the fold: gpic_once.h.
 static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kOnceTagged, "two-pass scratch overlaps the single-pass words");
-static_assert(kOnceDone + 4 <= kOnceGroupDone, "single-pass words overlap");
-static_assert(kOnceGroupDone + 128 * ((kMaxOnceBlocks + kDoneGroup - 1) / kDoneGroup) <= kCastWorkspaceBytes,
-              "cast workspace too small");
 template <typename T>
 constexpr int kOnceWords = sizeof(T) == 2 ? 16 : 12;   // 16-byte words a thread of the flat kernel holds (fp32: 12,
                                                         // which its wider narrowing code needs to fit 128 VGPRs)
@@ -879,7 +858,6 @@ constexpr int kOnceTiles = 2;       // 128 x 128 bf16 tiles a workgroup of the t
 constexpr int kHybridTiles = 8;     // the transposing kernel takes up to this many tiles per workgroup (2 held)
 constexpr int kHybridFlat = 8;      // the flat kernel takes up to this many times the words it can hold
 constexpr int kStream = 8;          // streamed words in flight per thread (flat hybrid)
-constexpr int kOnceWaitUs = 200;
 
 // A uniform index the compiler must treat as new here, so it recomputes the addresses derived from it instead of
 // keeping (and spilling) them across the fold's wait.
@@ -936,92 +914,6 @@ __device__ __forceinline__ uint32_t words_amax(const u32x4 (&w)[W]) {
     for (int i = 0; i < W; i++) m = max(m, word_amax_exact<T>(w[i]));
   }
   return m;
-}
-
-// Publishes this workgroup's maximum m (held by every thread) as this call's partial, then returns the maximum over
-// all G partials to every thread. share_max(c) must return (to every thread of the workgroup) workgroup c's maximum
-// computed from x; it runs only for a partial that did not appear within wait_ticks. The call's tag comes from the
-// workspace's epoch; the last workgroup to finish its fold advances the epoch (see above).
-template <class ShareMax>
-__device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wait_ticks, ShareMax share_max) {
-  __shared__ int missing[kMaxOnceBlocks];
-  __shared__ int nmissing;
-  __shared__ uint32_t stag;
-  uint64_t *tagged = reinterpret_cast<uint64_t *>((char *)ws + kOnceTagged);
-  uint32_t *epoch = reinterpret_cast<uint32_t *>((char *)ws + kOnceEpoch);
-  uint32_t *done = reinterpret_cast<uint32_t *>((char *)ws + kOnceDone);
-  const int G = gridDim.x;
-  if (threadIdx.x == 0) {
-    // The epoch cannot change before this workgroup has counted itself done (below). Relaxed atomics throughout: the
-    // epoch is read by the next call, which starts after this kernel has completed, and an acquire / release at
-    // agent scope would write back or invalidate whole caches on this multi-XCD part in each of the 1024 workgroups.
-    uint32_t t = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    t = t ? t : 1u;
-    stag = t;
-    __hip_atomic_store(tagged + blockIdx.x, ((uint64_t)t << 32) | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    nmissing = 0;
-  }
-  __syncthreads();
-  const uint32_t tag = stag;
-  uint32_t g = m;
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  for (int i = threadIdx.x; i < G; i += blockDim.x) {
-    uint64_t w = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    while ((uint32_t)(w >> 32) != tag && __builtin_amdgcn_s_memrealtime() - t0 < wait_ticks) {
-      __builtin_amdgcn_s_sleep(2);
-      w = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if ((uint32_t)(w >> 32) == tag) g = max(g, (uint32_t)w);
-    else missing[atomicAdd(&nmissing, 1)] = i;
-  }
-  g = block_max_u32(g);   // its barriers also publish `missing`
-  const int nm = nmissing;
-  if (nm > 0) {
-    // Waiters help each other: each starts at a different missing partial, computes it from x and publishes it (the
-    // same word its owner writes), and checks every other one again before computing it, so the missing partials are
-    // computed about once between all waiters rather than once by each.
-    __shared__ uint64_t seen;
-    int computed = 0;
-    for (int k = 0; k < nm; k++) {
-      const int c = missing[(k + blockIdx.x) % nm];
-      if (threadIdx.x == 0)   // (a zero wait bound skips the check: every partial missing at the first poll is computed)
-        seen = wait_ticks ? __hip_atomic_load(tagged + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-      __syncthreads();
-      const uint64_t w = seen;
-      __syncthreads();   // `seen` is rewritten by the next iteration
-      if ((uint32_t)(w >> 32) == tag) {
-        g = max(g, (uint32_t)w);
-      } else {
-        const uint32_t v = share_max(c);
-        g = max(g, v);
-        computed++;
-        if (threadIdx.x == 0)
-          __hip_atomic_store(tagged + c, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    if (threadIdx.x == 0 && computed > 0)
-      __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)computed,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  // Done with the partials: every value this workgroup read from them has been consumed before the barriers above,
-  // so no read of them is outstanding. The last of the G workgroups to get here ends the call's use of the words: the
-  // next call takes the next tag. Counted in two levels: the last workgroup of each group of kDoneGroup counts its
-  // group done (atomic read-modify-writes of one address are totally ordered, so exactly one workgroup sees each
-  // count complete); every counter is back at zero when the call ends.
-  if (threadIdx.x == 0) {
-    const int grp = blockIdx.x / kDoneGroup;
-    const uint32_t gsize = (uint32_t)min(kDoneGroup, G - grp * kDoneGroup);
-    uint32_t *gdone = reinterpret_cast<uint32_t *>((char *)ws + kOnceGroupDone + 128 * grp);
-    if (__hip_atomic_fetch_add(gdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1u) {
-      __hip_atomic_store(gdone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t groups = (uint32_t)((G + kDoneGroup - 1) / kDoneGroup);
-      if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1u) {
-        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  return g;
 }
 
 // Flat single-pass cast. x as nw 16-byte words (8 bf16 or 4 fp32 elements) plus `tail` (< 8 or < 4) elements;
@@ -1202,7 +1094,7 @@ static std::atomic<int> g_once_wait_us{kOnceWaitUs};
 
 // Workgroups of `kernel` (256 threads) the current device holds at once, capped at kMaxOnceBlocks; cached per device
 // in `cache` (one per kernel, slots initialised to -1).
-static int once_capacity(const void *kernel, DeviceCache &cache) {
+int once_capacity(const void *kernel, DeviceCache &cache) {
   return per_device(cache, [kernel](int dev) {
     int per = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess) per = 0;
@@ -1212,7 +1104,9 @@ static int once_capacity(const void *kernel, DeviceCache &cache) {
 }
 
 // s_memrealtime counts at 100 MHz on this target
-static uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(std::memory_order_relaxed)) * 100u; }
+uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(std::memory_order_relaxed)) * 100u; }
+
+bool once_enabled() { return g_once_enabled.load(std::memory_order_relaxed) != 0; }
 
 static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t;
 struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
@@ -1230,7 +1124,7 @@ static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant,
   constexpr int kE = 16 / sizeof(T);
   const int64_t nw = n / kE;
   const int64_t held = (int64_t)kOnceWords<T> * 256 * cap;   // words the grid holds in registers
-  if (!g_once_enabled.load(std::memory_order_relaxed) || cap <= 0 || n <= 0 || nw > kHybridFlat * held) return false;
+  if (!once_enabled() || cap <= 0 || n <= 0 || nw > kHybridFlat * held) return false;
   if (nw > held) {   // hybrid: every workgroup holds its full share, the rest is streamed
     const int64_t sgroups = (nw - held + 255) / 256;
     cast_once_kernel<T><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_wait_ticks());
@@ -1248,7 +1142,7 @@ static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, u
                                 float *dequant, void *ws, hipStream_t st) {
   const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), g_cap_t);
   const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
-  if (!g_once_enabled.load(std::memory_order_relaxed) || cap <= 0 || tiles <= 0 || tiles > (int64_t)kHybridTiles * cap)
+  if (!once_enabled() || cap <= 0 || tiles <= 0 || tiles > (int64_t)kHybridTiles * cap)
     return false;
   const int grid = (int)std::min<int64_t>(tiles, cap);
   cast_t_once_kernel<<<grid, 256, 0, st>>>(x, cols, rows, cols, q, cols, qt, ldt, dequant, ws, once_wait_ticks());

@@ -1,0 +1,228 @@
+"""The image blocks' two norm sites with the FP8 cast of their output folded into the producer:
+baselines/PixelGen/src/models/layers/fused_norm.py (lever K) on the HIP kernel of nano-gpic_amd/csrc/norm.hip.
+
+    site 1 (norm1):  h = RMSNorm(x) * (1 + scale) + shift                                   mod_rmsnorm
+    site 2 (norm2):  x_new = x + gate * a;  h = RMSNorm(x_new) * (1 + scale) + shift        res_mod_rmsnorm
+
+The reference computes h in bf16 and its FP8 linear then reads h again for the amax and the cast
+(fp8_native.py:3-6 names these separate passes as why FP8 lost end to end). Here one kernel writes h's tensorwise
+e4m3 bytes and scale directly, and h itself only when asked. Functions:
+
+- mod_rmsnorm / res_mod_rmsnorm / reference: the reference's API (fused_norm.py:293-313) with bf16 h, on the kernel;
+- fp8_mod_rmsnorm_linear(x, w_norm, shift, scale, eps, weight, bias): site 1 feeding a phase-3 FP8 linear (qkv_x);
+- fp8_res_mod_rmsnorm_mlp(x, a, gate, w_norm, shift, scale, eps, w12, w3): site 2 feeding the phase-3 FP8 SwiGLU MLP,
+  returning (x_new, mlp output).
+
+The backward of the norm is the reference's analytic one (fused_norm.py:94-140) in torch fp32 ops; the linears'
+backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
+"""
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+from .fp8_native import E4, fp8_gemm, fp8_gemm_mn, swiglu_bwd_q, swiglu_tcast, tcast, tcast_t
+
+
+def _vec(t, B, C):
+    """A [B, 1, C] modulation chunk (a view of the adaLN output) as a [B, C] view with unit column stride, a row
+    stride that is a multiple of 4 and an 8-byte aligned start, without a copy where it already is one."""
+    t = t.reshape(B, C)
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    if t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 8:
+        t = L.aligned(t.contiguous())
+    return t
+
+
+@torch.library.custom_op("gpic::fp8_res_mod_rmsnorm", mutates_args=())
+def res_mod_rmsnorm_q(x: torch.Tensor, a: torch.Tensor, gate: torch.Tensor, w: torch.Tensor, shift: torch.Tensor,
+                      scale: torch.Tensor, eps: float, has_res: bool, want_h: bool, want_q: bool = True
+                      ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x [B, N, C] bf16 (C % 256 == 0), a [B, N, C] bf16 (has_res), gate / shift / scale [B, 1, C], w [C] ->
+    (x_new [B, N, C] bf16 or an empty tensor, h [B, N, C] bf16 or an empty tensor (want_h), h's e4m3 bytes [B, N, C]
+    and their dequantization scale [1] fp32 (empty tensors unless want_q), rstd [B * N] fp32). want_q=False is the
+    norm alone (the reference's op)."""
+    L.require_gpu(x, a, gate, w, shift, scale)
+    if not (want_h or want_q):
+        raise ValueError("res_mod_rmsnorm_q needs want_h or want_q")
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.shape[2] % 256:
+        raise ValueError(f"the norm kernel takes bf16 x [B, N, C] with C % 256 == 0, got {x.dtype} {tuple(x.shape)}")
+    B, N, C = x.shape
+    xc = L.aligned(x.contiguous())
+    ac = L.aligned(a.to(torch.bfloat16).contiguous()) if has_res else None
+    if has_res and ac.shape != x.shape:
+        raise ValueError(f"a must be [B, N, C] like x, got {tuple(a.shape)}")
+    g = _vec(gate, B, C) if has_res else None
+    sh, sc = _vec(shift, B, C), _vec(scale, B, C)
+    wf = L.aligned(w.to(torch.float32).contiguous())
+    dev = x.device
+    xn = torch.empty_like(xc) if has_res else x.new_empty(0)
+    h = torch.empty_like(xc) if want_h else x.new_empty(0)
+    hq = torch.empty((B, N, C) if want_q else (0,), dtype=E4, device=dev)
+    s = torch.empty(1 if want_q else 0, dtype=torch.float32, device=dev)
+    rstd = torch.empty(B * N, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws = L.cast_workspace(dev)
+        L.check(L.lib().gpic_fp8_res_mod_rmsnorm(
+            xc.data_ptr(), L.ptr(ac), L.ptr(g), g.stride(0) if has_res else 0, wf.data_ptr(), sh.data_ptr(),
+            sh.stride(0), sc.data_ptr(), sc.stride(0), B * N, max(N, 1), C, float(eps), xn.data_ptr() if has_res else None,
+            h.data_ptr() if want_h else None, rstd.data_ptr(), hq.data_ptr() if want_q else None,
+            s.data_ptr() if want_q else None, ws.data_ptr(),
+            L.stream_ptr(dev)), "gpic_fp8_res_mod_rmsnorm")
+    return xn, h, hq, s, rstd
+
+
+@res_mod_rmsnorm_q.register_fake
+def _(x, a, gate, w, shift, scale, eps, has_res, want_h, want_q=True):
+    B, N, C = x.shape
+    return (torch.empty_like(x) if has_res else x.new_empty(0), torch.empty_like(x) if want_h else x.new_empty(0),
+            x.new_empty((B, N, C) if want_q else (0,), dtype=E4), x.new_empty(1 if want_q else 0, dtype=torch.float32),
+            x.new_empty(B * N, dtype=torch.float32))
+
+
+def _norm_backward(dh, dxn, xs, a, gate, w, scale, rstd):
+    """The reference's backward of the norm site (fused_norm.py:94-140) in torch fp32 ops: dh [B, N, C] (the
+    gradient of h), dxn (that of x_new, site 2) or None, xs = x_new (site 2) or x, rstd [B * N]. Returns dx, da (or
+    None), d_gate [B, C] (or None), d_w [C], d_shift [B, C], d_scale [B, C] (fp32 column sums)."""
+    B, N, C = xs.shape
+    r = rstd.view(B, N, 1)
+    t = xs.float() * r
+    wf = w.float()
+    n = (wf * t).to(xs.dtype).float()
+    dhf = dh.float()
+    dsh = dhf.sum(1)
+    dsc = (dhf * n).sum(1)
+    dn = dhf * (1.0 + scale.reshape(B, 1, C).float())
+    dw = (dn * t).sum((0, 1))
+    dt = dn * wf
+    mean = (dt * t).sum(-1, keepdim=True) / C
+    dx = r * (dt - t * mean)
+    if dxn is not None:
+        dx = dx + dxn.float()
+    if a is None:
+        return dx.to(xs.dtype), None, None, dw, dsh, dsc
+    da = dx * gate.reshape(B, 1, C).float()
+    dg = (dx * a.float()).sum(1)
+    return dx.to(xs.dtype), da.to(a.dtype), dg, dw, dsh, dsc
+
+
+def _param_grads(B, C, dg, dw, dsh, dsc, gate, w, shift, scale):
+    vec = lambda v, like: None if v is None else v.to(like.dtype).view(B, 1, C).reshape(like.shape)
+    return vec(dg, gate) if gate is not None else None, dw.to(w.dtype), vec(dsh, shift), vec(dsc, scale)
+
+
+class _ResModRMSNorm(torch.autograd.Function):
+    """The reference's res_mod_rmsnorm_fwd with bf16 h (fused_norm.py:150-175, 245-287) on the HIP kernel."""
+    @staticmethod
+    def forward(ctx, x, a, gate, w, shift, scale, eps, has_res):
+        xn, h, _, _, rstd = res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, has_res, True, False)
+        ctx.has_res = has_res
+        ctx.save_for_backward(xn if has_res else x, a if has_res else None, gate if has_res else None, w, shift, scale,
+                              rstd)
+        return (xn if has_res else x.new_empty(0)), h
+
+    @staticmethod
+    def backward(ctx, dxn, dh):
+        xs, a, gate, w, shift, scale, rstd = ctx.saved_tensors
+        B, _, C = xs.shape
+        dx, da, dg, dw, dsh, dsc = _norm_backward(dh, dxn if ctx.has_res else None, xs, a, gate, w, scale, rstd)
+        dgate, dw, dshift, dscale = _param_grads(B, C, dg, dw, dsh, dsc, gate, w, shift, scale)
+        return dx, da, dgate, dw, dshift, dscale, None, None
+
+
+def mod_rmsnorm(x, w, shift, scale, eps):
+    """h = RMSNorm(x) * (1 + scale) + shift; x [B, N, C], w [C], shift and scale [B, 1, C] (fused_norm.py:293-295)."""
+    return _ResModRMSNorm.apply(x, x, x, w, shift, scale, eps, False)[1]
+
+
+def res_mod_rmsnorm(x, a, gate, w, shift, scale, eps):
+    """x_new = x + gate * a; h = RMSNorm(x_new) * (1 + scale) + shift. Returns (x_new, h) (fused_norm.py:298-302)."""
+    return _ResModRMSNorm.apply(x, a, gate, w, shift, scale, eps, True)
+
+
+def reference(x, a, gate, w, shift, scale, eps, has_res):
+    """The model's own ops in eager mode (fused_norm.py:305-313), for tests: returns (x_new or x, h)."""
+    if has_res:
+        x = x + gate * a
+    hs = x.to(torch.float32)
+    var = hs.pow(2).mean(-1, keepdim=True)
+    hs = hs * torch.rsqrt(var + eps)
+    n = (w * hs).to(x.dtype)
+    return x, n * (1 + scale) + shift
+
+
+class _Fp8ModRMSNormLinear(torch.autograd.Function):
+    """Site 1 feeding a phase-3 FP8 linear: the norm kernel casts h to e4m3 (h is never written in bf16), the GEMM
+    reads those bytes; backward: FP8 dgrad (dh) and wgrad (from h's bytes), then the norm's backward."""
+    @staticmethod
+    def forward(ctx, x, w_norm, shift, scale, eps, weight, bias):
+        B, N, C = x.shape
+        _, _, hq, sh, rstd = res_mod_rmsnorm_q(x, x, x, w_norm, shift, scale, eps, False, False)
+        hq2 = hq.view(B * N, C)
+        wq, wqt, sw = tcast_t(weight)
+        y = fp8_gemm(hq2, sh, wq, sw, None if bias is None else bias.to(torch.bfloat16))
+        ctx.save_for_backward(x, w_norm, shift, scale, rstd, hq2, sh, wqt, sw)
+        ctx.has_b, ctx.wdt = bias is not None, weight.dtype
+        return y.view(B, N, weight.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w_norm, shift, scale, rstd, hq2, sh, wqt, sw = ctx.saved_tensors
+        B, N, C = x.shape
+        dy2 = dy.reshape(B * N, -1).to(torch.bfloat16)
+        dyq, sdy = tcast(dy2)
+        dh = fp8_gemm(dyq, sdy, wqt, sw, None, False).view(B, N, C)
+        dweight = fp8_gemm_mn(dyq, sdy, hq2, sh).to(ctx.wdt)
+        db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
+        dx, _, _, dw, dsh, dsc = _norm_backward(dh, None, x, None, None, w_norm, scale, rstd)
+        _, dw, dshift, dscale = _param_grads(B, C, None, dw, dsh, dsc, None, w_norm, shift, scale)
+        return dx, dw, dshift, dscale, None, dweight, db
+
+
+class _Fp8ResModRMSNormMLP(torch.autograd.Function):
+    """Site 2 feeding the phase-3 FP8 SwiGLU MLP: x_new = x + gate * a and h's e4m3 bytes from one kernel, then
+    w12, the SwiGLU product cast and w3 as _Fp8MLPF8; returns (x_new, y). Backward: the MLP's (FP8 dgrads and
+    wgrads, w12's wgrad from h's bytes), then the norm's with the upstream gradient of x_new."""
+    @staticmethod
+    def forward(ctx, x, a, gate, w_norm, shift, scale, eps, w12, w3):
+        B, N, C = x.shape
+        xn, _, hq, sh, rstd = res_mod_rmsnorm_q(x, a, gate, w_norm, shift, scale, eps, True, False)
+        hq2 = hq.view(B * N, C)
+        w12q, w12qt, s12 = tcast_t(w12)
+        z = fp8_gemm(hq2, sh, w12q, s12)
+        aq, sa = swiglu_tcast(z)
+        w3q, w3qt, s3 = tcast_t(w3)
+        y = fp8_gemm(aq, sa, w3q, s3)
+        ctx.save_for_backward(xn, a, gate, w_norm, shift, scale, rstd, hq2, sh, z, aq, sa, w12qt, s12, w3qt, s3)
+        ctx.dt = (w12.dtype, w3.dtype)
+        return xn, y.view(B, N, w3.shape[0])
+
+    @staticmethod
+    def backward(ctx, dxn, dy):
+        xn, a, gate, w_norm, shift, scale, rstd, hq2, sh, z, aq, sa, w12qt, s12, w3qt, s3 = ctx.saved_tensors
+        B, N, C = xn.shape
+        dy2 = dy.reshape(B * N, -1).to(torch.bfloat16)
+        dyq, sdy = tcast(dy2)
+        da_ = fp8_gemm(dyq, sdy, w3qt, s3, None, False)
+        dw3 = fp8_gemm_mn(dyq, sdy, aq, sa)
+        dzq, sdz = swiglu_bwd_q(z, da_)
+        dh = fp8_gemm(dzq, sdz, w12qt, s12, None, False).view(B, N, C)
+        dw12 = fp8_gemm_mn(dzq, sdz, hq2, sh)
+        dx, da, dg, dw, dsh, dsc = _norm_backward(dh, dxn, xn, a, gate, w_norm, scale, rstd)
+        dgate, dw, dshift, dscale = _param_grads(B, C, dg, dw, dsh, dsc, gate, w_norm, shift, scale)
+        return dx, da, dgate, dw, dshift, dscale, None, dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1])
+
+
+def fp8_mod_rmsnorm_linear(x, w_norm, shift, scale, eps, weight, bias: Optional[torch.Tensor] = None):
+    """linear(mod_rmsnorm(x, w_norm, shift, scale, eps)) with every GEMM in FP8 and the cast of h in the norm."""
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8ModRMSNormLinear.apply(x.to(torch.bfloat16), w_norm, shift, scale, eps, weight, bias)
+
+
+def fp8_res_mod_rmsnorm_mlp(x, a, gate, w_norm, shift, scale, eps, w12, w3):
+    """(x_new, mlp(h)) for x_new, h = res_mod_rmsnorm(x, a, gate, w_norm, shift, scale, eps), the SwiGLU MLP in FP8
+    (every GEMM) and the cast of h in the norm."""
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8ResModRMSNormMLP.apply(x.to(torch.bfloat16), a.to(torch.bfloat16), gate, w_norm, shift, scale, eps,
+                                          w12, w3)

@@ -232,3 +232,51 @@ void gpo_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H,
             dzq[r * 2 * H + k] = cast1(gpo_bf16_to_f32(dz[r * sdz + k]), scale);
     if (amax_out) *amax_out = m;
 }
+
+/* The norm sites' producer (fused_norm.py:64-91, res_mod_rmsnorm forward) as this build defines its arithmetic
+ * (nano-gpic_amd/csrc/norm.hip), row by row, every fp32 operation rounded on its own:
+ *   xb = bf16(x + gate * a) (a != NULL; else xb = x);  rstd = 1 / sqrt(ss / C + eps)  (IEEE);
+ *   n = bf16(w * (xb * rstd));  h = bf16(n * (1 + scale) + shift)
+ * with ss summed in the device's order: lane l (0..63) adds the squares of elements 4 (l + 64 j) + e in the order
+ * j, e; then the 64 lane sums are combined by the butterfly v_l += v_{l ^ o}, o = 32, 16, ..., 1 (C % 256 == 0).
+ * The reference sums in Triton's order and takes libdevice's rsqrt; its own eager formula (fused_norm.py:305-313)
+ * rounds gate * a to bf16 before the add. gate, shift, scale are [B, C] rows (strides sg, ssh, ssc), row r in batch
+ * r / ntok. Writes xn (a != NULL), h and rstd. */
+static inline float norm_xb(const uint16_t *x, const uint16_t *a, const uint16_t *gate, int64_t i, int64_t gi) {
+    float v = gpo_bf16_to_f32(x[i]);
+    if (a) v = gpo_bf16_to_f32(gpo_f32_to_bf16(v + gpo_bf16_to_f32(gate[gi]) * gpo_bf16_to_f32(a[i])));
+    return v;
+}
+
+void gpo_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_t *gate, int64_t sg, const float *w,
+                     const uint16_t *shift, int64_t ssh, const uint16_t *scale, int64_t ssc, int64_t rows, int64_t ntok,
+                     int64_t C, float eps, uint16_t *xn, uint16_t *h, float *rstd) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const int64_t b = r / ntok, J = C / 256;
+        float part[64], nxt[64];
+        for (int l = 0; l < 64; l++) {
+            float s = 0.0f;
+            for (int64_t j = 0; j < J; j++)
+                for (int e = 0; e < 4; e++) {
+                    const int64_t c = 4 * (l + 64 * j) + e;
+                    const float v = norm_xb(x, a, gate, r * C + c, b * sg + c);
+                    s = s + v * v;
+                }
+            part[l] = s;
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            for (int l = 0; l < 64; l++) nxt[l] = part[l] + part[l ^ o];
+            memcpy(part, nxt, sizeof part);
+        }
+        const float rs = 1.0f / sqrtf(part[0] / (float)C + eps);
+        rstd[r] = rs;
+        for (int64_t c = 0; c < C; c++) {
+            const float v = norm_xb(x, a, gate, r * C + c, b * sg + c);
+            if (a) xn[r * C + c] = gpo_f32_to_bf16(v);
+            const float n = gpo_bf16_to_f32(gpo_f32_to_bf16(w[c] * (v * rs)));
+            const float sc = gpo_bf16_to_f32(scale[b * ssc + c]), sh = gpo_bf16_to_f32(shift[b * ssh + c]);
+            h[r * C + c] = gpo_f32_to_bf16(n * (1.0f + sc) + sh);
+        }
+    }
+}

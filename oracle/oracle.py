@@ -73,6 +73,8 @@ def lib():
         L.gpo_swiglu_tcast.argtypes = [_u16p, _i64, _i64, _i64, _u8p, _i64, _f32p, _u32p]
         L.gpo_swiglu_bwd1.argtypes = [ctypes.c_uint16, ctypes.c_uint16, ctypes.c_uint16, _u16p, _u16p]
         L.gpo_swiglu_bwd.argtypes = [_u16p, _u16p, _i64, _i64, _i64, _i64, _u16p, _i64, _u8p, _f32p, _u32p]
+        L.gpo_mod_rmsnorm.argtypes = [_u16p, _u16p, _u16p, _i64, _f32p, _u16p, _i64, _u16p, _i64, _i64, _i64, _i64,
+                                      ctypes.c_float, _u16p, _u16p, _f32p]
         _lib = L
     return _lib
 
@@ -217,6 +219,38 @@ def swiglu_bwd(z, da):
     lib().gpo_swiglu_bwd(_p(z, _u16p), _p(da, _u16p), M, H, H2, H, _p(dz, _u16p), H2, _p(dzq, _u8p),
                          ctypes.byref(d), ctypes.byref(am))
     return dz, dzq, np.float32(d.value), int(am.value)
+
+
+# ---------------------------------------------------------------- the norm sites' producer (fused_norm.py:64-91)
+
+def mod_rmsnorm(x, w, shift, scale, ntok, eps, a=None, gate=None):
+    """res_mod_rmsnorm's forward (a, gate given) or mod_rmsnorm's (fused_norm.py:64-91) in this build's arithmetic:
+    x, a [rows, C] bf16 bits; w [C] fp32; gate, shift, scale [B, C] bf16 bits (row b serves rows b * ntok ..);
+    returns (x_new bits or None, h bits, rstd fp32)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    rows, C = x.shape
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    sh = np.ascontiguousarray(shift, dtype=np.uint16)
+    sc = np.ascontiguousarray(scale, dtype=np.uint16)
+    h = np.empty((rows, C), dtype=np.uint16)
+    rstd = np.empty(rows, dtype=np.float32)
+    if a is not None:
+        a = np.ascontiguousarray(a, dtype=np.uint16)
+        gate = np.ascontiguousarray(gate, dtype=np.uint16)
+        xn = np.empty((rows, C), dtype=np.uint16)
+        ap, gp, xp = _p(a, _u16p), _p(gate, _u16p), _p(xn, _u16p)
+    else:
+        xn, ap, gp, xp = None, None, None, None
+    lib().gpo_mod_rmsnorm(_p(x, _u16p), ap, gp, C, _p(w, _f32p), _p(sh, _u16p), C, _p(sc, _u16p), C, rows, ntok, C,
+                          ctypes.c_float(eps), xp, _p(h, _u16p), _p(rstd, _f32p))
+    return xn, h, rstd
+
+
+def mod_rmsnorm_q(x, w, shift, scale, ntok, eps, a=None, gate=None):
+    """The norm followed by h's tcast: (x_new or None, h, rstd, hq bytes, dequant)."""
+    xn, h, rstd = mod_rmsnorm(x, w, shift, scale, ntok, eps, a, gate)
+    hq, d, _ = tcast(h)
+    return xn, h, rstd, hq, d
 
 
 # ---------------------------------------------------------------- the scaled GEMM (fp8_native.py:175-178, 320-331)

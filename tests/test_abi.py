@@ -73,6 +73,16 @@ def test_validation_codes():
     assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, wsp, 0, wsp, wsp, None) == -1
     assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, None, 16, wsp, wsp, None) == -1
     assert b(wsp, wsp, 4, 16, 32, 16, wsp + 8, wsp, wsp, 16, wsp, wsp, None) == -4
+    # the norm sites' producer: C % 256, rows % ntok, strides, nothing to write, misaligned weight
+    nm = lib.gpic_fp8_res_mod_rmsnorm
+    assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 4, 2, 128, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
+    assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 5, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
+    assert nm(wsp, None, None, 0, wsp, wsp, 255, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
+    assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, None, None, wsp, None) == -1
+    assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, None, wsp, wsp, None) == -1
+    assert nm(wsp, None, None, 0, wsp + 8, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp,
+              None) == -4
+    assert nm(wsp, wsp, None, 256, wsp, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, wsp, None, wsp, wsp, wsp, wsp, None) == -1
     # GEMM: K % 16, N % 16, leading dimensions, null scales
     g = lib.gpic_fp8_gemm
     assert g(wsp, 24, wsp, wsp, 24, wsp, None, wsp, 16, 4, 16, 24, 1, None, 0, None) == -3

@@ -1,0 +1,184 @@
+"""GPU parity of the norm sites' producer with its e4m3 cast (gpic_fp8_res_mod_rmsnorm, norm.hip) against the oracle,
+bit for bit (x_new, rstd, h, h's bytes and scale), and of the functions built on it: the reference's mod_rmsnorm /
+res_mod_rmsnorm API (fused_norm.py:293-313) and the fused FP8 consumers, which must equal the same computation done
+unfused (the norm writing bf16 h, then the phase-3 linear / MLP casting it) bit for bit, forward and backward."""
+import numpy as np
+import pytest
+import torch
+
+import gpic_fp8 as G
+from gpic_fp8 import _lib as L
+from oracle import oracle as O
+from parity import assert_bf16_bits_equal, bits, qb
+
+pytestmark = pytest.mark.gpu
+
+
+def inputs(B, N, C, seed, dev, res=True, k=1.0, outliers=0.0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(B, N, C, generator=g, device=dev) * k
+    if outliers:
+        cols = torch.randperm(C, generator=g, device=dev)[:round(outliers * C)]
+        x[..., cols] *= 50.0
+    x = x.to(torch.bfloat16)
+    a = torch.randn(B, N, C, generator=g, device=dev).to(torch.bfloat16)
+    # gate / shift / scale as the block gets them: [B, 1, C] chunks (strided views) of one adaLN output
+    mod = (torch.randn(B, 1, 6 * C, generator=g, device=dev) * 0.2).to(torch.bfloat16)
+    shift, scale, gate = mod[..., :C], mod[..., C:2 * C], mod[..., 2 * C:3 * C]
+    w = (1 + 0.1 * torch.randn(C, generator=g, device=dev))
+    return x, (a if res else x), (gate if res else x), w, shift, scale
+
+
+def oracle(x, a, gate, w, shift, scale, eps, res):
+    B, N, C = x.shape
+    u = lambda t, r: bits(t.reshape(r, C))
+    return O.mod_rmsnorm_q(u(x, B * N), w.cpu().numpy(), u(shift, B), u(scale, B), N, eps,
+                           u(a, B * N) if res else None, u(gate, B) if res else None)
+
+
+def check(x, a, gate, w, shift, scale, eps, res):
+    B, N, C = x.shape
+    xn, h, hq, s, rstd = G.res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, res, True)
+    oxn, oh, orstd, ohq, od = oracle(x, a, gate, w, shift, scale, eps, res)
+    if res:
+        assert np.array_equal(bits(xn.reshape(-1, C)), oxn)
+    assert np.array_equal(rstd.cpu().numpy().view(np.uint32), orstd.view(np.uint32)), "rstd"
+    assert_bf16_bits_equal(bits(h.reshape(-1, C)), oh)
+    assert s.item() == od, (s.item(), od)
+    assert np.array_equal(qb(hq.reshape(-1, C)), ohq)
+    # without the bf16 h: the same bytes
+    _, h0, hq0, s0, _ = G.res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, res, False)
+    assert h0.numel() == 0 and s0.item() == s.item() and torch.equal(hq0.view(torch.uint8), hq.view(torch.uint8))
+    # the norm alone (no cast, the reference's op): the same h, x_new and rstd
+    xn1, h1, hq1, s1, r1 = G.res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, res, True, False)
+    assert hq1.numel() == 0 and s1.numel() == 0
+    assert torch.equal(h1.view(torch.int16), h.view(torch.int16)) and torch.equal(r1.view(torch.int32), rstd.view(torch.int32))
+    if res:
+        assert torch.equal(xn1.view(torch.int16), xn.view(torch.int16))
+    return hq, s
+
+
+@pytest.fixture
+def knob():
+    yield
+    L.set_single_pass(True, -1)
+
+
+@pytest.mark.parametrize("res", [False, True])
+@pytest.mark.parametrize("B,N,C", [
+    (128, 256, 1024),    # d12, one GPU's 32768 tokens: the single pass (8 rows per wave, 1024 workgroups)
+    (128, 256, 1792),    # d18: more than the single pass holds -> two passes
+    (2, 100, 768),       # single pass, a partly filled last workgroup
+    (3, 64, 2560),       # wider than the single pass takes (C / 256 = 10) -> two passes
+    (8, 512, 256),       # narrow rows (10 per wave)
+])
+def test_norm_against_oracle(dev, B, N, C, res):
+    x, a, gate, w, shift, scale = inputs(B, N, C, B + N + C + res, dev, res, outliers=0.01)
+    check(x, a, gate, w, shift, scale, 1e-6, res)
+
+
+def test_norm_single_two_pass_and_zero_wait_agree(dev, knob):
+    """The d12 site 2 through the single pass, its zero-wait path (partials not yet published computed from the rows)
+    and the forced two-pass path: the same bytes, equal to the oracle's."""
+    x, a, gate, w, shift, scale = inputs(128, 256, 1024, 11, dev, True)
+    outs = []
+    for enabled, wait in ((True, -1), (True, 0), (False, -1)):
+        L.set_single_pass(enabled, wait)
+        outs.append(check(x, a, gate, w, shift, scale, 1e-6, True))
+    for hq, s in outs[1:]:
+        assert s.item() == outs[0][1].item() and torch.equal(hq.view(torch.uint8), outs[0][0].view(torch.uint8))
+
+
+def test_norm_nan_row_and_empty(dev):
+    """A NaN in x makes its row NaN (as the reference's would), ignored by the amax and cast to -448 (the cast rule);
+    an empty input writes only the scale of an empty tensor."""
+    x, a, gate, w, shift, scale = inputs(4, 64, 1024, 12, dev, True)
+    x[1, 7, 100] = float("nan")
+    check(x, a, gate, w, shift, scale, 1e-6, True)
+    e = x[:, :0]
+    xn, h, hq, s, rstd = G.res_mod_rmsnorm_q(e, e, gate, w, shift, scale, 1e-6, True, True)
+    assert hq.numel() == 0 and s.item() == np.float32(1e-12) / np.float32(448.0)
+
+
+def _eager(x, a, gate, w, shift, scale, eps, res):
+    """The reference kernel's formula (x + gate * a in fp32, one rounding of h) in torch fp32 autograd."""
+    xs = (x.float() + gate.float() * a.float()) if res else x.float()
+    xs = xs.to(torch.bfloat16).float() if res else xs
+    r = torch.rsqrt(xs.pow(2).mean(-1, keepdim=True) + eps)
+    n = (w.float() * (xs * r))
+    return xs, n * (1 + scale.float()) + shift.float()
+
+
+@pytest.mark.parametrize("res", [False, True])
+def test_drop_in_api_and_backward(dev, res):
+    """mod_rmsnorm / res_mod_rmsnorm (the reference's API): h is the kernel's (the oracle's) and the gradients of x,
+    a, gate, w, shift, scale are within 1e-2 of fp32 autograd of the reference kernel's formula."""
+    B, N, C, eps = 4, 128, 1024, 1e-6
+    x, a, gate, w, shift, scale = inputs(B, N, C, 13 + res, dev, res)
+    leaves = [t.detach().clone().requires_grad_() for t in (x, a, gate, w, shift, scale)]
+    xl, al, gl, wl, shl, scl = leaves
+    if res:
+        xn, h = G.res_mod_rmsnorm(xl, al, gl, wl, shl, scl, eps)
+    else:
+        h = G.mod_rmsnorm(xl, wl, shl, scl, eps)
+    _, oh, _, _, _ = oracle(x, a, gate, w, shift, scale, eps, res)
+    assert_bf16_bits_equal(bits(h.reshape(-1, C)), oh)
+    dh = (torch.randn_like(h) * 0.1).to(torch.bfloat16)
+    dxn = (torch.randn_like(h) * 0.1).to(torch.bfloat16) if res else None
+    torch.autograd.backward([h, xn] if res else [h], [dh, dxn] if res else [dh])
+    ref_leaves = [t.detach().float().clone().requires_grad_() for t in (x, a, gate, w, shift, scale)]
+    rxs, rh = _eager(*ref_leaves, eps, res)
+    torch.autograd.backward([rh, rxs] if res else [rh], [dh.float(), dxn.float()] if res else [dh.float()])
+    names = ("x", "a", "gate", "w", "shift", "scale") if res else ("x", None, None, "w", "shift", "scale")
+    for n, got, want in zip(names, leaves, ref_leaves):
+        if n is None:
+            continue
+        r = (torch.linalg.norm(got.grad.float() - want.grad) / torch.linalg.norm(want.grad)).item()
+        assert r < 1e-2, (n, r)
+
+
+def test_fused_site1_linear_equals_unfused(dev):
+    """fp8_mod_rmsnorm_linear (h cast in the norm, never written in bf16) against mod_rmsnorm then fp8_linear_f8 (h
+    written in bf16 and cast by tcast): the same output and gradients bit for bit."""
+    B, N, C, eps = 8, 256, 1024, 1e-6
+    x, _, _, w, shift, scale = inputs(B, N, C, 21, dev, False, outliers=0.01)
+    g = torch.Generator(device=dev).manual_seed(22)
+    weight = (torch.randn(3 * C, C, generator=g, device=dev) / C ** 0.5).to(torch.bfloat16)
+    dy = (torch.randn(B, N, 3 * C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    runs = []
+    for fused in (True, False):
+        leaves = [t.detach().clone().requires_grad_() for t in (x, w, shift, scale, weight)]
+        xl, wl, shl, scl, Wl = leaves
+        y = (G.fp8_mod_rmsnorm_linear(xl, wl, shl, scl, eps, Wl) if fused
+             else G.fp8_linear_f8(G.mod_rmsnorm(xl, wl, shl, scl, eps), Wl))
+        y.backward(dy)
+        runs.append([y] + [t.grad for t in leaves])
+    for got, want in zip(*runs):
+        assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got,
+                           want.view(torch.int16) if want.dtype == torch.bfloat16 else want)
+
+
+def test_fused_site2_mlp_equals_unfused(dev):
+    """fp8_res_mod_rmsnorm_mlp against res_mod_rmsnorm then fp8_mlp_f8: x_new, the MLP output and every gradient
+    (x, a, gate, w, shift, scale, w12, w3) bit for bit."""
+    B, N, C, H, eps = 8, 256, 1024, 4096, 1e-6
+    x, a, gate, w, shift, scale = inputs(B, N, C, 31, dev, True)
+    g = torch.Generator(device=dev).manual_seed(32)
+    w12 = (torch.randn(2 * H, C, generator=g, device=dev) / C ** 0.5).to(torch.bfloat16)
+    w3 = (torch.randn(C, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16)
+    dy = (torch.randn(B, N, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    dxn = (torch.randn(B, N, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    runs = []
+    for fused in (True, False):
+        leaves = [t.detach().clone().requires_grad_() for t in (x, a, gate, w, shift, scale, w12, w3)]
+        xl, al, gl, wl, shl, scl, w12l, w3l = leaves
+        if fused:
+            xn, y = G.fp8_res_mod_rmsnorm_mlp(xl, al, gl, wl, shl, scl, eps, w12l, w3l)
+        else:
+            xn, h = G.res_mod_rmsnorm(xl, al, gl, wl, shl, scl, eps)
+            y = G.fp8_mlp_f8(h, w12l, w3l)
+        torch.autograd.backward([xn, y], [dxn, dy])
+        runs.append([xn, y] + [t.grad for t in leaves])
+    for got, want in zip(*runs):
+        assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got,
+                           want.view(torch.int16) if want.dtype == torch.bfloat16 else want)

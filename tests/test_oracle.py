@@ -307,3 +307,74 @@ def test_torch_swiglu_equals_c_oracle():
     assert diff.max() <= 1 and (diff == 0).mean() > 0.99
     q2, s2 = O.torch_tcast(dz)
     assert s2.item() == sdz.item() and torch.equal(q2.view(torch.uint8), dzq.view(torch.uint8))
+
+
+# ---------------------------------------------------------------- the norm sites' producer (fused_norm.py:64-91)
+
+def _norm_inputs(B, N, C, seed, res=True, k=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(B, N, C, generator=g) * k).to(torch.bfloat16)
+    a = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
+    gate = (torch.randn(B, 1, C, generator=g) * 0.2).to(torch.bfloat16)
+    sh = (torch.randn(B, 1, C, generator=g) * 0.1).to(torch.bfloat16)
+    sc = (torch.randn(B, 1, C, generator=g) * 0.1).to(torch.bfloat16)
+    w = 1 + 0.1 * torch.randn(C, generator=g)
+    return x, (a if res else None), (gate if res else None), w, sh, sc
+
+
+def _oracle_norm(x, a, gate, w, sh, sc, eps):
+    B, N, C = x.shape
+    return O.mod_rmsnorm(_u16(x).reshape(-1, C), w.numpy(), _u16(sh).reshape(B, C), _u16(sc).reshape(B, C), N, eps,
+                         None if a is None else _u16(a).reshape(-1, C),
+                         None if gate is None else _u16(gate).reshape(B, C))
+
+
+@pytest.mark.parametrize("res", [False, True])
+@pytest.mark.parametrize("C", [256, 768, 1024, 1792])
+def test_norm_against_torch(res, C):
+    """x_new equals torch's x + gate * a in fp32 rounded once to bf16 (the reference kernel's, fused_norm.py:82); rstd
+    is within 2 fp32 ulp of torch.rsqrt(mean(x_new^2) + eps); h equals torch's n = bf16(w * (x_new * rstd)),
+    bf16(n * (1 + scale) + shift) in fp32 (fused_norm.py:85-89) bit for bit when fed the oracle's rstd."""
+    B, N, eps = 3, 40, 1e-6
+    x, a, gate, w, sh, sc = _norm_inputs(B, N, C, C + res, res)
+    xn, h, rstd = _oracle_norm(x, a, gate, w, sh, sc, eps)
+    xs = (x.float() + gate.float() * a.float()).to(torch.bfloat16) if res else x
+    if res:
+        assert np.array_equal(xn, _u16(xs).reshape(-1, C))
+    rs_t = torch.rsqrt(xs.float().pow(2).mean(-1) + eps).reshape(-1).numpy()
+    assert np.abs(rstd.astype(np.float64) / rs_t - 1).max() <= 2.5e-7
+    r = torch.from_numpy(rstd).view(B, N, 1)
+    n = (w * (xs.float() * r)).to(torch.bfloat16).float()
+    ht = (n * (1 + sc.float()) + sh.float()).to(torch.bfloat16)
+    assert np.array_equal(h, _u16(ht).reshape(-1, C))
+
+
+def test_norm_power_of_two_invariance():
+    """With eps = 0, scaling x by 2^k leaves h unchanged bit for bit (the sum of squares, the square root and the
+    division scale exactly): a check of the sum's structure that does not restate it."""
+    x, _, _, w, sh, sc = _norm_inputs(2, 33, 1024, 5, False)
+    _, h0, r0 = _oracle_norm(x, None, None, w, sh, sc, 0.0)
+    for k in (-3, 2, 7):
+        _, h1, r1 = _oracle_norm((x.float() * 2.0 ** k).to(torch.bfloat16), None, None, w, sh, sc, 0.0)
+        assert np.array_equal(h0, h1) and np.array_equal(r1 * np.float32(2.0 ** k), r0)
+
+
+def test_norm_mutant_unrounded_n_fails():
+    """A restatement that skips the bf16 rounding of n (fused_norm.py:86) is caught by the torch comparison above."""
+    x, _, _, w, sh, sc = _norm_inputs(2, 40, 1024, 6, False)
+    _, h, rstd = _oracle_norm(x, None, None, w, sh, sc, 1e-6)
+    r = torch.from_numpy(rstd).view(2, 40, 1)
+    n_unrounded = w * (x.float() * r)
+    hm = (n_unrounded * (1 + sc.float()) + sh.float()).to(torch.bfloat16)
+    assert not np.array_equal(h, _u16(hm).reshape(-1, 1024))
+
+
+def test_norm_q_is_tcast_of_h():
+    """mod_rmsnorm_q's bytes and scale are the tcast of its h (the cast rule pinned above)."""
+    x, a, gate, w, sh, sc = _norm_inputs(2, 64, 1024, 7, True)
+    B, N, C = x.shape
+    xn, h, rstd, hq, d = O.mod_rmsnorm_q(_u16(x).reshape(-1, C), w.numpy(), _u16(sh).reshape(B, C),
+                                         _u16(sc).reshape(B, C), N, 1e-6, _u16(a).reshape(-1, C),
+                                         _u16(gate).reshape(B, C))
+    q2, d2, _ = O.tcast(h)
+    assert d == d2 and np.array_equal(hq, q2)
