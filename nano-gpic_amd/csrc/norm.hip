@@ -8,19 +8,20 @@
 // that the linear that consumes h reads 1 byte per element and h itself never has to exist in bf16 (it may be written
 // as well, for a caller that wants it). x_new and the per-row 1 / rms (rstd) are written for the backward.
 //
-// The arithmetic, every fp32 operation rounded on its own (-ffp-contract=off), row by row:
-//   xb = bf16(x + gate * a)                     (site 2; site 1: xb = x)
-//   ss = sum of xb^2: lane l of the row's wave adds the squares of its elements 4 (l + 64 j) + e in the order j, e,
-//        then the 64 lane sums are combined by the butterfly v += v[lane ^ o], o = 32, 16, 8, 4, 2, 1
+// The arithmetic, row by row, in fp32; fma() is one fused multiply-add (one rounding, as Triton compiles the
+// reference's a * b + c on the GPU), every other operation rounds on its own (-ffp-contract=off):
+//   xb = bf16(fma(gate, a, x))                  (site 2; site 1: xb = x)
+//   ss: lane l of the row's wave accumulates ss = fma(xb, xb, ss) over its elements 4 (l + 64 j) + e in the order
+//       j, e, then the 64 lane sums are combined by the butterfly v += v[lane ^ o], o = 32, 16, 8, 4, 2, 1
 //   rstd = 1 / sqrt(ss / C + eps)               (IEEE division and square root)
-//   n = bf16(w * (xb * rstd));  h = bf16(n * (1 + scale) + shift)
+//   n = bf16(w * (xb * rstd));  h = bf16(fma(n, 1 + scale, shift))
 // The reference computes the same expression with Triton's reduction order and libdevice's rsqrt, whose last bits
 // are the H100's: this build fixes the order above, which the CPU oracle restates bit for bit.
 //
 // Two designs, as for the casts: rows that fit the chip's registers (C <= 2048 and at most the single-pass capacity)
 // take one launch -- each wave holds the bf16 h of its rows, the workgroups agree on the amax through the tagged
-// partials of the cast workspace (gpic_once.h), and each casts from its registers; larger ones take two, the second
-// recomputing h from the x_new (or x) and rstd the first wrote.
+// partials of the cast workspace (gpic_once.h), and each casts from its registers; larger ones, and calls that want
+// the bf16 h written as well, take two, the second recomputing h from the x_new (or x) and rstd the first wrote.
 #include <algorithm>
 
 #include "gpic_device.h"
@@ -48,9 +49,36 @@ struct NormArgs {
 
 __device__ __forceinline__ u32x2 ld8(const uint16_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
 
+// No memory access and no instruction moves across this point, neither in the compiler's IR nor in its machine
+// scheduler: keeps loads in the phase they belong to (hoisted loads hold registers from the top of the kernel).
+__device__ __forceinline__ void phase_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // The four fp32 values of a group's 8 bytes of bf16.
 __device__ __forceinline__ void unpack4(u32x2 v, float (&f)[4]) {
   f[0] = bf16_lo(v.x), f[1] = bf16_hi(v.x), f[2] = bf16_lo(v.y), f[3] = bf16_hi(v.y);
+}
+
+// x_new = bf16(x + gate * a) of four elements, the product and sum fused (one rounding, as the reference's Triton
+// kernel compiles x + g * a), packed.
+__device__ __forceinline__ u32x2 xnew_packed(const float (&x)[4], const float (&g)[4], const float (&a)[4]) {
+  return u32x2{pack_bf16(__builtin_fmaf(g[0], a[0], x[0]), __builtin_fmaf(g[1], a[1], x[1])),
+               pack_bf16(__builtin_fmaf(g[2], a[2], x[2]), __builtin_fmaf(g[3], a[3], x[3]))};
+}
+
+// h of four elements, packed bf16 (and in hv before its rounding): n = bf16(w * (x * rstd));
+// h = bf16(n * (1 + scale) + shift) with the multiply-add fused.
+__device__ __forceinline__ u32x2 h_packed(const float (&x)[4], const float (&w)[4], float rstd, const float (&sc)[4],
+                                          const float (&sh)[4], float (&hv)[4]) {
+  const u32x2 nw{pack_bf16(w[0] * (x[0] * rstd), w[1] * (x[1] * rstd)),
+                 pack_bf16(w[2] * (x[2] * rstd), w[3] * (x[3] * rstd))};
+  float n[4];
+  unpack4(nw, n);
+#pragma unroll
+  for (int e = 0; e < 4; e++) hv[e] = __builtin_fmaf(n[e], 1.0f + sc[e], sh[e]);
+  return u32x2{pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3])};
 }
 
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
@@ -77,13 +105,12 @@ __device__ __forceinline__ uint32_t norm_row(const NormArgs &p, int64_t row, u32
       float av[4], gv[4];
       unpack4(ld8(p.a + row * p.C + c), av);
       unpack4(ld8(p.gate + b * p.sg + c), gv);
-#pragma unroll
-      for (int e = 0; e < 4; e++) x[e] = bf16_round(x[e] + gv[e] * av[e]);
-      if (kStore)
-        *reinterpret_cast<u32x2 *>(p.xn + row * p.C + c) = u32x2{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
+      const u32x2 xb = xnew_packed(x, gv, av);
+      unpack4(xb, x);
+      if (kStore) *reinterpret_cast<u32x2 *>(p.xn + row * p.C + c) = xb;
     }
 #pragma unroll
-    for (int e = 0; e < 4; e++) ss = ss + x[e] * x[e];
+    for (int e = 0; e < 4; e++) ss = __builtin_fmaf(x[e], x[e], ss);
   }
   ss = wave_sum_butterfly(ss);
   // (__builtin_sqrtf is the correctly rounded square root; HIP's __fsqrt_rn maps to the hardware approximation)
@@ -98,8 +125,7 @@ __device__ __forceinline__ uint32_t norm_row(const NormArgs &p, int64_t row, u32
       unpack4(ld8(xr + c), x);
       unpack4(ld8(p.a + row * p.C + c), av);
       unpack4(ld8(p.gate + b * p.sg + c), gv);
-#pragma unroll
-      for (int e = 0; e < 4; e++) x[e] = bf16_round(x[e] + gv[e] * av[e]);
+      unpack4(xnew_packed(x, gv, av), x);
     } else {
       unpack4(ld8(xr + c), x);
     }
@@ -108,12 +134,7 @@ __device__ __forceinline__ uint32_t norm_row(const NormArgs &p, int64_t row, u32
     unpack4(ld8(p.scale + b * p.ssc + c), sc);
     const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
     float hv[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const float n = bf16_round(w4[e] * (x[e] * rstd));
-      hv[e] = n * (1.0f + sc[e]) + sh[e];
-    }
-    const u32x2 hw{pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3])};
+    const u32x2 hw = h_packed(x, w4, rstd, sc, sh, hv);
     m = max(m, max(bf16x2_absmax_nonan(hw.x), bf16x2_absmax_nonan(hw.y)));
     if (kJ > 0) H[j] = hw;
     if (kStore && p.h) *reinterpret_cast<u32x2 *>(p.h + row * p.C + c) = hw;
@@ -130,12 +151,7 @@ __device__ __forceinline__ u32x2 h_from_stats(const NormArgs &p, int64_t row, in
   unpack4(ld8(p.scale + b * p.ssc + c), sc);
   const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
   float hv[4];
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const float n = bf16_round(w4[e] * (x[e] * rstd));
-    hv[e] = n * (1.0f + sc[e]) + sh[e];
-  }
-  return u32x2{pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3])};
+  return h_packed(x, w4, rstd, sc, sh, hv);
 }
 
 __device__ __forceinline__ uint32_t cast4_packed(u32x2 hw, float s) {
@@ -143,45 +159,148 @@ __device__ __forceinline__ uint32_t cast4_packed(u32x2 hw, float s) {
 }
 
 // Single pass: wave w of workgroup g holds rows (4 g + w) kR .. + kR - 1 (kJ groups of 4 per lane each), the
-// workgroups fold their maxima (gpic_once.h), and each casts its rows from its registers.
-template <int kJ, int kR>
+// workgroups fold their maxima (gpic_once.h), and each casts its rows from its registers. The rows of a wave go
+// through each phase together, so that one memory latency covers all of them: every row's x is requested first,
+// then (site 2) a and gate are folded in, the kR butterflies run interleaved, and w, shift and scale are read once
+// per group and used for all the rows; h replaces x in the same registers. Rows past the end re-read the last row
+// (same values, so the same maximum) and store nothing. kUni: every row of a wave lies in one batch (ntok % kR ==
+// 0), so gate, shift and scale are one vector per wave.
+template <int kJ, int kR, bool kUni, bool kRes>
 __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *ws, uint32_t wait_ticks) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  auto row_of = [&](int64_t g, int r) { return (g * 4 + wave) * kR + r; };
-  u32x2 H[kR][kJ];
-  uint32_t m = 0;
+  // (the wave index as a scalar: the rows' addresses are then scalar bases plus one per-lane offset)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * kR;
+  const int64_t C = p.C;
+  auto rowi = [&](int r) { return min(row0 + r, p.rows - 1); };
+  auto bat = [&](int r) { return (kUni ? row0 : rowi(r)) / p.ntok; };
+  u32x2 X[kR][kJ];
+#pragma unroll
+  for (int r = 0; r < kR; r++)
+#pragma unroll
+    for (int j = 0; j < kJ; j++) X[r][j] = ld8(p.x + rowi(r) * C + 4 * (lane + 64 * j));
+  const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);   // rows of this wave that exist
+  // site 2: a (and, per row unless kUni, gate) through a ring of kD rows: the loads of row r + kD - 1 are issued
+  // before row r is used, and the fences keep the compiler from hoisting every row's loads to the top (x and a of
+  // all rows at once would not fit the registers)
+  constexpr int kD = 3;
+  u32x2 A[kD][kJ], Gt[kD][kJ], G0[kJ];
+  auto load_a = [&](int r) {
+#pragma unroll
+    for (int j = 0; j < kJ; j++) {
+      A[r % kD][j] = ld8(p.a + rowi(r) * C + 4 * (lane + 64 * j));
+      if (!kUni) Gt[r % kD][j] = ld8(p.gate + bat(r) * p.sg + 4 * (lane + 64 * j));
+    }
+  };
+  if (kRes) {
+    if (kUni) {
+#pragma unroll
+      for (int j = 0; j < kJ; j++) G0[j] = ld8(p.gate + bat(0) * p.sg + 4 * (lane + 64 * j));
+    }
+#pragma unroll
+    for (int r = 0; r < kD - 1 && r < kR; r++) load_a(r);
+  }
+  // phase 1: x_new (site 2) and each lane's sum of squares, row by row as the rows come in
+  float S[kR];
 #pragma unroll
   for (int r = 0; r < kR; r++) {
-    const int64_t row = row_of(blockIdx.x, r);
-    if (row < p.rows) {
-      m = max(m, norm_row<kJ, true>(p, row, H[r]));
-    } else {
+    S[r] = 0.0f;
+    if (kRes) {
+      if (r + kD - 1 < kR) load_a(r + kD - 1);
+      phase_fence();
+    }
 #pragma unroll
-      for (int j = 0; j < kJ; j++) H[r][j] = u32x2{0u, 0u};
+    for (int j = 0; j < kJ; j++) {
+      float x[4];
+      unpack4(X[r][j], x);
+      if (kRes) {
+        float av[4], gv[4];
+        unpack4(A[r % kD][j], av);
+        unpack4(kUni ? G0[j] : Gt[r % kD][j], gv);
+        X[r][j] = xnew_packed(x, gv, av);
+        unpack4(X[r][j], x);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) S[r] = __builtin_fmaf(x[e], x[e], S[r]);
+    }
+    // row r's results are made here, before the next row's fence (the compiler would otherwise sink the arithmetic
+    // to its uses and keep every row's a live); the packed words are then the only copy of the row (else phase 1's
+    // unpacked fp32 values are reused in phase 3 and the registers double)
+#pragma unroll
+    for (int j = 0; j < kJ; j++) asm volatile("" : "+v"(X[r][j]));
+    asm volatile("" : "+v"(S[r]));
+    if (kRes && r < nr) {
+#pragma unroll
+      for (int j = 0; j < kJ; j++) *reinterpret_cast<u32x2 *>(p.xn + (row0 + r) * C + 4 * (lane + 64 * j)) = X[r][j];
     }
   }
-  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int c) {
-    // workgroup c's maximum from its rows (nothing stored): for a partial that did not appear in time
-    uint32_t a = 0;
-    for (int r = 0; r < kR; r++) {
-      const int64_t row = row_of(c, r);
-      if (row < p.rows) a = max(a, norm_row<0, false>(p, row, nullptr));
+  // phase 2: the kR butterflies interleaved, rstd
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+    for (int r = 0; r < kR; r++) S[r] = S[r] + __shfl_xor(S[r], o, 64);
+  phase_fence();   // w, shift and scale are read below, not hoisted to the top beside the rows
+  float rs[kR];
+#pragma unroll
+  for (int r = 0; r < kR; r++) {
+    rs[r] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(S[r], (float)p.C) + p.eps));
+    if (lane == r && r < nr) p.rstd[row0 + r] = rs[r];
+  }
+  // phase 3: h in place of x, and the largest |h|. Its loads of w, shift and scale come after every row's x (the
+  // vector memory counter is in order), so this phase starts once all the rows are in: the reason the rows are not
+  // taken in smaller batches.
+  float mf = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kJ; j++) {
+    const int c = 4 * (lane + 64 * j);
+    const float4 wv = *reinterpret_cast<const float4 *>(p.w + c);
+    const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
+    float sh[4], sc[4];
+    if (kUni) {
+      unpack4(ld8(p.shift + bat(0) * p.ssh + c), sh);
+      unpack4(ld8(p.scale + bat(0) * p.ssc + c), sc);
     }
-    return block_max_u32(a);
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      if (!kUni) {
+        unpack4(ld8(p.shift + bat(r) * p.ssh + c), sh);
+        unpack4(ld8(p.scale + bat(r) * p.ssc + c), sc);
+      }
+      float x[4], hv[4];
+      unpack4(X[r][j], x);
+      X[r][j] = h_packed(x, w4, rs[r], sc, sh, hv);
+      // the largest |h| in fp32, NaN ignored (maxNum); rounded to bf16 at the end, it is the largest |bf16 h|
+      // (rounding is monotonic), in one instruction per element instead of a compare and select on the halves
+#pragma unroll
+      for (int e = 0; e < 4; e++) mf = fmaxf(mf, fabsf(hv[e]));
+    }
+  }
+  // h is made here, before the fold, and kept only as packed words (the compiler would otherwise carry phase 3's
+  // fp32 values across the fold into the cast below)
+#pragma unroll
+  for (int r = 0; r < kR; r++)
+#pragma unroll
+    for (int j = 0; j < kJ; j++) asm volatile("" : "+v"(X[r][j]));
+  phase_fence();
+  const uint32_t g = once_fold(block_max_u32(__float_as_uint(bf16_round(mf))), ws, wait_ticks, [&](int cb) {
+    // workgroup cb's maximum from its rows (nothing stored): for a partial that did not appear in time
+    uint32_t v = 0;
+    for (int r = 0; r < kR; r++) {
+      const int64_t row = ((int64_t)cb * 4 + wave) * kR + r;
+      if (row < p.rows) v = max(v, norm_row<0, false>(p, row, nullptr));
+    }
+    return block_max_u32(v);
   });
   float scale, deq;
   scales_from_amax(g, scale, deq);
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.dequant = deq;
 #pragma unroll
-  for (int r = 0; r < kR; r++) {
-    const int64_t row = row_of(blockIdx.x, r);
-    if (row < p.rows) {
+  for (int r = 0; r < kR; r++)
+    if (r < nr) {
 #pragma unroll
       for (int j = 0; j < kJ; j++)
-        __builtin_nontemporal_store(cast4_packed(H[r][j], scale),
-                                    reinterpret_cast<uint32_t *>(p.hq + row * p.C + 4 * (lane + 64 * j)));
+        __builtin_nontemporal_store(cast4_packed(X[r][j], scale),
+                                    reinterpret_cast<uint32_t *>(p.hq + (row0 + r) * C + 4 * (lane + 64 * j)));
     }
-  }
 }
 
 // Two passes, 1: rows strided over the waves of the grid; x_new, rstd (and h) written, one partial maximum per
@@ -218,11 +337,13 @@ __global__ __launch_bounds__(256) void norm_cast_kernel(NormArgs p, const uint32
 
 // ------------------------------------------------------------------------------------------- host side
 
-static DeviceCache g_cap_norm[9];
+static DeviceCache g_cap_norm[9][2][2];   // [kJ][kUni][kRes]
 struct NormCacheInit {
   NormCacheInit() {
-    for (auto &c : g_cap_norm)
-      for (int i = 0; i < kMaxDevices; i++) c[i] = -1;
+    for (auto &cj : g_cap_norm)
+      for (auto &cu : cj)
+        for (auto &c : cu)
+          for (int i = 0; i < kMaxDevices; i++) c[i] = -1;
   }
 };
 static NormCacheInit g_norm_cache_init;
@@ -232,14 +353,23 @@ static NormCacheInit g_norm_cache_init;
 template <int kJ>
 constexpr int kRowsOnce = kJ >= 3 ? 32 / kJ : 10;
 
+template <int kJ, bool kUni, bool kRes>
+static bool launch_norm_once_t(const NormArgs &p, void *ws, hipStream_t st) {
+  constexpr int kR = kRowsOnce<kJ>;
+  const int cap = once_capacity(reinterpret_cast<const void *>(&norm_q_once_kernel<kJ, kR, kUni, kRes>),
+                                g_cap_norm[kJ][kUni][kRes]);
+  const int64_t wgs = (p.rows + 4 * kR - 1) / (4 * kR);
+  if (cap <= 0 || wgs > cap) return false;
+  norm_q_once_kernel<kJ, kR, kUni, kRes><<<(int)wgs, 256, 0, st>>>(p, ws, once_wait_ticks());
+  return true;
+}
+
 template <int kJ>
 static bool launch_norm_once(const NormArgs &p, void *ws, hipStream_t st) {
-  constexpr int kR = kRowsOnce<kJ>;
-  const int cap = once_capacity(reinterpret_cast<const void *>(&norm_q_once_kernel<kJ, kR>), g_cap_norm[kJ]);
-  const int64_t wgs = (p.rows + 4 * kR - 1) / (4 * kR);
-  if (!once_enabled() || cap <= 0 || wgs > cap) return false;
-  norm_q_once_kernel<kJ, kR><<<(int)wgs, 256, 0, st>>>(p, ws, once_wait_ticks());
-  return true;
+  if (!once_enabled() || p.h) return false;   // (bf16 h as well: the two passes)
+  const bool uni = p.ntok % kRowsOnce<kJ> == 0;
+  if (p.a) return uni ? launch_norm_once_t<kJ, true, true>(p, ws, st) : launch_norm_once_t<kJ, false, true>(p, ws, st);
+  return uni ? launch_norm_once_t<kJ, true, false>(p, ws, st) : launch_norm_once_t<kJ, false, false>(p, ws, st);
 }
 
 }  // namespace gpic

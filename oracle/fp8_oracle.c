@@ -234,17 +234,19 @@ void gpo_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H,
 }
 
 /* The norm sites' producer (fused_norm.py:64-91, res_mod_rmsnorm forward) as this build defines its arithmetic
- * (nano-gpic_amd/csrc/norm.hip), row by row, every fp32 operation rounded on its own:
- *   xb = bf16(x + gate * a) (a != NULL; else xb = x);  rstd = 1 / sqrt(ss / C + eps)  (IEEE);
- *   n = bf16(w * (xb * rstd));  h = bf16(n * (1 + scale) + shift)
- * with ss summed in the device's order: lane l (0..63) adds the squares of elements 4 (l + 64 j) + e in the order
- * j, e; then the 64 lane sums are combined by the butterfly v_l += v_{l ^ o}, o = 32, 16, ..., 1 (C % 256 == 0).
+ * (nano-gpic_amd/csrc/norm.hip), row by row in fp32; fmaf is one fused multiply-add (one rounding, as Triton
+ * compiles the reference's a * b + c on the GPU), every other operation rounds on its own:
+ *   xb = bf16(fmaf(gate, a, x)) (a != NULL; else xb = x);  rstd = 1 / sqrt(ss / C + eps)  (IEEE);
+ *   n = bf16(w * (xb * rstd));  h = bf16(fmaf(n, 1 + scale, shift))
+ * with ss accumulated in the device's order: lane l (0..63) takes ss = fmaf(xb, xb, ss) over elements
+ * 4 (l + 64 j) + e in the order j, e; then the 64 lane sums are combined by the butterfly v_l += v_{l ^ o},
+ * o = 32, 16, ..., 1 (C % 256 == 0).
  * The reference sums in Triton's order and takes libdevice's rsqrt; its own eager formula (fused_norm.py:305-313)
  * rounds gate * a to bf16 before the add. gate, shift, scale are [B, C] rows (strides sg, ssh, ssc), row r in batch
  * r / ntok. Writes xn (a != NULL), h and rstd. */
 static inline float norm_xb(const uint16_t *x, const uint16_t *a, const uint16_t *gate, int64_t i, int64_t gi) {
     float v = gpo_bf16_to_f32(x[i]);
-    if (a) v = gpo_bf16_to_f32(gpo_f32_to_bf16(v + gpo_bf16_to_f32(gate[gi]) * gpo_bf16_to_f32(a[i])));
+    if (a) v = gpo_bf16_to_f32(gpo_f32_to_bf16(fmaf(gpo_bf16_to_f32(gate[gi]), gpo_bf16_to_f32(a[i]), v)));
     return v;
 }
 
@@ -261,7 +263,7 @@ void gpo_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_t *gate,
                 for (int e = 0; e < 4; e++) {
                     const int64_t c = 4 * (l + 64 * j) + e;
                     const float v = norm_xb(x, a, gate, r * C + c, b * sg + c);
-                    s = s + v * v;
+                    s = fmaf(v, v, s);
                 }
             part[l] = s;
         }
@@ -276,7 +278,7 @@ void gpo_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_t *gate,
             if (a) xn[r * C + c] = gpo_f32_to_bf16(v);
             const float n = gpo_bf16_to_f32(gpo_f32_to_bf16(w[c] * (v * rs)));
             const float sc = gpo_bf16_to_f32(scale[b * ssc + c]), sh = gpo_bf16_to_f32(shift[b * ssh + c]);
-            h[r * C + c] = gpo_f32_to_bf16(n * (1.0f + sc) + sh);
+            h[r * C + c] = gpo_f32_to_bf16(fmaf(n, 1.0f + sc, sh));
         }
     }
 }

@@ -334,7 +334,8 @@ def _oracle_norm(x, a, gate, w, sh, sc, eps):
 def test_norm_against_torch(res, C):
     """x_new equals torch's x + gate * a in fp32 rounded once to bf16 (the reference kernel's, fused_norm.py:82); rstd
     is within 2 fp32 ulp of torch.rsqrt(mean(x_new^2) + eps); h equals torch's n = bf16(w * (x_new * rstd)),
-    bf16(n * (1 + scale) + shift) in fp32 (fused_norm.py:85-89) bit for bit when fed the oracle's rstd."""
+    bf16(n * (1 + scale) + shift) (fused_norm.py:85-89) bit for bit when fed the oracle's rstd, the multiply-add
+    evaluated exactly (float64, exact for these operands) and rounded once to fp32, as a fused multiply-add does."""
     B, N, eps = 3, 40, 1e-6
     x, a, gate, w, sh, sc = _norm_inputs(B, N, C, C + res, res)
     xn, h, rstd = _oracle_norm(x, a, gate, w, sh, sc, eps)
@@ -345,8 +346,27 @@ def test_norm_against_torch(res, C):
     assert np.abs(rstd.astype(np.float64) / rs_t - 1).max() <= 2.5e-7
     r = torch.from_numpy(rstd).view(B, N, 1)
     n = (w * (xs.float() * r)).to(torch.bfloat16).float()
-    ht = (n * (1 + sc.float()) + sh.float()).to(torch.bfloat16)
+    ht = (n.double() * (1 + sc.float()).double() + sh.double()).float().to(torch.bfloat16)
     assert np.array_equal(h, _u16(ht).reshape(-1, C))
+
+
+def test_norm_multiply_add_is_fused():
+    """h's n * (1 + scale) + shift is one fused multiply-add: with scales near 2^-16 (1 + scale then has up to 24
+    significant bits, so the product rounds in fp32) and shift = -1 (cancellation), the oracle equals the exact value
+    rounded once and differs from the separately rounded product and sum. (x + gate * a and the sum of squares take
+    products of bf16 values, exact in fp32, so fusing does not change their bits.)"""
+    B, N, C = 2, 256, 1024
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
+    w = torch.ones(C)
+    sc = (torch.randn(B, 1, C, generator=g) * 2.0 ** -16).to(torch.bfloat16)
+    sh = torch.full((B, 1, C), -1.0).to(torch.bfloat16)
+    _, h, rstd = _oracle_norm(x, None, None, w, sh, sc, 1e-6)
+    n = (w * (x.float() * torch.from_numpy(rstd).view(B, N, 1))).to(torch.bfloat16).float()
+    fused = (n.double() * (1 + sc.float()).double() + sh.double()).float().to(torch.bfloat16)
+    unfused = (n * (1 + sc.float()) + sh.float()).to(torch.bfloat16)
+    assert np.array_equal(h, _u16(fused).reshape(-1, C))
+    assert (h != _u16(unfused).reshape(-1, C)).sum() > 50
 
 
 def test_norm_power_of_two_invariance():
@@ -365,7 +385,7 @@ def test_norm_mutant_unrounded_n_fails():
     _, h, rstd = _oracle_norm(x, None, None, w, sh, sc, 1e-6)
     r = torch.from_numpy(rstd).view(2, 40, 1)
     n_unrounded = w * (x.float() * r)
-    hm = (n_unrounded * (1 + sc.float()) + sh.float()).to(torch.bfloat16)
+    hm = (n_unrounded.double() * (1 + sc.float()).double() + sh.double()).float().to(torch.bfloat16)
     assert not np.array_equal(h, _u16(hm).reshape(-1, 1024))
 
 
