@@ -141,16 +141,18 @@ int gpic_fp8_swiglu_bwd_t(const uint16_t *z, const uint16_t *da, int64_t M, int6
  * The norm sites' producer with the cast of its output folded in. Replaces gpic::res_mod_rmsnorm_fwd
  * (baselines/PixelGen/src/models/layers/fused_norm.py:150-175, kernel :64-91) followed by the FP8 linear's tcast of
  * its output h (fp8_native.py:114-122), as one producer (the reference keeps them apart, fp8_native.py:3-6):
- *   site 2 (a != NULL): x_new = bf16(x + gate * a) -> xn;   site 1 (a == NULL): x_new = x
+ *   site 2 (a != NULL): x_new = bf16(fma(gate, a, x)) -> xn;   site 1 (a == NULL): x_new = x
  *   rstd = 1 / sqrt(sum(x_new^2) / C + eps) -> rstd [rows];  n = bf16(w * (x_new * rstd))
- *   h = bf16(n * (1 + scale) + shift) -> h (when h != NULL), and its tensorwise e4m3 bytes -> hq, dequant (the
+ *   h = bf16(fma(n, 1 + scale, shift)) -> h (when h != NULL), and its tensorwise e4m3 bytes -> hq, dequant (the
  *   tcast rule: amax over the non-NaN values, IEEE scales, saturating round-to-nearest-even)
  *   x, a, xn, h: [rows, C] bf16 (C % 256 == 0, 16-byte aligned); hq [rows, C] e4m3; w [C] fp32 (16-byte aligned)
  *   gate, shift, scale: [B, C] bf16 rows with strides sg, ssh, ssc (multiples of 4, >= C; 8-byte aligned); row r of
  *   x uses row r / ntok of them (rows % ntok == 0)
  * dequant == NULL (then h != NULL, hq unused): the norm alone, as the reference's op (one pass writing h).
- * Every fp32 operation is rounded on its own, and the sum of squares is taken in a fixed order (norm.hip states it);
- * the reference's order and rsqrt are Triton's and libdevice's. Uses the cast workspace (its single-pass partials).
+ * fma is one fused multiply-add (as Triton compiles the reference's expressions on the GPU), every other fp32
+ * operation is rounded on its own, and the sum of squares is taken in a fixed order (norm.hip states it); the
+ * reference's order and rsqrt are Triton's and libdevice's. Uses the cast workspace (its single-pass partials); a
+ * call with both h and dequant runs the two-pass kernels (the single pass does not write h).
  */
 int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_t *gate, int64_t sg, const float *w,
                              const uint16_t *shift, int64_t ssh, const uint16_t *scale, int64_t ssc, int64_t rows,
