@@ -453,15 +453,6 @@ def main():
     sw_ms = time_device(lambda: G.swiglu_tcast(z), 10, 2)
     swb_ms = time_device(lambda: G.swiglu_bwd_q(z, da), 10, 2)
     del z, da
-    # the up projection as the step runs it (the GEMM computing the product in its epilogue) against the GEMM then the
-    # product cast above
-    xu = torch.randn(M_TOK, C, generator=gc, device=dev).to(torch.bfloat16)
-    wu = (torch.randn(2 * H, C, generator=gc, device=dev) * C ** -0.5).to(torch.bfloat16)
-    xuq, sxu = G.tcast(xu)
-    wuq, swu = G.tcast(wu)
-    up_unf_ms = time_device(lambda: G.swiglu_tcast(G.fp8_gemm(xuq, sxu, wuq, swu)), 10, 2)
-    up_fus_ms = time_device(lambda: G.gemm_swiglu_tcast(xuq, sxu, wuq, swu), 10, 2)
-    del xu, wu, xuq, wuq
     w32_bytes = w32.numel() * 5 + 4
     sw_min, sw_moved = M_TOK * H * 5, M_TOK * H * 9               # min: read z, write q; as built: + write a, read a
     swb_min, swb_moved = M_TOK * H * 8, M_TOK * H * 14            # min: read z, da, write dzq; as built: z, da twice
@@ -561,12 +552,7 @@ def main():
                    "bwd_us": round(swb_ms * 1e3, 1) if swb_ms else None, "bwd_min_bytes": swb_min,
                    "bwd_moved_bytes": swb_moved,
                    "bwd_GBs_moved": round(swb_moved / swb_ms / 1e6, 1) if swb_ms else None,
-                   "bwd_frac_min": round(swb_min / swb_ms / 1e6 / PEAK_HBM_GBS, 4) if swb_ms else None,
-                   "up_workload": "w12 up projection with the product cast, x [32768 x 1024] e4m3: fused (the step's "
-                                  "path: the GEMM's epilogue writes the product beside z, then a flat cast) against "
-                                  "fp8_gemm then swiglu_tcast, device time",
-                   "up_fused_us": round(up_fus_ms * 1e3, 1) if up_fus_ms else None,
-                   "up_unfused_us": round(up_unf_ms * 1e3, 1) if up_unf_ms else None},
+                   "bwd_frac_min": round(swb_min / swb_ms / 1e6 / PEAK_HBM_GBS, 4) if swb_ms else None},
         "norm_sites": norm,
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),

@@ -180,26 +180,6 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
                   void *ws, size_t ws_bytes, void *stream);
 
 /*
- * The SwiGLU MLP's up projection with its product cast: replaces _mm (fp8_native.py:175-178) of w12 followed by
- * gpic::fp8_swiglu_tcast (fp8_native.py:130-144, kernels :52-78), as in _Fp8MLP.forward (fp8_native.py:235-245):
- *   z = bf16(sa * sb * A B^T)                         A [M, K] e4m3 (x), B [2H, K] e4m3 (w12: gate rows, then value)
- *   a = bf16(bf16(z1 sigmoid(z1)) z2)                 z1 = z[:, :H], z2 = z[:, H:]; a -> `a` [M, H] bf16 (contiguous)
- *   q, dequant = tcast(a)                             q [M, H] e4m3 (contiguous), the tcast rule
- *   z [M, 2H] bf16, row stride ldz (written: the backward needs it)
- *   H % 128 == 0, K % 16 == 0, lda / ldb % 16 == 0, ldz % 8 == 0; lda, ldb < 2^23, ldz < 2^22, H < 2^21,
- *   2 H ldb < 2^31; any M.
- * The same bits as gpic_fp8_gemm then gpic_fp8_swiglu_tcast: the GEMM's epilogue computes a from each lane's
- * matching z1 and z2 accumulators (a tile takes 128 gate and the same 128 value rows of B) and writes it beside z with
- * each workgroup's largest |a|; a flat cast then reads a once. bf16(z1 sigmoid(z1)) comes from a table of all 65536
- * bf16 values in the library's static device memory (128 KiB per GPU), which every call rewrites (same values) on its
- * stream before its GEMM. ws: the cast workspace (its partial maxima). Three launches on `stream`: the table, the GEMM,
- * the cast.
- */
-int gpic_fp8_gemm_swiglu_tcast(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb,
-                               const float *sb, int64_t M, int64_t H, int64_t K, uint16_t *z, int64_t ldz, uint16_t *a,
-                               uint8_t *q, float *dequant, void *ws, void *stream);
-
-/*
  * Scaled FP8 GEMM with both operands "MN-major" (K is their row index): the weight gradient straight from the
  * untransposed e4m3 bytes of the layer's output gradient and input.
  *   C[m, n] = bf16(sa * sb * sum_k A[k, m] * B[k, n]);  if bias: C[m, n] = bf16(C[m, n] + bias[n])

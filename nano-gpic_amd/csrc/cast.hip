@@ -167,13 +167,21 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(const T *__restrict_
 // r + (kLutELo << 8): the index of a value is then a 16-bit rotate, subtract and clamp, done for both halves of a
 // 32-bit word of bf16 at once with packed 16-bit instructions. The clamp sends values outside the table to entry
 // kLutSize, which the LDS copy holds as -1 (no sigmoid is negative): that marks them for direct computation.
-// (kLutELo, kLutSize: gpic_device.h; ws_table: gpic_launch.h)
+constexpr int kLutELo = 111, kLutEHi = 134;
+constexpr int kLutHalf = (kLutEHi - kLutELo + 1) * 128;
+constexpr int kLutSize = 2 * kLutHalf;
 constexpr int kLutLds = kLutSize + 4;   // LDS copy: the table, the sentinel, padding
 static_assert(kMaxParts * 4 + kLutSize * 4 <= (int)kCastWorkspaceBytes, "cast workspace too small");
 static_assert((kLutELo << 8) + kLutSize <= 0x10000, "table indices are 16-bit");
 
+// The workspace: partial maxima at the start, the sigmoid table after them.
+__host__ __device__ inline float *ws_table(void *ws) { return reinterpret_cast<float *>((char *)ws + kMaxParts * 4); }
+
 __device__ __forceinline__ void lut_build(float *lut) {
-  for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) lut[i] = lut_entry(i);
+  for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) {
+    const uint32_t h = (uint32_t)(i + (kLutELo << 8));        // rotated bits
+    lut[i] = sigmoid(bf16_lo((h >> 1) | ((h & 1u) << 15)));
+  }
   if (threadIdx.x == 0) lut[kLutSize] = -1.0f;
   __syncthreads();
 }
@@ -1185,13 +1193,6 @@ static int scratch_address(hipStream_t st, void **out) {
 
 // SwiGLU kernels: rows strided over at most kSwigluBlocks workgroups (each builds its 24 KiB sigmoid table once).
 static inline int swiglu_grid(int64_t M) { return (int)(M < 1 ? 1 : (M > kSwigluBlocks ? kSwigluBlocks : M)); }
-
-int launch_cast_from_partials(const uint16_t *x, int64_t n, const uint32_t *partial, int nparts, uint8_t *q,
-                              float *dequant, hipStream_t st) {
-  const int gc = n > 0 ? grid_for((n / 16 + kUnroll - 1) / kUnroll, kMaxCastBlocks) : 1;
-  cast_kernel<uint16_t><<<gc, kCastThreads, 0, st>>>(x, n, partial, nparts, q, dequant);
-  return (int)hipGetLastError();
-}
 
 }  // namespace gpic
 

@@ -32,7 +32,6 @@
 //  * Split-K (for the small-output wgrad shapes): each split writes fp32 partials; a second kernel sums them in
 //    split order (deterministic) and applies scale, bias and the bf16 rounding.
 #include <algorithm>
-#include <mutex>
 
 #include "gpic_device.h"
 #include "gpic_launch.h"
@@ -131,22 +130,14 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
 // the transposing ds_read_b64_tr_b8.
 // kBNt: the tile's width, 256 or 128 -- the narrow tile class for shapes whose 256 x 256 tiles leave CUs idle or end
 // on a partial round: each wave then owns 64 x 64 of C, a B K tile is 16 KiB (MN-major: 128 K rows x 128 bytes).
-// The SwiGLU instance (kSw; K-major, wide tile, no split, no bias): C = z = x w12^T [M, N = 2H] with w12 = [gate;
-// value], and beside it y = a = bf16(sl z2) [M, H] (ldy), sl = bf16(z1 sigmoid(z1)) read from `slt` (indexed by z1's
-// bf16 bits), and each workgroup's largest |a| in part[blockIdx.x] (float bits). Tile column block i (32 columns) of
-// tile n0 holds z columns (i & 1) H + n0 / 2 + 32 (i >> 1) + [0, 32): each wave's 4 blocks are z1, z2, z1, z2 of the
-// same 64 hidden units, so a lane holds matching z1 and z2 in acc[2 p][mi] and acc[2 p + 1][mi].
-template <bool kTail, bool kMN, int kBNt, bool kSw = false>
+template <bool kTail, bool kMN, int kBNt>
 __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__restrict__ A, int lda,
                                                             const uint8_t *__restrict__ B, int ldb,
                                                             const float *__restrict__ sa, const float *__restrict__ sb,
                                                             const uint16_t *__restrict__ bias, uint16_t *__restrict__ C,
                                                             int64_t ldc, float *__restrict__ P, int M, int N, int K,
-                                                            int ksplit, int tiles_m, int tiles_n, int splits,
-                                                            uint16_t *__restrict__ Y, int64_t ldy,
-                                                            const uint16_t *__restrict__ slt, uint32_t *__restrict__ part) {
+                                                            int ksplit, int tiles_m, int tiles_n, int splits) {
   static_assert(kBNt == 256 || kBNt == 128, "tile widths: 256 or 128");
-  static_assert(!kSw || (!kMN && kBNt == 256), "the SwiGLU instance: K-major, wide tile");
   constexpr int kWTNt = kBNt / 2;                 // wave tile columns
   constexpr int kTNt = kWTNt / 32;                // 32-column MFMA tiles per wave: 4 or 2
   constexpr int kHalfB = kBNt * kBK;              // one B K tile: 32 or 16 KiB
@@ -213,10 +204,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       w.voB = w.n0 + 16 * mchunkB < N ? baseB : kOOB;
     } else {
       w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
-      if constexpr (kSw)   // rows n0 / 2 + ... of gate and H + n0 / 2 + ... of value (the loads add the block offsets)
-        w.rB = buffer_rsrc(B + (int64_t)(w.n0 / 2) * ldb, (N - w.n0 / 2) * ldb);
-      else
-        w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBNt) * ldb);
+      w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBNt) * ldb);
       w.voA = w.voB = 0;
     }
     return w;
@@ -249,10 +237,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       else lds_dma16(isA ? w.rA : w.rB, k0 + 16 * i + mrow < w.kend ? vo + k0 * ld : kOOB, 0, to);
     } else {
       const int R0 = (i * kLoaders + (wave & 3)) * 8;
-      // (SwiGLU: block i of B from gate / value row (i & 1) H + 32 (i >> 1) past the item's first hidden unit)
-      const int vo = isA ? baseA + i * opaque(32 * lda)
-                   : kSw ? baseB + (i & 1) * opaque((N / 2) * ldb) + (i >> 1) * opaque(32 * ldb)
-                         : baseB + i * opaque(32 * ldb);
+      const int vo = isA ? baseA + i * opaque(32 * lda) : baseB + i * opaque(32 * ldb);
       const uint32_t to = lds_addr(smem) + dst + R0 * kBK;
       if (!kTail || k0 + kBK <= w.kend) lds_dma16(isA ? w.rA : w.rB, vo, k0, to);
       else lds_dma16(isA ? w.rA : w.rB, k0 + kchunk < w.kend ? vo + k0 : kOOB, 0, to);
@@ -378,9 +363,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     } else if (kBNt == 128 || pend == 16) {
       if (two) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    } else if (kSw) {   // 16 stores of z and 8 of a
-      if (two) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
     } else {
       if (two) asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
@@ -393,7 +375,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   Item cur = item(it);
   if (group == 0) send_prologue(cur);
   int pend = 0;   // stores group 0 issued after the current item's prologue loads
-  float amax_a = 0.0f;   // SwiGLU: the largest |a| of this lane's items before a's rounding (maxNum: NaN dropped)
   for (;;) {
     v16f acc[kTNt][kTM];
 #pragma unroll
@@ -445,40 +426,11 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     }
     if (group == 0) phase_barrier();
 
-    // ---- SwiGLU: z rounded to bf16 as the epilogue stores it, packed; acc dies here
-    uint32_t zp[kSw ? kTNt : 1][kSw ? kTM : 1][8];   // SwiGLU: z as the epilogue stores it (packed bf16); acc dies here
-    if constexpr (kSw) {
-#pragma unroll
-      for (int ni = 0; ni < kTNt; ni++)
-#pragma unroll
-        for (int mi = 0; mi < kTM; mi++)
-#pragma unroll
-          for (int j = 0; j < 8; j++) zp[ni][mi][j] = pack_bf16(acc[ni][mi][2 * j] * s, acc[ni][mi][2 * j + 1] * s);
-    }
-
     // ---- the next item's first loads go out now (into A stages 0, 1 and B stage 0: nothing reads them any more),
     // so their latency passes during this item's epilogue
     const int nit = it + gridDim.x;
     const bool more = nit < work;
     if (more && group == 0) send_prologue(item(nit));
-
-    // ---- SwiGLU: sl = bf16(z1 sigmoid(z1)) of every z1 of the lane from the table, issued now and used after z's
-    // staging and stores, so that their latency passes meanwhile. (Waiting for them waits for every vector memory
-    // operation issued before them -- one in-order counter -- and by then the prologue loads above have landed.)
-    uint32_t sl[kSw ? kTM : 1][2][16];
-    if constexpr (kSw) {
-#pragma unroll
-      for (int mi = 0; mi < kTM; mi++)
-#pragma unroll
-        for (int pp = 0; pp < 2; pp++)
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            const uint32_t w1 = zp[2 * pp][mi][j];
-            sl[mi][pp][2 * j] = slt[w1 & 0xffffu];
-            sl[mi][pp][2 * j + 1] = slt[w1 >> 16];
-          }
-      asm volatile("" ::: "memory");   // the reads are issued here (not sunk to their first use)
-    }
 
     // ---- epilogue: acc[ni][mi] lane l holds C[m][n] for m = mi * 32 + (l & 31) and, through col_of,
     // n = ni * 32 + 16 * (r / 8) + 8 * (l >> 5) + r % 8, r = 0..15: two runs of 8 consecutive columns, each one
@@ -489,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const int el = opaque_v(lane);
     const int rows_c = min(M - cur.m0, kBM);
     const int wr = el & 31, wh = el >> 5;
-    if (!kSw && P) {   // split-K fp32 partials
+    if (P) {   // split-K fp32 partials
       const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(P + ((int64_t)cur.split * M + cur.m0) * N), 0, rows_c * N * 4, kBufferFlags);
 #pragma unroll
@@ -524,12 +476,9 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       constexpr int kLPR = kRowB / 16, kRPI = 64 / kLPR;   // read-back: lanes per row, rows per instruction
       auto slot = [](int c, int r) { return kBNt == 256 ? c ^ (r & 15) : c ^ ((r >> 1) & 7); };
       const int rr = (unsigned)el / kLPR, rc = (unsigned)el % kLPR;   // read-back: rows kRPI j + rr, chunk rc
-      // the read-back lane's 8 columns (SwiGLU: tile block 4 wn + rc / 4 is z column block (rc / 4) & 1 of
-      // gate / value at hidden unit n0 / 2 + 32 (2 wn + rc / 8))
-      const int n = kSw ? ((rc >> 2) & 1) * (N / 2) + cur.n0 / 2 + 32 * (2 * wn + (rc >> 3)) + 8 * (rc & 3)
-                        : cur.n0 + wn * kWTNt + 8 * rc;
+      const int n = cur.n0 + wn * kWTNt + 8 * rc;   // the read-back lane's 8 columns
       uint32_t b[4] = {0, 0, 0, 0};
-      if (!kSw && bias && n < N) {
+      if (bias && n < N) {
         const u32x2 b0 = *reinterpret_cast<const u32x2 *>(bias + n), b1 = *reinterpret_cast<const u32x2 *>(bias + n + 4);
         b[0] = b0.x, b[1] = b0.y, b[2] = b1.x, b[3] = b1.y;
       }
@@ -551,8 +500,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
               st16_t w;
 #pragma unroll
               for (int e = 0; e < 4; e++)
-                w[e] = kSw ? zp[kSw ? ni : 0][kSw ? mi : 0][4 * hh + e]
-                           : pack_bf16(v[8 * hh + 2 * e] * s, v[8 * hh + 2 * e + 1] * s);
+                w[e] = pack_bf16(v[8 * hh + 2 * e] * s, v[8 * hh + 2 * e + 1] * s);
               *(GPIC_LDS st16_t *)(cst + wr * kRowB + 16 * slot(4 * ni + 2 * hh + wh, wr)) = w;
             }
           }
@@ -573,7 +521,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
         for (int j = 0; j < kNI; j++) {
           st16_t w = wv[j];
           if (kMN && kRPI * j >= 16) w = st16_t{w[2], w[3], w[0], w[1]};   // rows 16..31: halves exchanged
-          if (!kSw && bias) {   // bf16(bf16(acc * s) + bias)
+          if (bias) {   // bf16(bf16(acc * s) + bias)
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));
           }
@@ -583,62 +531,10 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
         }
       }
       pend = kStoresBF16;
-      if constexpr (kSw) {   // a: each lane's two runs of 8 per (mi, pair), 16 bytes each, straight from registers
-        // sl is used from here on, after z's stores (the compiler would otherwise start on a among them and wait for
-        // the table reads there)
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int mi = 0; mi < kTM; mi++)
-#pragma unroll
-          for (int pp = 0; pp < 2; pp++)
-#pragma unroll
-            for (int j = 0; j < 16; j++) asm volatile("" : "+v"(sl[mi][pp][j]));
-        // a = bf16(sl z2). The largest |a| is taken on the fp32 products before their rounding and rounded once at the
-        // end: rounding is monotonic, so it is the largest |bf16 a|, at one instruction per element.
-        uint32_t aw[kTM][2][8];
-#pragma unroll
-        for (int mi = 0; mi < kTM; mi++)
-#pragma unroll
-          for (int pp = 0; pp < 2; pp++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-              const uint32_t w2 = zp[2 * pp + 1][mi][j];
-              const float p0 = __uint_as_float(sl[mi][pp][2 * j] << 16) * bf16_lo(w2);
-              const float p1 = __uint_as_float(sl[mi][pp][2 * j + 1] << 16) * bf16_hi(w2);
-              aw[mi][pp][j] = pack_bf16(p0, p1);
-              amax_a = fmaxf(amax_a, fmaxf(fabsf(p0), fabsf(p1)));
-            }
-        const __amdgpu_buffer_rsrc_t rY = __builtin_amdgcn_make_buffer_rsrc((void *)(Y + (int64_t)cur.m0 * ldy), 0,
-                                                                            rows_c * (int)ldy * 2, kBufferFlags);
-#pragma unroll
-        for (int mi = 0; mi < kTM; mi++)
-#pragma unroll
-          for (int pp = 0; pp < 2; pp++)
-#pragma unroll
-            for (int q = 0; q < 2; q++) {
-              const int r = wm * kWTM + mi * 32 + wr;
-              const int col = cur.n0 / 2 + 32 * (2 * wn + pp) + 16 * q + 8 * wh;
-              const u32x4 w{aw[mi][pp][4 * q], aw[mi][pp][4 * q + 1], aw[mi][pp][4 * q + 2], aw[mi][pp][4 * q + 3]};
-              __builtin_amdgcn_raw_buffer_store_b128(w, rY, r < rows_c ? (r * (int)ldy + col) * 2 : kOOB, 0, 0);
-            }
-        pend = kStoresBF16 + 8;
-      }
     }
     if (!more) break;
     it = nit;
     cur = item(opaque(nit));   // recomputed rather than kept live through the epilogue
-  }
-  if constexpr (kSw) {   // the workgroup's largest |a| (every wave is done with the LDS: its read-backs were waited for)
-    const uint32_t m = wave_max_u32(__float_as_uint(bf16_round(amax_a)));   // (non-negative: ordered as integers)
-    lds_barrier();
-    if (lane == 0) ((GPIC_LDS uint32_t *)smem)[wave] = m;
-    lds_barrier();
-    if (threadIdx.x == 0) {
-      uint32_t g = 0;
-#pragma unroll
-      for (int w = 0; w < kThreads / 64; w++) g = max(g, ((const GPIC_LDS uint32_t *)smem)[w]);
-      part[blockIdx.x] = g;
-    }
   }
 }
 
@@ -752,62 +648,13 @@ static int launch_gemm(const uint8_t *A, int64_t lda, const float *sa, const uin
                               : (K % kBK ? gemm_tn_kernel<true, kMN, 256> : gemm_tn_kernel<false, kMN, 256>);
   kernel<<<grid, kThreads, 0, st>>>(
       A, (int)lda, B, (int)ldb, sa, sb, bias, C, ldc, P, (int)M, (int)N, (int)K, p.ksplit, p.tiles_m, p.tiles_n,
-      p.splits, nullptr, 0, nullptr, nullptr);
+      p.splits);
   if (P) {
     const int64_t quads = M * (N / 4);
     int64_t g = (quads + 255) / 256;
     if (g > 8192) g = 8192;
     splitk_reduce_kernel<<<(int)g, 256, 0, st>>>(P, p.splits, (int)M, (int)N, sa, sb, bias, C, ldc);
   }
-  return (int)hipGetLastError();
-}
-
-// sl = bf16(z sigmoid(z)) for each of the 65536 bf16 values z (index: z's bits), the SwiGLU instance's table: 128 KiB
-// of static device memory per GPU. Every call writes it on its own stream before its GEMM (the same values each
-// time, so calls on other streams that read it meanwhile read the same bits), so no call depends on another's fill.
-static __device__ __align__(256) uint16_t sl_table[65536];
-static std::mutex g_sl_mu;
-static void *g_sl_ptr[kMaxDevices];
-
-__global__ __launch_bounds__(256) void sl_table_kernel(uint16_t *__restrict__ t) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const float z = bf16_lo((uint32_t)i);
-  t[i] = (uint16_t)bf16_rne(z * sigmoid(z));
-}
-
-static int sl_table_address(void **out) {
-  const int dev = current_device();
-  if (dev < 0 || dev >= kMaxDevices) return GPIC_EINVAL;
-  std::lock_guard<std::mutex> lock(g_sl_mu);
-  if (!g_sl_ptr[dev]) {
-    void *ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(sl_table));
-    if (e != hipSuccess) return (int)e;
-    if (!ptr) return GPIC_EINVAL;
-    g_sl_ptr[dev] = ptr;
-  }
-  *out = g_sl_ptr[dev];
-  return GPIC_OK;
-}
-
-// The SwiGLU launch: one wide tile per 128 hidden units, no split (the epilogue needs whole z), a persistent grid as
-// above, whose workgroups each leave one partial maximum of |a| in the cast workspace.
-static int launch_gemm_swiglu(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb,
-                              const float *sb, uint16_t *z, int64_t ldz, uint16_t *a, int64_t M, int64_t H, int64_t K,
-                              void *ws, hipStream_t st, int *nparts) {
-  const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (2 * H) / kBN;
-  const int work = (int)(tiles_m * tiles_n);
-  const int slots = num_cus() & ~7;
-  const int grid = work <= slots || slots < 8 ? work : slots;
-  *nparts = grid;
-  void *slt = nullptr;
-  int rc = sl_table_address(&slt);
-  if (rc) return rc;
-  sl_table_kernel<<<65536 / 256, 256, 0, st>>>(static_cast<uint16_t *>(slt));
-  auto *kernel = K % kBK ? gemm_tn_kernel<true, false, 256, true> : gemm_tn_kernel<false, false, 256, true>;
-  kernel<<<grid, kThreads, 0, st>>>(A, (int)lda, B, (int)ldb, sa, sb, nullptr, z, ldz, nullptr, (int)M, (int)(2 * H),
-                                    (int)K, (int)(std::max<int64_t>((K + kBK - 1) / kBK, 1) * kBK), (int)tiles_m,
-                                    (int)tiles_n, 1, a, H, static_cast<const uint16_t *>(slt), static_cast<uint32_t *>(ws));
   return (int)hipGetLastError();
 }
 
@@ -833,29 +680,6 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
   if (lda < K || ldb < K || ldc < N || lda >= (1 << 23) || ldb >= (1 << 23) || ldc >= (1 << 22) || M >= (1 << 30))
     return GPIC_ESHAPE;
   return launch_gemm<false>(A, lda, sa, B, ldb, sb, bias, C, ldc, M, N, K, ws, ws_bytes, (hipStream_t)stream);
-}
-
-int gpic_fp8_gemm_swiglu_tcast(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb,
-                               const float *sb, int64_t M, int64_t H, int64_t K, uint16_t *z, int64_t ldz, uint16_t *a,
-                               uint8_t *q, float *dequant, void *ws, void *stream) {
-  if (M < 0 || H < 0 || K < 0 || !sa || !sb || !dequant || !ws || (M > 0 && H > 0 && (!z || !a || !q)) ||
-      (M > 0 && H > 0 && K > 0 && (!A || !B)))
-    return GPIC_EINVAL;
-  if (H % 128 != 0 || K % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldz % 8 != 0) return GPIC_ESHAPE;
-  // 32-bit buffer offsets: z's and a's rows within a tile (ldz, H < 2^22), B's rows from a tile's first hidden unit
-  if (lda < K || ldb < K || ldz < 2 * H || lda >= (1 << 23) || ldb >= (1 << 23) || ldz >= (1 << 22) ||
-      H >= (1 << 21) || 2 * H * ldb >= (int64_t(1) << 31) || M >= (1 << 30))
-    return GPIC_ESHAPE;
-  if (!aligned16(A) || !aligned16(B) || !aligned16(z) || !aligned16(a) || !aligned16(q) || !aligned16(ws))
-    return GPIC_EALIGN;
-  hipStream_t st = (hipStream_t)stream;
-  const uint32_t *partial = static_cast<const uint32_t *>(ws);
-  if (M == 0 || H == 0)   // nothing but the scale of an empty tensor
-    return launch_cast_from_partials(nullptr, 0, partial, 0, nullptr, dequant, st);
-  int nparts = 0;
-  int rc = launch_gemm_swiglu(A, lda, sa, B, ldb, sb, z, ldz, a, M, H, K, ws, st, &nparts);
-  if (rc) return rc;
-  return launch_cast_from_partials(a, M * H, partial, nparts, q, dequant, st);
 }
 
 int gpic_fp8_gemm_mn(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,

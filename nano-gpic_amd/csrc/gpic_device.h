@@ -111,19 +111,6 @@ __device__ __forceinline__ float exp_cw(float t) {
 
 __device__ __forceinline__ float sigmoid(float x) { return __fdiv_rn(1.0f, 1.0f + exp_cw(-x)); }
 
-// The SwiGLU kernels' sigmoid table: sigmoid() of the bf16 values with exponent field in [kLutELo, kLutEHi]
-// (2^-16 <= |z1| < 2^8), both signs, 6144 floats. Entry r holds the value whose bf16 bits, rotated left by one (sign
-// to bit 0), are r + (kLutELo << 8); other values (tiny, huge, zero, NaN) are computed directly.
-constexpr int kLutELo = 111, kLutEHi = 134;
-constexpr int kLutHalf = (kLutEHi - kLutELo + 1) * 128;
-constexpr int kLutSize = 2 * kLutHalf;
-
-// The value of entry r (the same sigmoid() as every other use).
-__device__ __forceinline__ float lut_entry(int r) {
-  const uint32_t h = (uint32_t)(r + (kLutELo << 8));   // rotated bits
-  return sigmoid(__uint_as_float(((h >> 1) | ((h & 1u) << 15)) << 16));
-}
-
 // ------------------------------------------------------------------------------------------- reductions
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {

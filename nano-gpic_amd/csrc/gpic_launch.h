@@ -22,14 +22,6 @@ constexpr size_t kCastWorkspaceBytes = 44 * 1024;     // partial maxima (4 KiB),
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// The cast workspace: partial maxima at the start (kMaxParts words), the SwiGLU sigmoid table after them.
-__host__ __device__ inline float *ws_table(void *ws) { return reinterpret_cast<float *>((char *)ws + kMaxParts * 4); }
-
-// The launcher of cast.hip used by the GEMM's SwiGLU entry point: the flat cast of n bf16 values whose amax is the
-// maximum of `nparts` partial maxima (float bits).
-int launch_cast_from_partials(const uint16_t *x, int64_t n, const uint32_t *partial, int nparts, uint8_t *q,
-                              float *dequant, hipStream_t st);
-
 // Device attributes the launches depend on, cached per device: each GPU of the process gets its own entry (the
 // library may run on several), and a cache slot is written whole by whichever thread computes it first (all compute
 // the same value). Devices past kMaxDevices are queried on every call.

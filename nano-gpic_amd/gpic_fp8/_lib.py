@@ -36,8 +36,6 @@ SIGNATURES = {
     "gpic_fp8_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "gpic_fp8_gemm": (_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
     "gpic_fp8_gemm_mn": (_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
-    "gpic_fp8_gemm_swiglu_tcast": (_int, [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
-                                           _vp, _vp]),
 }
 
 DTYPE_CODE = {torch.bfloat16: 0, torch.float32: 1}

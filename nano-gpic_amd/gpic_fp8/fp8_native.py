@@ -287,54 +287,6 @@ def _(a, sa, b, sb, bias=None, fast=True):
     return a.new_empty(a.shape[0], b.shape[0], dtype=torch.bfloat16)
 
 
-@torch.library.custom_op("gpic::fp8_gemm_swiglu_tcast", mutates_args=())
-def gemm_swiglu_tcast(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor,
-                      sb: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """The SwiGLU MLP's up projection and its product cast in one: z = fp8_gemm(a, sa, b, sb) [M, 2H] for b = w12's
-    e4m3 bytes [2H, K] (gate rows, then value rows), and (q, s) = swiglu_tcast(z) -- the same bits as the two ops
-    (fp8_native.py:175-178 then :130-144), but the GEMM's epilogue computes the product from z while z is still in
-    registers and writes it (bf16) beside z with its partial maxima, so z is not read again. Needs H % 128 == 0."""
-    L.require_gpu(a, b, sa, sb)
-    a = _gemm_operand(a, "a")
-    b = _gemm_operand(b, "b")
-    M, K = a.shape
-    N = b.shape[0]
-    if b.shape[1] != K or N % 256 or K % 16:
-        raise ValueError(f"gemm_swiglu_tcast needs a [M, K], b [2H, K] with H % 128 == 0 and K % 16 == 0, got "
-                         f"{tuple(a.shape)} and {tuple(b.shape)}")
-    H = N // 2
-    sa = sa.to(torch.float32).reshape(1)
-    sb = sb.to(torch.float32).reshape(1)
-    z = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
-    y = torch.empty(M, H, dtype=torch.bfloat16, device=a.device)
-    q = torch.empty(M, H, dtype=E4, device=a.device)
-    s = torch.empty(1, dtype=torch.float32, device=a.device)
-    with torch.cuda.device(a.device):
-        ws = L.cast_workspace(a.device)
-        L.check(L.lib().gpic_fp8_gemm_swiglu_tcast(a.data_ptr(), a.stride(0), sa.data_ptr(), b.data_ptr(), b.stride(0),
-                                                   sb.data_ptr(), M, H, K, z.data_ptr(), z.stride(0), y.data_ptr(),
-                                                   q.data_ptr(), s.data_ptr(), ws.data_ptr(), L.stream_ptr(a.device)),
-                "gpic_fp8_gemm_swiglu_tcast")
-    return z, q, s
-
-
-@gemm_swiglu_tcast.register_fake
-def _(a, sa, b, sb):
-    M, H = a.shape[0], b.shape[0] // 2
-    return (a.new_empty(M, 2 * H, dtype=torch.bfloat16), a.new_empty(M, H, dtype=E4),
-            a.new_empty(1, dtype=torch.float32))
-
-
-def _up_swiglu(xq, sx, w12q, s12):
-    """z = x w12^T and the e4m3 SwiGLU product (aq, sa): one fused op when w12 has 2H rows with H % 128 == 0 (the
-    GEMM computes the product in its epilogue), else the GEMM then swiglu_tcast -- the same bits either way."""
-    if w12q.shape[0] % 256 == 0 and xq.shape[1] % 16 == 0:
-        return gemm_swiglu_tcast(xq, sx, w12q, s12)
-    z = fp8_gemm(xq, sx, w12q, s12)
-    aq, sa = swiglu_tcast(z)
-    return z, aq, sa
-
-
 def _gemm_operand_mn(t, name):
     if t.dtype != E4 or t.dim() != 2:
         raise ValueError(f"{name} must be a 2-D float8_e4m3fn tensor, got {t.dtype} {tuple(t.shape)}")
@@ -484,7 +436,8 @@ class _Fp8MLP(torch.autograd.Function):
         x2 = x.reshape(-1, shape[-1])
         xq, sx = tcast(x2)
         w12q, s12 = tcast(w12)
-        z, aq, sa = _up_swiglu(xq, sx, w12q, s12)
+        z = _mm(xq, sx, w12q, s12)
+        aq, sa = swiglu_tcast(z)
         w3q, s3 = tcast(w3)
         y = _mm(aq, sa, w3q, s3)
         ctx.save_for_backward(x2, z, aq, sa, w12, w3)
@@ -516,7 +469,8 @@ class _Fp8MLPF8(torch.autograd.Function):
         x2 = x.reshape(-1, shape[-1])
         xq, sx = tcast(x2)
         w12q, w12qt, s12 = tcast_t(w12)
-        z, aq, sa = _up_swiglu(xq, sx, w12q, s12)
+        z = fp8_gemm(xq, sx, w12q, s12)
+        aq, sa = swiglu_tcast(z)
         w3q, w3qt, s3 = tcast_t(w3)
         y = fp8_gemm(aq, sa, w3q, s3)
         ctx.save_for_backward(xq, sx, z, aq, sa, w12qt, s12, w3qt, s3)

@@ -104,16 +104,6 @@ def test_validation_codes():
     assert mn(wsp + 8, 32, wsp, wsp, 32, wsp, None, wsp, 32, 32, 32, 5, None, 0, None) == -4
     assert mn(None, 32, wsp, None, 32, wsp, None, None, 32, 0, 32, 5, None, 0, None) == 0
     assert mn(wsp, 32, wsp, wsp, 32, wsp, None, wsp, 1 << 22, 32, 32, 5, None, 0, None) == -3
-    # the up projection with its SwiGLU product cast: H % 128, ldz >= 2H and < 2^22, K % 16, nulls, alignment
-    sw = lib.gpic_fp8_gemm_swiglu_tcast
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 64, 32, wsp, 128, wsp, wsp, wsp, wsp, None) == -3
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 128, 32, wsp, 128, wsp, wsp, wsp, wsp, None) == -3
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 128, 24, wsp, 256, wsp, wsp, wsp, wsp, None) == -3
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 128, 32, wsp, 1 << 22, wsp, wsp, wsp, wsp, None) == -3
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 128, 32, wsp, 256, None, wsp, wsp, wsp, None) == -1
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 128, 32, wsp, 256, wsp, wsp, None, wsp, None) == -1
-    assert sw(wsp, 32, wsp, wsp, 32, wsp, 4, 128, 32, wsp, 256, wsp, wsp, wsp, None, None) == -1
-    assert sw(wsp, 32, wsp, wsp + 8, 32, wsp, 4, 128, 32, wsp, 256, wsp, wsp, wsp, wsp, None) == -4
 
 
 def test_single_pass_knob_is_host_only():
