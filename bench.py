@@ -242,6 +242,47 @@ def norm_sites(G, dev, B=128, N=256, eps=1e-6):
     return out
 
 
+def norm_block(G, dev, B=128, N=256, eps=1e-6, steps=20):
+    """The d12 block's two norm sites with the FP8 linears they feed, fwd + bwd over 32768 tokens (site 1 -> qkv_x,
+    site 2 -> the SwiGLU MLP; every GEMM FP8): fused (the norm kernel writes h's e4m3 bytes, h never exists in bf16:
+    fp8_mod_rmsnorm_linear, fp8_res_mod_rmsnorm_mlp) against unfused (mod_rmsnorm / res_mod_rmsnorm write bf16 h,
+    then fp8_linear_f8 / fp8_mlp_f8 cast it). Both give the same bits; ms per step, alternating runs."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(12)
+
+    def bf(*shape, std=1.0, grad=True):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(grad)
+
+    x, a = bf(B, N, C), bf(B, N, C)
+    mod = bf(B, 1, 6 * C, std=0.2)
+    wn1 = (1 + 0.1 * torch.randn(C, generator=g, device=dev)).requires_grad_()
+    wn2 = (1 + 0.1 * torch.randn(C, generator=g, device=dev)).requires_grad_()
+    wqkv, w12, w3 = bf(3 * C, C, std=C ** -0.5), bf(2 * H, C, std=C ** -0.5), bf(C, H, std=H ** -0.5)
+    dy1, dy3, dxn = bf(B, N, 3 * C, std=0.1, grad=False), bf(B, N, C, std=0.1, grad=False), \
+        bf(B, N, C, std=0.1, grad=False)
+
+    def run(fused):
+        sh1, sc1, sh2, sc2, g2 = (mod[..., i * C:(i + 1) * C] for i in range(5))
+        if fused:
+            y1 = G.fp8_mod_rmsnorm_linear(x, wn1, sh1, sc1, eps, wqkv)
+            xn, y3 = G.fp8_res_mod_rmsnorm_mlp(x, a, g2, wn2, sh2, sc2, eps, w12, w3)
+        else:
+            y1 = G.fp8_linear_f8(G.mod_rmsnorm(x, wn1, sh1, sc1, eps), wqkv)
+            xn, h2 = G.res_mod_rmsnorm(x, a, g2, wn2, sh2, sc2, eps)
+            y3 = G.fp8_mlp_f8(h2, w12, w3)
+        torch.autograd.backward([y1, xn, y3], [dy1, dxn, dy3])
+
+    t = {"fused": [], "unfused": []}
+    for _ in range(2):
+        for k in ("fused", "unfused"):
+            t[k].append(time_region(lambda: run(k == "fused"), steps, 3))
+    f, u = min(t["fused"]), min(t["unfused"])
+    return {"workload": f"d12 block: both norm sites and the FP8 linears they feed (qkv_x, SwiGLU MLP), fwd + bwd over "
+                        f"{B * N} tokens; fused: the norm kernels write h's e4m3 bytes; unfused: bf16 h, then the "
+                        f"linears cast it (ms per step, best of 2 alternating runs of {steps})",
+            "fused_ms": round(f, 4), "unfused_ms": round(u, 4), "saved_us": round((u - f) * 1e3, 1)}
+
+
 def gemm_source_sha():
     import hashlib
     with open(os.path.join(ROOT, "nano-gpic_amd", "csrc", "gemm.hip"), "rb") as f:
@@ -304,7 +345,7 @@ def cpu_baseline(runs=5, sample_tokens=8192):
     threads = cpu_threads()
     torch.set_num_threads(threads)
 
-    g = torch.Generator().manual_seed(0)                    # config 1 (SURVEY 8d): X [4096 x 768], W [768 x 768]
+    g = torch.Generator().manual_seed(0)                    # config 1: X [4096 x 768], W [768 x 768]
     X = torch.randn(4096, 768, generator=g).to(torch.bfloat16)
     W = (torch.randn(768, 768, generator=g) / 768 ** 0.5).to(torch.bfloat16)
 
@@ -461,6 +502,7 @@ def main():
     # * a, RMSNorm + modulation -> the MLP) at d12, h's e4m3 bytes from the norm kernel (fused) against the norm
     # writing bf16 h and tcast(h) reading it back (unfused), device time
     norm = norm_sites(G, dev)
+    nblock = norm_block(G, dev)
 
     # ---- config 5: the d18 block (C = 1792, H = 7168) with 1% outlier activation channels, fwd + bwd
     C18, H18 = 1792, 7168
@@ -554,6 +596,7 @@ def main():
                    "bwd_GBs_moved": round(swb_moved / swb_ms / 1e6, 1) if swb_ms else None,
                    "bwd_frac_min": round(swb_min / swb_ms / 1e6 / PEAK_HBM_GBS, 4) if swb_ms else None},
         "norm_sites": norm,
+        "norm_block": nblock,
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
                       "tflops": round(fl18 / ms18 / 1e9, 1)},

@@ -159,6 +159,26 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
                              int64_t ntok, int64_t C, float eps, uint16_t *xn, uint16_t *h, float *rstd, uint8_t *hq,
                              float *dequant, void *ws, void *stream);
 
+/*
+ * The norm sites' backward. Replaces gpic::res_mod_rmsnorm_bwd (fused_norm.py:249-275, kernel :94-147) with its
+ * column sums done on the device in a fixed order (the reference adds its partials with torch.sum):
+ *   t = xs * rstd, n = bf16(w t), dn = dh (1 + scale), dt = dn w, mean = sum_row(dt t) / C
+ *   dx = bf16(rstd (dt - t mean) + dxn);   site 2 (a != NULL): da = bf16(dx_fp32 gate)
+ *   d_shift[b] = sum dh, d_scale[b] = sum dh n, d_gate[b] = sum dx_fp32 a  (over the rows of batch b)  [B, C] fp32
+ *   d_w = sum dn t (over all rows)  [C] fp32
+ *   dh, dxn, xs (x_new at site 2, x at site 1), a, dx, da: [rows, C] bf16 (16-byte aligned); dxn may be NULL at site 2
+ *   and must be NULL at site 1 (as gate, d_gate); gate, scale: [B, C] bf16 rows (strides sg, ssc); w [C] fp32;
+ *   rstd [rows] fp32 (the forward's); C % 256 == 0, C <= 2048, rows % ntok == 0.
+ *   ws: gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes(rows, ntok, C) bytes (the partial column sums).
+ * Deterministic: every sum is taken in a fixed order.
+ */
+size_t gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t ntok, int64_t C);
+int gpic_fp8_res_mod_rmsnorm_bwd(const uint16_t *dh, const uint16_t *dxn, const uint16_t *xs, const uint16_t *a,
+                                 const uint16_t *gate, int64_t sg, const float *w, const uint16_t *scale, int64_t ssc,
+                                 const float *rstd, int64_t rows, int64_t ntok, int64_t C, uint16_t *dx, uint16_t *da,
+                                 float *dshift, float *dscale, float *dgate, float *dw, void *ws, size_t ws_bytes,
+                                 void *stream);
+
 /* Bytes of workspace gpic_fp8_gemm needs for this problem (0 when it runs without split-K). */
 size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 

@@ -372,6 +372,234 @@ static bool launch_norm_once(const NormArgs &p, void *ws, hipStream_t st) {
   return uni ? launch_norm_once_t<kJ, true, false>(p, ws, st) : launch_norm_once_t<kJ, false, false>(p, ws, st);
 }
 
+
+// ------------------------------------------------------------------------------------------- backward
+
+// The norm sites' backward (fused_norm.py:94-147): for each row, with t = xs * rstd (xs = x_new at site 2, x at
+// site 1), n = bf16(w t), dn = dh (1 + scale), dt = dn w, mean = sum(dt t) / C:
+//   dx = rstd (dt - t mean) (+ dxn at site 2)   -> bf16 dx;   site 2: da = bf16(dx gate)
+// and the column sums d_shift[b] = sum dh, d_scale[b] = sum dh n, d_gate[b] = sum dx a (over the rows of batch b),
+// d_w = sum dn t (over all rows), in fp32. A workgroup takes kBwdRows consecutive rows of one batch, one wave per row
+// (lane l: elements 4 (l + 64 j) + e, as the forward); each wave keeps its column sums in registers, the four waves
+// add theirs in LDS in wave order, and the workgroup writes one partial row per sum; norm_bwd_reduce_kernel then adds
+// the partials in workgroup order. Every sum has a fixed order: the gradients are deterministic.
+constexpr int kBwdRows = 64;   // rows per workgroup (16 per wave)
+
+struct NormBwdArgs {
+  const uint16_t *dh, *dxn, *xs, *a, *gate;   // dxn, a, gate: site 2 only (else null)
+  const float *w;
+  const uint16_t *scale;
+  const float *rstd;
+  uint16_t *dx, *da;
+  float *part;                                // [4][P][C]: shift, scale, w, gate partials
+  int64_t rows, ntok, sg, ssc;
+  int C, tiles_b, P;
+};
+
+template <int kJ, bool kRes, bool kDxn>
+__global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pid = blockIdx.x;
+  const int64_t b = pid / p.tiles_b, tile = pid % p.tiles_b;
+  const int64_t r0 = tile * kBwdRows, rend = min<int64_t>(p.ntok, r0 + kBwdRows);   // token range in batch b
+  const int64_t C = p.C;
+  // the columns' w (fp32) and scale, gate (packed bf16: fewer registers, unpacked where used)
+  float w4[kJ][4];
+  u32x2 SC[kJ], GT[kJ];
+#pragma unroll
+  for (int j = 0; j < kJ; j++) {
+    const int c = 4 * (lane + 64 * j);
+    const float4 wv = *reinterpret_cast<const float4 *>(p.w + c);
+    w4[j][0] = wv.x, w4[j][1] = wv.y, w4[j][2] = wv.z, w4[j][3] = wv.w;
+    SC[j] = ld8(p.scale + b * p.ssc + c);
+    if (kRes) GT[j] = ld8(p.gate + b * p.sg + c);
+  }
+  float ash[kJ][4], asc[kJ][4], aw[kJ][4], ag[kJ][4];
+#pragma unroll
+  for (int j = 0; j < kJ; j++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) ash[j][e] = asc[j][e] = aw[j][e] = ag[j][e] = 0.0f;
+  // A row's loads (packed bf16), issued one row ahead: the next row's are in flight while this one is computed.
+  constexpr int kPre = kJ <= 4 ? 1 : 0;
+  u32x2 DH[2][kJ], XS[2][kJ], AV[2][kJ], DX[2][kJ];
+  auto load_row = [&](int buf, int64_t r) {
+    const int64_t row = b * p.ntok + r;
+#pragma unroll
+    for (int j = 0; j < kJ; j++) {
+      const int64_t o = row * C + 4 * (lane + 64 * j);
+      DH[buf][j] = ld8(p.dh + o);
+      XS[buf][j] = ld8(p.xs + o);
+      if (kRes) AV[buf][j] = ld8(p.a + o);
+      if (kDxn) DX[buf][j] = ld8(p.dxn + o);
+    }
+  };
+  auto do_row = [&](int buf, int64_t r) {
+    // (scale and gate stay packed: the compiler would otherwise unpack them once, out of the row loop, into twice the
+    // registers)
+#pragma unroll
+    for (int j = 0; j < kJ; j++) {
+      asm volatile("" : "+v"(SC[j]));
+      if (kRes) asm volatile("" : "+v"(GT[j]));
+    }
+    const int64_t row = b * p.ntok + r;
+    const float rs = p.rstd[row];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kJ; j++) {
+      float dh[4], x[4], sc[4];
+      unpack4(DH[buf][j], dh);
+      unpack4(XS[buf][j], x);
+      unpack4(SC[j], sc);
+      const u32x2 nw{pack_bf16(w4[j][0] * (x[0] * rs), w4[j][1] * (x[1] * rs)),
+                     pack_bf16(w4[j][2] * (x[2] * rs), w4[j][3] * (x[3] * rs))};
+      float n[4];
+      unpack4(nw, n);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float t = x[e] * rs;
+        ash[j][e] = ash[j][e] + dh[e];
+        asc[j][e] = __builtin_fmaf(dh[e], n[e], asc[j][e]);
+        const float dn = dh[e] * (1.0f + sc[e]);
+        aw[j][e] = __builtin_fmaf(dn, t, aw[j][e]);
+        s = __builtin_fmaf(dn * w4[j][e], t, s);
+      }
+    }
+    const float mean = __fdiv_rn(wave_sum_butterfly(s), (float)p.C);
+#pragma unroll
+    for (int j = 0; j < kJ; j++) {   // t and dt again from the packed row (fewer registers than keeping them)
+      const int c = 4 * (lane + 64 * j);
+      float dh[4], x[4], sc[4], dx[4];
+      unpack4(DH[buf][j], dh);
+      unpack4(XS[buf][j], x);
+      unpack4(SC[j], sc);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float t = x[e] * rs;
+        const float dt = (dh[e] * (1.0f + sc[e])) * w4[j][e];
+        dx[e] = rs * (dt - t * mean);
+      }
+      if (kDxn) {
+        float d[4];
+        unpack4(DX[buf][j], d);
+#pragma unroll
+        for (int e = 0; e < 4; e++) dx[e] = dx[e] + d[e];
+      }
+      if (kRes) {
+        float av[4], g[4];
+        unpack4(AV[buf][j], av);
+        unpack4(GT[j], g);
+#pragma unroll
+        for (int e = 0; e < 4; e++) ag[j][e] = __builtin_fmaf(dx[e], av[e], ag[j][e]);
+        *reinterpret_cast<u32x2 *>(p.da + row * C + c) =
+            u32x2{pack_bf16(dx[0] * g[0], dx[1] * g[1]), pack_bf16(dx[2] * g[2], dx[3] * g[3])};
+      }
+      *reinterpret_cast<u32x2 *>(p.dx + row * C + c) = u32x2{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3])};
+    }
+  };
+  int64_t r = r0 + wave;
+  if (kPre) {
+    if (r < rend) load_row(0, r);
+    for (; r < rend; r += 8) {   // rows r (buffer 0) and r + 4 (buffer 1)
+      if (r + 4 < rend) load_row(1, r + 4);
+      do_row(0, r);
+      if (r + 4 >= rend) break;
+      if (r + 8 < rend) load_row(0, r + 8);
+      do_row(1, r + 4);
+    }
+  } else {
+    for (; r < rend; r += 4) {
+      load_row(0, r);
+      do_row(0, r);
+    }
+  }
+  // the four waves' column sums added in LDS in wave order, then one partial row per sum
+  extern __shared__ float red[];   // [4 waves][kNS sums][C]
+  constexpr int kNS = kRes ? 4 : 3;
+#pragma unroll
+  for (int j = 0; j < kJ; j++) {
+    const int c = 4 * (lane + 64 * j);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      red[(wave * kNS + 0) * C + c + e] = ash[j][e];
+      red[(wave * kNS + 1) * C + c + e] = asc[j][e];
+      red[(wave * kNS + 2) * C + c + e] = aw[j][e];
+      if (kRes) red[(wave * kNS + 3) * C + c + e] = ag[j][e];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kNS * C; i += 256) {
+    const int k = i / (int)C, c = i % (int)C;
+    float v = red[(0 * kNS + k) * C + c];
+#pragma unroll
+    for (int wv = 1; wv < 4; wv++) v = v + red[(wv * kNS + k) * C + c];
+    p.part[((int64_t)k * p.P + pid) * C + c] = v;
+  }
+}
+
+// The partials added in a fixed order. Workgroups [0, nbc): d_shift, d_scale, d_gate [B, C] over the tiles of each
+// batch, one thread per (batch, column). The next ceil(C / 16) workgroups: d_w [C] over all P partials, 16 columns
+// per workgroup: thread (k, c) adds partials [k P / 16, (k + 1) P / 16) of column c, then the 16 chunk sums of a
+// column are added in chunk order (a single thread per column would wait on P dependent loads).
+__global__ __launch_bounds__(256) void norm_bwd_reduce_kernel(const float *__restrict__ part, int P, int tiles_b, int B,
+                                                              int C, bool res, float *__restrict__ dsh,
+                                                              float *__restrict__ dsc, float *__restrict__ dg,
+                                                              float *__restrict__ dw) {
+  const int64_t nbc = (int64_t)B * C;
+  const int64_t wg_bc = (nbc + 255) / 256;
+  if (blockIdx.x < wg_bc) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nbc) return;
+    const int64_t bb = i / C, c = i % C;
+    float s0 = 0.0f, s1 = 0.0f, s3 = 0.0f;
+    for (int t = 0; t < tiles_b; t++) {
+      const int64_t prow = bb * tiles_b + t;
+      s0 = s0 + part[(0 * (int64_t)P + prow) * C + c];
+      s1 = s1 + part[(1 * (int64_t)P + prow) * C + c];
+      if (res) s3 = s3 + part[(3 * (int64_t)P + prow) * C + c];
+    }
+    dsh[i] = s0;
+    dsc[i] = s1;
+    if (res) dg[i] = s3;
+    return;
+  }
+  __shared__ float chunk[16][16];
+  const int cl = threadIdx.x & 15, k = threadIdx.x >> 4;
+  const int c = (int)(blockIdx.x - wg_bc) * 16 + cl;
+  const int per = (P + 15) / 16, q0 = k * per, q1 = min(P, q0 + per);
+  float sw = 0.0f;
+  if (c < C) {
+    const float *pw = part + 2 * (int64_t)P * C + c;
+    int q = q0;
+    for (; q + 8 <= q1; q += 8) {   // 8 loads in flight, added in order
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = pw[(int64_t)(q + u) * C];
+#pragma unroll
+      for (int u = 0; u < 8; u++) sw = sw + v[u];
+    }
+    for (; q < q1; q++) sw = sw + pw[(int64_t)q * C];
+  }
+  chunk[k][cl] = sw;
+  __syncthreads();
+  if (k == 0 && c < C) {
+    float t = chunk[0][cl];
+#pragma unroll
+    for (int kk = 1; kk < 16; kk++) t = t + chunk[kk][cl];
+    dw[c] = t;
+  }
+}
+
+template <int kJ>
+static void launch_norm_bwd(const NormBwdArgs &p, bool res, hipStream_t st) {
+  const size_t lds = (size_t)4 * (res ? 4 : 3) * p.C * sizeof(float);
+  if (!res) norm_bwd_kernel<kJ, false, false><<<p.P, 256, lds, st>>>(p);
+  else if (p.dxn) norm_bwd_kernel<kJ, true, true><<<p.P, 256, lds, st>>>(p);
+  else norm_bwd_kernel<kJ, true, false><<<p.P, 256, lds, st>>>(p);
+}
+
+static int64_t norm_bwd_parts(int64_t rows, int64_t ntok) {
+  return ntok > 0 ? (rows / ntok) * ((ntok + kBwdRows - 1) / kBwdRows) : 0;
+}
 }  // namespace gpic
 
 using namespace gpic;
@@ -420,6 +648,56 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
   norm_stats_kernel<<<g1, 256, 0, st>>>(p, partial);
   const int g2 = (int)std::min<int64_t>((rows + 3) / 4, 2048);
   norm_cast_kernel<<<g2, 256, 0, st>>>(p, partial, g1);
+  return (int)hipGetLastError();
+}
+
+
+size_t gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t ntok, int64_t C) {
+  if (rows <= 0 || ntok <= 0 || C <= 0 || rows % ntok != 0) return 0;
+  return (size_t)4 * norm_bwd_parts(rows, ntok) * C * sizeof(float);
+}
+
+int gpic_fp8_res_mod_rmsnorm_bwd(const uint16_t *dh, const uint16_t *dxn, const uint16_t *xs, const uint16_t *a,
+                                 const uint16_t *gate, int64_t sg, const float *w, const uint16_t *scale, int64_t ssc,
+                                 const float *rstd, int64_t rows, int64_t ntok, int64_t C, uint16_t *dx, uint16_t *da,
+                                 float *dshift, float *dscale, float *dgate, float *dw, void *ws, size_t ws_bytes,
+                                 void *stream) {
+  const bool res = a != nullptr;
+  if (rows < 0 || C <= 0 || ntok <= 0 || !w || !scale || !dshift || !dscale || !dw || (res && (!gate || !dgate)))
+    return GPIC_EINVAL;
+  if (rows > 0 && (!dh || !xs || !rstd || !dx || (res && !da) || !ws)) return GPIC_EINVAL;
+  if (!res && (dxn || dgate)) return GPIC_EINVAL;
+  if (C % 256 != 0 || C > 2048 || rows % ntok != 0 || ssc % 4 != 0 || ssc < C || (res && (sg % 4 != 0 || sg < C)))
+    return GPIC_ESHAPE;
+  if (!aligned16(dh) || (dxn && !aligned16(dxn)) || !aligned16(xs) || (a && !aligned16(a)) || !aligned16(w) ||
+      ((uintptr_t)scale & 7u) || ((uintptr_t)gate & 7u) || !aligned16(dx) || (da && !aligned16(da)) ||
+      !aligned16(ws))
+    return GPIC_EALIGN;
+  const int64_t B = rows / ntok;
+  hipStream_t st = (hipStream_t)stream;
+  if (rows == 0) {   // no rows: d_w is zero (the reduce over no partials writes it; no memset, so a graph can hold it)
+    norm_bwd_reduce_kernel<<<(int)((C + 15) / 16), 256, 0, st>>>(nullptr, 0, 0, 0, (int)C, res, dshift, dscale,
+                                                                  dgate, dw);
+    return (int)hipGetLastError();
+  }
+  const int64_t P = norm_bwd_parts(rows, ntok);
+  if (ws_bytes < (size_t)4 * P * C * sizeof(float)) return GPIC_EWORKSPACE;
+  if (P >= (int64_t(1) << 31) / 4 || B * C >= (int64_t(1) << 31)) return GPIC_ESHAPE;
+  NormBwdArgs p{dh, dxn, xs, a, gate, w, scale, rstd, dx, da, static_cast<float *>(ws), rows, ntok, sg, ssc, (int)C,
+                (int)((ntok + kBwdRows - 1) / kBwdRows), (int)P};
+  switch (C / 256) {
+    case 1: launch_norm_bwd<1>(p, res, st); break;
+    case 2: launch_norm_bwd<2>(p, res, st); break;
+    case 3: launch_norm_bwd<3>(p, res, st); break;
+    case 4: launch_norm_bwd<4>(p, res, st); break;
+    case 5: launch_norm_bwd<5>(p, res, st); break;
+    case 6: launch_norm_bwd<6>(p, res, st); break;
+    case 7: launch_norm_bwd<7>(p, res, st); break;
+    default: launch_norm_bwd<8>(p, res, st); break;
+  }
+  const int64_t grid = (B * C + 255) / 256 + (C + 15) / 16;
+  norm_bwd_reduce_kernel<<<(int)grid, 256, 0, st>>>(static_cast<const float *>(ws), (int)P, p.tiles_b, (int)B, (int)C,
+                                                     res, dshift, dscale, dgate, dw);
   return (int)hipGetLastError();
 }
 

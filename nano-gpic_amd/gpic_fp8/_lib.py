@@ -33,6 +33,9 @@ SIGNATURES = {
     "gpic_fp8_swiglu_bwd_t": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_res_mod_rmsnorm": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                                          ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "gpic_fp8_res_mod_rmsnorm_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gpic_fp8_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "gpic_fp8_gemm": (_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
     "gpic_fp8_gemm_mn": (_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),

@@ -1,5 +1,6 @@
-"""The image blocks' two norm sites with the FP8 cast of their output folded into the producer:
-baselines/PixelGen/src/models/layers/fused_norm.py (lever K) on the HIP kernel of nano-gpic_amd/csrc/norm.hip.
+"""The image blocks' two norm sites with the FP8 cast of their output folded into the producer (the activation amax
+taken where h is made): baselines/PixelGen/src/models/layers/fused_norm.py (the reference's MFU lever K) on the HIP
+kernels of nano-gpic_amd/csrc/norm.hip.
 
     site 1 (norm1):  h = RMSNorm(x) * (1 + scale) + shift                                   mod_rmsnorm
     site 2 (norm2):  x_new = x + gate * a;  h = RMSNorm(x_new) * (1 + scale) + shift        res_mod_rmsnorm
@@ -13,8 +14,8 @@ e4m3 bytes and scale directly, and h itself only when asked. Functions:
 - fp8_res_mod_rmsnorm_mlp(x, a, gate, w_norm, shift, scale, eps, w12, w3): site 2 feeding the phase-3 FP8 SwiGLU MLP,
   returning (x_new, mlp output).
 
-The backward of the norm is the reference's analytic one (fused_norm.py:94-140) in torch fp32 ops; the linears'
-backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
+The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel (res_mod_rmsnorm_bwd);
+the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
 """
 from typing import Optional
 
@@ -81,30 +82,60 @@ def _(x, a, gate, w, shift, scale, eps, has_res, want_h, want_q=True):
             x.new_empty(B * N, dtype=torch.float32))
 
 
-def _norm_backward(dh, dxn, xs, a, gate, w, scale, rstd):
-    """The reference's backward of the norm site (fused_norm.py:94-140) in torch fp32 ops: dh [B, N, C] (the
-    gradient of h), dxn (that of x_new, site 2) or None, xs = x_new (site 2) or x, rstd [B * N]. Returns dx, da (or
-    None), d_gate [B, C] (or None), d_w [C], d_shift [B, C], d_scale [B, C] (fp32 column sums)."""
+@torch.library.custom_op("gpic::fp8_res_mod_rmsnorm_bwd", mutates_args=())
+def res_mod_rmsnorm_bwd(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch.Tensor, a: Optional[torch.Tensor],
+                        gate: Optional[torch.Tensor], w: torch.Tensor, scale: torch.Tensor, rstd: torch.Tensor
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The norm site's backward (fused_norm.py:94-147, op :249-275) on the HIP kernel: dh [B, N, C] (the gradient of
+    h), dxn (that of x_new, site 2) or None, xs = x_new (site 2) or x, a and gate (site 2) or None, rstd [B * N].
+    Returns dx, da (empty at site 1), d_gate [B, C] (empty at site 1), d_w [C], d_shift [B, C], d_scale [B, C]: fp32
+    column sums taken in a fixed order."""
+    L.require_gpu(dh, xs, w, scale, rstd)
     B, N, C = xs.shape
-    r = rstd.view(B, N, 1)
-    t = xs.float() * r
-    wf = w.float()
-    n = (wf * t).to(xs.dtype).float()
-    dhf = dh.float()
-    dsh = dhf.sum(1)
-    dsc = (dhf * n).sum(1)
-    dn = dhf * (1.0 + scale.reshape(B, 1, C).float())
-    dw = (dn * t).sum((0, 1))
-    dt = dn * wf
-    mean = (dt * t).sum(-1, keepdim=True) / C
-    dx = r * (dt - t * mean)
-    if dxn is not None:
-        dx = dx + dxn.float()
+    res = a is not None
+    dhc = L.aligned(dh.to(torch.bfloat16).contiguous())
+    xsc = L.aligned(xs.contiguous())
+    dxc = L.aligned(dxn.to(torch.bfloat16).contiguous()) if (res and dxn is not None) else None
+    ac = L.aligned(a.to(torch.bfloat16).contiguous()) if res else None
+    g = _vec(gate, B, C) if res else None
+    sc = _vec(scale, B, C)
+    wf = L.aligned(w.to(torch.float32).contiguous())
+    dev = xs.device
+    dx = torch.empty_like(xsc)
+    da = torch.empty_like(xsc) if res else xs.new_empty(0)
+    f32 = dict(dtype=torch.float32, device=dev)
+    if B * N == 0:   # no rows: every column sum is zero
+        z = torch.zeros(B, C, **f32)
+        return dx, da, (z.clone() if res else torch.empty(0, **f32)), torch.zeros(C, **f32), z.clone(), z.clone()
+    dg = torch.empty(B, C, **f32) if res else torch.empty(0, **f32)
+    dw, dsh, dsc = torch.empty(C, **f32), torch.empty(B, C, **f32), torch.empty(B, C, **f32)
+    with torch.cuda.device(dev):
+        nws = L.lib().gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes(B * N, max(N, 1), C)
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=dev)
+        L.check(L.lib().gpic_fp8_res_mod_rmsnorm_bwd(
+            dhc.data_ptr(), L.ptr(dxc), xsc.data_ptr(), L.ptr(ac), L.ptr(g), g.stride(0) if res else 0, wf.data_ptr(),
+            sc.data_ptr(), sc.stride(0), rstd.data_ptr(), B * N, max(N, 1), C, dx.data_ptr(),
+            da.data_ptr() if res else None, dsh.data_ptr(), dsc.data_ptr(), dg.data_ptr() if res else None,
+            dw.data_ptr(), ws.data_ptr(), nws, L.stream_ptr(dev)), "gpic_fp8_res_mod_rmsnorm_bwd")
+    return dx, da, dg, dw, dsh, dsc
+
+
+@res_mod_rmsnorm_bwd.register_fake
+def _(dh, dxn, xs, a, gate, w, scale, rstd):
+    B, N, C = xs.shape
+    res = a is not None
+    f32 = dict(dtype=torch.float32)
+    return (torch.empty_like(xs), torch.empty_like(xs) if res else xs.new_empty(0),
+            xs.new_empty((B, C) if res else (0,), **f32), xs.new_empty(C, **f32), xs.new_empty(B, C, **f32),
+            xs.new_empty(B, C, **f32))
+
+
+def _norm_backward(dh, dxn, xs, a, gate, w, scale, rstd):
+    """The norm site's backward: (dx, da or None, d_gate or None, d_w, d_shift, d_scale), the column sums fp32."""
+    dx, da, dg, dw, dsh, dsc = res_mod_rmsnorm_bwd(dh, dxn if a is not None else None, xs, a, gate, w, scale, rstd)
     if a is None:
-        return dx.to(xs.dtype), None, None, dw, dsh, dsc
-    da = dx * gate.reshape(B, 1, C).float()
-    dg = (dx * a.float()).sum(1)
-    return dx.to(xs.dtype), da.to(a.dtype), dg, dw, dsh, dsc
+        return dx, None, None, dw, dsh, dsc
+    return dx, da, dg, dw, dsh, dsc
 
 
 def _param_grads(B, C, dg, dw, dsh, dsc, gate, w, shift, scale):

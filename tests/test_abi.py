@@ -83,6 +83,24 @@ def test_validation_codes():
     assert nm(wsp, None, None, 0, wsp + 8, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp,
               None) == -4
     assert nm(wsp, wsp, None, 256, wsp, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, wsp, None, wsp, wsp, wsp, wsp, None) == -1
+    # the norm's backward: C % 256 and <= 2048, rows % ntok, site-1 arguments, workspace size, alignment
+    nb = lib.gpic_fp8_res_mod_rmsnorm_bwd
+    nbw = lib.gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes
+    assert nbw(4, 2, 256) == 4 * 2 * 256 * 4 and nbw(4, 3, 256) == 0 and nbw(0, 1, 256) == 0
+    assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 256, wsp, 4, 2, 128, wsp, None, wsp, wsp, None, wsp, wsp, 1 << 20,
+              None) == -3
+    assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 4096, wsp, 4, 2, 4096, wsp, None, wsp, wsp, None, wsp, wsp,
+              1 << 20, None) == -3
+    assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 256, wsp, 5, 2, 256, wsp, None, wsp, wsp, None, wsp, wsp, 1 << 20,
+              None) == -3
+    assert nb(wsp, wsp, wsp, None, None, 0, wsp, wsp, 256, wsp, 4, 2, 256, wsp, None, wsp, wsp, None, wsp, wsp, 1 << 20,
+              None) == -1
+    assert nb(wsp, None, wsp, wsp, None, 256, wsp, wsp, 256, wsp, 4, 2, 256, wsp, wsp, wsp, wsp, wsp, wsp, wsp, 1 << 20,
+              None) == -1
+    assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 256, wsp, 4, 2, 256, wsp, None, wsp, wsp, None, wsp, wsp, 16,
+              None) == -5
+    assert nb(wsp + 8, None, wsp, None, None, 0, wsp, wsp, 256, wsp, 4, 2, 256, wsp, None, wsp, wsp, None, wsp, wsp,
+              1 << 20, None) == -4
     # GEMM: K % 16, N % 16, leading dimensions, null scales
     g = lib.gpic_fp8_gemm
     assert g(wsp, 24, wsp, wsp, 24, wsp, None, wsp, 16, 4, 16, 24, 1, None, 0, None) == -3

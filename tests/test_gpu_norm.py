@@ -182,3 +182,78 @@ def test_fused_site2_mlp_equals_unfused(dev):
     for got, want in zip(*runs):
         assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got,
                            want.view(torch.int16) if want.dtype == torch.bfloat16 else want)
+
+
+def torch_backward(dh, dxn, xs, a, gate, w, scale, rstd):
+    """The reference's analytic backward of the norm site (fused_norm.py:94-147) in torch fp32 ops, the checker of
+    the HIP kernel: (dx, da, d_gate, d_w, d_shift, d_scale) with dx, da before their bf16 rounding."""
+    B, N, C = xs.shape
+    r = rstd.view(B, N, 1)
+    t = xs.float() * r
+    wf = w.float()
+    n = (wf * t).to(torch.bfloat16).float()
+    dhf = dh.float()
+    dsh, dsc = dhf.sum(1), (dhf * n).sum(1)
+    dn = dhf * (1.0 + scale.reshape(B, 1, C).float())
+    dw = (dn * t).sum((0, 1))
+    dt = dn * wf
+    dx = r * (dt - t * ((dt * t).sum(-1, keepdim=True) / C))
+    if dxn is not None:
+        dx = dx + dxn.float()
+    if a is None:
+        return dx, None, None, dw, dsh, dsc
+    return dx, dx * gate.reshape(B, 1, C).float(), (dx * a.float()).sum(1), dw, dsh, dsc
+
+
+def _close_bf16(got, want, name):
+    """got (bf16) within one bf16 rounding of want (fp32) plus 1e-5 of want's rms: the row sum's order differs from
+    torch's, so dt - t * mean may differ in its last fp32 bits where it cancels."""
+    g, w = got.float(), want
+    tol = w.abs() * 2.0 ** -8 + 1e-5 * w.pow(2).mean().sqrt()
+    bad = ((g - w).abs() > tol).sum().item()
+    assert bad == 0, f"{name}: {bad} elements out of bounds"
+
+
+def _close_f32(got, want, name, rel=1e-5):
+    err = ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
+    assert err < rel, (name, err)
+
+
+@pytest.mark.parametrize("res,dxn", [(False, False), (True, True), (True, False)])
+@pytest.mark.parametrize("B,N,C", [(128, 256, 1024), (4, 100, 768), (2, 64, 1792), (3, 50, 2048)])
+def test_backward_kernel(dev, B, N, C, res, dxn):
+    """The HIP backward (gpic_fp8_res_mod_rmsnorm_bwd) against the reference's formula in torch fp32, and twice in a
+    row bit for bit (fixed summation order)."""
+    from gpic_fp8 import norm as NM
+    x, a, gate, w, shift, scale = inputs(B, N, C, 40 + B + C + res, dev, res)
+    xn, h, _, _, rstd = G.res_mod_rmsnorm_q(x, a, gate, w, shift, scale, 1e-6, res, True, False)
+    xs = xn if res else x
+    g = torch.Generator(device=dev).manual_seed(41)
+    dh = (torch.randn(B, N, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    dx_up = (torch.randn(B, N, C, generator=g, device=dev) * 0.1).to(torch.bfloat16) if (res and dxn) else None
+    args = (dh, dx_up, xs, a if res else None, gate if res else None, w, scale, rstd)
+    out = NM.res_mod_rmsnorm_bwd(*args)
+    ref = torch_backward(*args)
+    dx, da, dg, dwk, dsh, dsc = out
+    _close_bf16(dx, ref[0], "dx")
+    _close_f32(dwk, ref[3], "d_w")
+    _close_f32(dsh, ref[4], "d_shift")
+    _close_f32(dsc, ref[5], "d_scale")
+    if res:
+        _close_bf16(da, ref[1], "da")
+        _close_f32(dg, ref[2], "d_gate")
+    again = NM.res_mod_rmsnorm_bwd(*args)
+    for u, v in zip(out, again):
+        assert torch.equal(u.view(torch.int32) if u.dtype == torch.float32 else u.view(torch.int16),
+                           v.view(torch.int32) if v.dtype == torch.float32 else v.view(torch.int16))
+
+
+def test_backward_kernel_empty(dev):
+    """No rows: dx and da are empty, every column sum is zero."""
+    from gpic_fp8 import norm as NM
+    x, a, gate, w, shift, scale = inputs(2, 8, 256, 42, dev, True)
+    e = x[:, :0]
+    dx, da, dg, dw, dsh, dsc = NM.res_mod_rmsnorm_bwd(e, e, e, e, gate, w, scale,
+                                                      torch.empty(0, device=dev, dtype=torch.float32))
+    assert dx.numel() == 0 and da.numel() == 0 and torch.equal(dw, torch.zeros_like(dw))
+    assert not dg.any() and not dsh.any() and not dsc.any() and dg.shape == (2, 256)
