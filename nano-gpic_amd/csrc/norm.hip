@@ -158,22 +158,19 @@ __device__ __forceinline__ uint32_t cast4_packed(u32x2 hw, float s) {
   return e4m3x4(sat(bf16_lo(hw.x) * s), sat(bf16_hi(hw.x) * s), sat(bf16_lo(hw.y) * s), sat(bf16_hi(hw.y) * s));
 }
 
-// Single pass: wave w of workgroup g holds rows (4 g + w) kR .. + kR - 1 (kJ groups of 4 per lane each), the
-// workgroups fold their maxima (gpic_once.h), and each casts its rows from its registers. The rows of a wave go
-// through each phase together, so that one memory latency covers all of them: every row's x is requested first,
+// A wave's kR consecutive rows from row0 (kJ groups of 4 per lane each) through the norm: x_new (site 2) and rstd
+// written, h left as packed bf16 in X, and the largest |h| returned (fp32, before h's rounding; NaN ignored). The rows
+// go through each phase together, so that one memory latency covers all of them: every row's x is requested first,
 // then (site 2) a and gate are folded in, the kR butterflies run interleaved, and w, shift and scale are read once
 // per group and used for all the rows; h replaces x in the same registers. Rows past the end re-read the last row
 // (same values, so the same maximum) and store nothing. kUni: every row of a wave lies in one batch (ntok % kR ==
-// 0), so gate, shift and scale are one vector per wave.
+// 0), so gate, shift and scale are one vector per wave. row0 must be wave-uniform (a scalar: the rows' addresses are
+// then scalar bases plus one per-lane offset).
 template <int kJ, int kR, bool kUni, bool kRes>
-__global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *ws, uint32_t wait_ticks) {
-  // (the wave index as a scalar: the rows' addresses are then scalar bases plus one per-lane offset)
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * kR;
+__device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int lane, u32x2 (&X)[kR][kJ]) {
   const int64_t C = p.C;
   auto rowi = [&](int r) { return min(row0 + r, p.rows - 1); };
   auto bat = [&](int r) { return (kUni ? row0 : rowi(r)) / p.ntok; };
-  u32x2 X[kR][kJ];
 #pragma unroll
   for (int r = 0; r < kR; r++)
 #pragma unroll
@@ -274,13 +271,26 @@ __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *w
       for (int e = 0; e < 4; e++) mf = fmaxf(mf, fabsf(hv[e]));
     }
   }
-  // h is made here, before the fold, and kept only as packed words (the compiler would otherwise carry phase 3's
-  // fp32 values across the fold into the cast below)
+  // h is made here and kept only as packed words (the compiler would otherwise carry phase 3's fp32 values into
+  // the caller's fold and stores)
 #pragma unroll
   for (int r = 0; r < kR; r++)
 #pragma unroll
     for (int j = 0; j < kJ; j++) asm volatile("" : "+v"(X[r][j]));
   phase_fence();
+  return mf;
+}
+
+// Single pass: wave w of workgroup g takes rows (4 g + w) kR .. + kR - 1 through norm_rows, the workgroups fold their
+// maxima (gpic_once.h), and each casts its rows from its registers.
+template <int kJ, int kR, bool kUni, bool kRes>
+__global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *ws, uint32_t wait_ticks) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * kR;
+  const int64_t C = p.C;
+  const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);   // rows of this wave that exist
+  u32x2 X[kR][kJ];
+  const float mf = norm_rows<kJ, kR, kUni, kRes>(p, row0, lane, X);
   const uint32_t g = once_fold(block_max_u32(__float_as_uint(bf16_round(mf))), ws, wait_ticks, [&](int cb) {
     // workgroup cb's maximum from its rows (nothing stored): for a partial that did not appear in time
     uint32_t v = 0;
@@ -301,6 +311,34 @@ __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *w
         __builtin_nontemporal_store(cast4_packed(X[r][j], scale),
                                     reinterpret_cast<uint32_t *>(p.hq + (row0 + r) * C + 4 * (lane + 64 * j)));
     }
+}
+
+// Two passes, 1 (rows of at most 2048): workgroup g takes the groups of 4 kR rows g, g + G, ... through norm_rows,
+// writes h when asked, and leaves the largest |h| of its rows in partial[g] (float bits of the bf16 value).
+// (Two workgroups per CU and 256 registers a lane: it loops over its groups, so it needs no more residency than that,
+// and the loop keeps more live than the single pass.) kH: write h.
+template <int kJ, int kR, bool kUni, bool kRes, bool kH>
+__global__ __launch_bounds__(256, 2) void norm_rows_kernel(NormArgs p, uint32_t *__restrict__ partial, int64_t groups) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t C = p.C;
+  float mf = 0.0f;
+  for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
+    const int64_t row0 = (g * 4 + wave) * kR;
+    const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);
+    u32x2 X[kR][kJ];
+    mf = fmaxf(mf, norm_rows<kJ, kR, kUni, kRes>(p, row0, lane, X));
+    if (kH) {
+#pragma unroll
+      for (int r = 0; r < kR; r++)
+        if (r < nr) {
+#pragma unroll
+          for (int j = 0; j < kJ; j++)
+            *reinterpret_cast<u32x2 *>(p.h + (row0 + r) * C + 4 * (lane + 64 * j)) = X[r][j];
+        }
+    }
+  }
+  const uint32_t m = block_max_u32(__float_as_uint(bf16_round(mf)));
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
 // Two passes, 1: rows strided over the waves of the grid; x_new, rstd (and h) written, one partial maximum per
@@ -362,6 +400,45 @@ static bool launch_norm_once_t(const NormArgs &p, void *ws, hipStream_t st) {
   if (cap <= 0 || wgs > cap) return false;
   norm_q_once_kernel<kJ, kR, kUni, kRes><<<(int)wgs, 256, 0, st>>>(p, ws, once_wait_ticks());
   return true;
+}
+
+// The first of the two passes for rows of at most 2048: one partial maximum per workgroup in `partial` (at most
+// kMaxParts workgroups, each taking every G-th group of 4 kR rows). Returns the number of partials.
+template <int kJ, bool kUni, bool kRes>
+static int launch_norm_rows_t(const NormArgs &p, uint32_t *partial, hipStream_t st) {
+  constexpr int kR = kRowsOnce<kJ>;
+  const int64_t groups = (p.rows + 4 * kR - 1) / (4 * kR);
+  const int g = (int)std::min<int64_t>(groups, kMaxParts);
+  if (p.h) norm_rows_kernel<kJ, kR, kUni, kRes, true><<<g, 256, 0, st>>>(p, partial, groups);
+  else norm_rows_kernel<kJ, kR, kUni, kRes, false><<<g, 256, 0, st>>>(p, partial, groups);
+  return g;
+}
+
+template <int kJ>
+static int launch_norm_rows(const NormArgs &p, uint32_t *partial, hipStream_t st) {
+  const bool uni = p.ntok % kRowsOnce<kJ> == 0;
+  if (p.a) return uni ? launch_norm_rows_t<kJ, true, true>(p, partial, st) : launch_norm_rows_t<kJ, false, true>(p, partial, st);
+  return uni ? launch_norm_rows_t<kJ, true, false>(p, partial, st) : launch_norm_rows_t<kJ, false, false>(p, partial, st);
+}
+
+// Pass 1 of the two passes: the multi-row kernel for rows of at most 2048, else the row-at-a-time one. Returns the
+// number of partial maxima written to `partial`.
+static int norm_first_pass(const NormArgs &p, uint32_t *partial, hipStream_t st) {
+  switch (p.C / 256) {
+    case 1: return launch_norm_rows<1>(p, partial, st);
+    case 2: return launch_norm_rows<2>(p, partial, st);
+    case 3: return launch_norm_rows<3>(p, partial, st);
+    case 4: return launch_norm_rows<4>(p, partial, st);
+    case 5: return launch_norm_rows<5>(p, partial, st);
+    case 6: return launch_norm_rows<6>(p, partial, st);
+    case 7: return launch_norm_rows<7>(p, partial, st);
+    case 8: return launch_norm_rows<8>(p, partial, st);
+    default: {
+      const int g = (int)std::min<int64_t>((p.rows + 3) / 4, kMaxParts);
+      norm_stats_kernel<<<g, 256, 0, st>>>(p, partial);
+      return g;
+    }
+  }
 }
 
 template <int kJ>
@@ -627,7 +704,7 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
     return (int)hipGetLastError();
   }
   if (!cast) {   // the norm alone (h, x_new, rstd): the first pass of the two-pass path, its partial maxima unused
-    norm_stats_kernel<<<(int)std::min<int64_t>((rows + 3) / 4, kMaxParts), 256, 0, st>>>(p, static_cast<uint32_t *>(ws));
+    norm_first_pass(p, static_cast<uint32_t *>(ws), st);
     return (int)hipGetLastError();
   }
   bool done = false;
@@ -644,8 +721,7 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
   }
   if (done) return (int)hipGetLastError();
   uint32_t *partial = static_cast<uint32_t *>(ws);
-  const int g1 = (int)std::min<int64_t>((rows + 3) / 4, kMaxParts);
-  norm_stats_kernel<<<g1, 256, 0, st>>>(p, partial);
+  const int g1 = norm_first_pass(p, partial, st);
   const int g2 = (int)std::min<int64_t>((rows + 3) / 4, 2048);
   norm_cast_kernel<<<g2, 256, 0, st>>>(p, partial, g1);
   return (int)hipGetLastError();
