@@ -10,7 +10,9 @@ bf16. value = 3.2985 TFLOP / measured step time.
 
 Also measured live: the 12 GEMM launches alone (the roofline's dominant kernel, HIP events on the launch stream),
 the config-2 cast ([32768 x 1024] bf16 -> e4m3, GB/s of algorithmic bytes), hipBLASLt's FP8 GEMM on the same 12
-shapes via torch._scaled_mm (a comparator only), and the CPU baseline (the oracle, a bounded sample).
+shapes via torch._scaled_mm (a comparator only), the MFMA rate the device sustains at 100% issue on random and on
+constant e4m3 operands (tests/hip/mfma_ceiling.hip: the power-limited ceiling the GEMM's fraction is read against),
+and the CPU baseline (the oracle, a bounded sample).
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-compare]
 """
@@ -283,6 +285,27 @@ def norm_block(G, dev, B=128, N=256, eps=1e-6, steps=20):
             "fused_ms": round(f, 4), "unfused_ms": round(u, 4), "saved_us": round((u - f) * 1e3, 1)}
 
 
+def mfma_ceiling():
+    """The FP8 MFMA rate the device sustains at 100% issue on random e4m3 operands (tests/hip/mfma_ceiling.hip: every
+    SIMD issuing v_mfma_f32_32x32x64_f8f6f4 back to back from LDS, no HBM traffic), and on constant operands, measured
+    live. Random operands draw enough power that the clock drops below the 2.4 GHz of the published peak; None if the
+    measurement library has not been built."""
+    import ctypes
+    path = os.path.join(ROOT, "tests", "hip", "libmfma_ceiling.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    d = ctypes.c_double
+    lib.gpic_probe_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.POINTER(d)] * 4
+    out = {}
+    for name, rnd in (("const", 0), ("random", 1)):
+        ms, tf, ghz, busy = d(), d(), d(), d()
+        if lib.gpic_probe_mfma_ceiling(rnd, 8000, ms, tf, ghz, busy) != 0:
+            return None
+        out[name] = {"TFLOPs": round(tf.value, 1), "clock_GHz": round(ghz.value, 3), "mfma_busy": round(busy.value, 4)}
+    return out
+
+
 def gemm_source_sha():
     import hashlib
     with open(os.path.join(ROOT, "nano-gpic_amd", "csrc", "gemm.hip"), "rb") as f:
@@ -550,6 +573,7 @@ def main():
             hip = {"error": f"{type(e).__name__}: {str(e)[:200]}"}
     del ops
 
+    ceiling = mfma_ceiling()
     cpu = None if args.no_cpu else cpu_baseline()
     gemm_tflops = fl / gemm_ms / 1e9
     traffic = gemm_traffic()
@@ -575,7 +599,9 @@ def main():
                      "kernel": "gemm_tn_kernel (K-major fwd / dgrad, MN-major wgrad instances; + split-K reduce)",
                      "launches_per_step": len(shapes),
                      "avg_launch_us": round(gemm_ms * 1e3 / len(shapes), 1), "gemm_ms_per_step": round(gemm_ms, 4),
-                     "per_shape": per_shape},
+                     "per_shape": per_shape,
+                     "mfma_ceiling": ceiling,
+                     "frac_of_random_ceiling": round(gemm_tflops / ceiling["random"]["TFLOPs"], 4) if ceiling else None},
         "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale, L2 / MALL flushed before each "
                              "call (a 512 MB write; median of 20); the warm figures are back-to-back calls",
                  "us": round(cast_cold_ms * 1e3, 2), "achieved_GBs": round(cast_bytes / cast_cold_ms / 1e6, 1),

@@ -34,21 +34,28 @@ def build(verbose=False):
     return LIB
 
 
-def build_selfcheck(verbose=False):
-    """The test-only bf16 self-check library (tests/hip), with the same compiler flags as the product."""
+TEST_LIBS = {"bf16_selfcheck.hip": "libbf16_selfcheck.so", "mfma_ceiling.hip": "libmfma_ceiling.so"}
+
+
+def build_test_libs(verbose=False):
+    """The test-side libraries under tests/hip (the bf16 rounding self-check, the MFMA ceiling measurement), with the
+    same compiler flags as the product."""
     root = os.path.dirname(os.path.dirname(HERE))
-    src = os.path.join(root, "tests", "hip", "bf16_selfcheck.hip")
-    out = os.path.join(root, "tests", "hip", "libbf16_selfcheck.so")
-    cmd = [HIPCC, *FLAGS, "-o", out + ".tmp", src]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-6000:]}")
-    os.replace(out + ".tmp", out)
-    return out
+    outs = []
+    for src_name, lib_name in TEST_LIBS.items():
+        src = os.path.join(root, "tests", "hip", src_name)
+        out = os.path.join(root, "tests", "hip", lib_name)
+        cmd = [HIPCC, *FLAGS, "-o", out + ".tmp", src]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-6000:]}")
+        os.replace(out + ".tmp", out)
+        outs.append(out)
+    return outs
 
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
-    print(build_selfcheck(verbose="-v" in sys.argv))
+    print(build_test_libs(verbose="-v" in sys.argv))
