@@ -343,6 +343,41 @@ def test_single_pass_concurrent_streams(dev, single_pass_default):
         assert torch.equal(qt.view(torch.uint8), rqt.view(torch.uint8))
 
 
+def test_single_pass_beside_a_persistent_gemm(dev, single_pass_default):
+    """A persistent GEMM (one workgroup holding all 160 KiB of LDS on every CU) runs on one stream while single-pass
+    casts run on another: the casts' workgroups find CUs only as the GEMM's leave them, so their grids start piecemeal
+    and the bounded waits run out. Every result equals the one computed alone (bytes and scale), for casts issued
+    before, during and after the GEMMs."""
+    g = torch.Generator(device=dev).manual_seed(23)
+    xs = [(torch.randn(32768, 1024, generator=g, device=dev) * (1 + 2 * i)).to(torch.bfloat16) for i in range(3)]
+    ref = [G.tcast(x) for x in xs]
+    a = torch.randn(32768, 1024, generator=g, device=dev).to(torch.bfloat16)
+    b = (torch.randn(8192, 1024, generator=g, device=dev) / 32).to(torch.bfloat16)
+    aq, sa = G.tcast(a)
+    bq, sb = G.tcast(b)
+    y0 = G.fp8_gemm(aq, sa, bq, sb)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    outs, ys = [], []
+    for order in range(3):
+        if order == 0:          # casts first, the GEMMs right behind them
+            with torch.cuda.stream(s2):
+                outs += [G.tcast(x) for x in xs]
+            with torch.cuda.stream(s1):
+                ys += [G.fp8_gemm(aq, sa, bq, sb) for _ in range(2)]
+        else:                   # GEMMs first (order 1) or between two casts (order 2)
+            with torch.cuda.stream(s1):
+                ys += [G.fp8_gemm(aq, sa, bq, sb) for _ in range(2)]
+            with torch.cuda.stream(s2):
+                outs += [G.tcast(x) for x in (xs if order == 1 else reversed(xs))]
+        torch.cuda.synchronize()
+    for i, (q, s) in enumerate(outs):
+        rq, rs = ref[i % 3] if i < 6 else ref[2 - i % 3]
+        assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8)), i
+    for y in ys:
+        assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
+
+
 @pytest.mark.parametrize("shape,dtype", [((32768, 3072), torch.bfloat16), ((41_000_009,), torch.bfloat16),
                                          ((8192, 4096), torch.float32), ((4_194_304 * 8 * 8,), torch.bfloat16)])
 def test_flat_hybrid_matches_two_pass(dev, shape, dtype, single_pass_default):
