@@ -5,13 +5,15 @@
 //
 // Design (CDNA4):
 //  * Macro tile 256 x 256 x 128 per workgroup of 8 waves, two per SIMD. Wave w owns the 64 x 128 sub-tile
-//    (rows 64 * (w >> 1), columns 128 * (w & 1)) as 2 x 4 MFMA tiles of v_mfma_f32_32x32x64_f8f6f4 (both operands
-//    e4m3, fp32 accumulators in VGPRs: 239 of the 256 a wave of two per SIMD may hold, so the epilogue's VALU
-//    work reads them without AGPR copies; measured 0.5% faster than accumulators in AGPRs).
+//    (rows 64 * (w >> 1), columns 128 * (w & 1)) as 4 x 8 MFMA tiles of v_mfma_f32_16x16x128_f8f6f4, one instruction
+//    per tile and K tile (both operands e4m3, fp32 accumulators in VGPRs, so the epilogue's VALU work reads them
+//    without AGPR copies). The 16 x 16 x 128 form does the 32 x 32 x 64 form's work per cycle at lower power: on random
+//    e4m3 operands an MFMA-only loop held the clock at 1.87-1.95 GHz against 1.59-1.68 (3.9-4.1 against 3.3-3.5
+//    PFLOP/s), and this kernel is power-bound on real data.
 //  * A narrow class, 256 x 128, for shapes whose 256 x 256 tiles leave CUs idle: each wave then owns 64 x 64, the B
 //    K tile is 16 KiB; the host picks the width and the K split per shape, the same for both operand layouts.
 //  * Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share the SIMDs pairwise and run one phase apart. In each
-//    phase one group issues its 16 MFMAs of a K tile while the other reads its 12 fragments of that K tile from LDS,
+//    phase one group issues its 32 MFMAs of a K tile while the other reads its 12 fragments of that K tile from LDS,
 //    with its share of a later K tile's loads between the reads (group 0 sends B one K tile ahead, group 1 sends A
 //    two ahead); a workgroup barrier separates phases. The MFMA pipe of every SIMD sees the two groups' MFMA blocks
 //    back to back. LDS: 3 A stages and 2 B stages of 32 KiB, all of gfx950's 160 KiB.
@@ -23,9 +25,9 @@
 //    256 B per clock to 16 lanes at a time; the fragment reads of 16 consecutive rows at one chunk then hit 16
 //    different 16-byte bank groups (measured: no SQ_LDS_BANK_CONFLICT cycles).
 //  * The MFMA is issued as B-fragment x A-fragment with B's rows permuted in LDS (col_of), so each lane's
-//    accumulators hold runs of 8 consecutive columns of one row of C. The bf16 epilogue rounds them, passes each
-//    32-row block through LDS and stores 16 bytes per lane, whole 256-byte row segments per 16 lanes; split-K
-//    partials go out as 16-byte fp32 stores straight from the accumulators.
+//    accumulators hold, for each pair of 16-column tiles, a run of 8 consecutive columns of one row of C. The bf16
+//    epilogue rounds them, passes each 32-row block through LDS and stores 16 bytes per lane, whole 256-byte row
+//    segments per 16 lanes; split-K partials go out as 16-byte fp32 stores straight from the accumulators.
 //  * Persistent grid: work items (tile, K split) are dealt to the workgroups round robin and the id is remapped so
 //    each XCD walks a contiguous range of tiles in groups of kGroupM tile rows (neighbouring workgroups share A and B
 //    panels in that XCD's L2). The next item's first loads are issued before the current item's epilogue.
@@ -53,7 +55,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kBM = 256, kBN = 256, kBK = 128;         // the wide tile (the narrow one is 256 x 128: kBNt)
 constexpr int kThreads = 512;                          // 8 waves: 2 groups x 4
 constexpr int kWTM = 64;                               // wave tile rows (columns: kWTNt, 128 or 64)
-constexpr int kTM = kWTM / 32;                         // 32 x 32 MFMA tiles per wave in M: 2
+constexpr int kTM = kWTM / 16;                         // 16 x 16 MFMA tiles per wave in M: 4
 constexpr int kHalfBytes = kBM * kBK;                  // 32 KiB: an A K tile (and a wide tile's B K tile)
 constexpr int kAStages = 3, kBStages = 2;              // A is sent two K tiles ahead, B one
 constexpr int kBBase = kAStages * kHalfBytes;          // B stages follow the A stages (160 KiB in all for the wide tile)
@@ -69,22 +71,28 @@ constexpr int kOOB = (int)0x80000000;                  // an offset past any des
 constexpr int kStoreNT = 2;
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
-// MN-major K tiles (rows of 256 bytes): 16-byte chunk c of K row r lives in slot c ^ mn_swz(r). A transposing read
-// takes two adjacent chunks (2c', 2c' + 1) of 8 consecutive rows; the XOR with 2 (r & 7) sends those 16 chunks to 16
+// MN-major K tiles (rows of 256 bytes): 16-byte chunk c of K row r lives in slot c ^ mn_swz(r). A 16-lane group of a
+// transposing read takes one chunk of 8 consecutive rows, and the two groups of a half-wave take the same chunk 32
+// rows apart (K bytes 32 g of the fragment); the XOR with 2 (r & 7) | (r >> 5) & 1 sends those 16 chunks to 16
 // different slots, i.e. all 64 banks.
-__device__ __forceinline__ int mn_swz(int r) { return (r & 7) << 1; }
+__device__ __forceinline__ int mn_swz(int r) { return ((r & 7) << 1) | ((r >> 5) & 1); }
 // The narrow tile's MN-major B K tile has rows of 128 bytes (8 chunks): chunk c of K row r lives in slot
-// c ^ mn_swz_n(r). Two rows share a 256-byte bank window, so the 8 rows x 2 chunks of a transposing read hit 16
-// different 16-byte slots when the 4 rows of each parity XOR the chunk pair with 4 different even masks.
-__device__ __forceinline__ int mn_swz_n(int r) { return ((r >> 1) & 3) << 1; }
+// c ^ mn_swz_n(r). Two rows share a 256-byte bank window, so the 8 rows of a group hit 8 different 16-byte slots when
+// the 4 rows of each parity XOR the chunk with 4 different even masks, and the two groups 32 rows apart differ in
+// the lowest bit.
+__device__ __forceinline__ int mn_swz_n(int r) { return (((r >> 1) & 3) << 1) | ((r >> 5) & 1); }
 
-// The column of C that MFMA output row i (0..31) of a 32 x 32 tile stands for: i with bits 2 and 3 exchanged. Lane l
-// holds output rows 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15; through this map those are the columns
-// 16 (v / 8) + 8 (l / 32) + v % 8, i.e. two runs of 8 consecutive columns. An involution that keeps every aligned
-// group of 16 rows, so with N % 16 == 0 the rows past N stay past N.
-__host__ __device__ constexpr int col_of(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
-static_assert(col_of(13) == 13 && col_of(8) == 4 && col_of(4) == 8 && col_of(17) == 17 && col_of(col_of(22)) == 22,
-              "col_of swaps bits 2 and 3");
+// The column of C that MFMA output row i of a pair of 16 x 16 tiles (i = 0..31: tile i / 16, row i % 16) stands for.
+// Lane l holds output rows 4 (l / 16) + v, v = 0..3, of each tile; through this map those of tiles 2p and 2p + 1 are
+// the columns 32 p + 8 (l / 16) + [0, 8), one run of 8. In bits: i = (h, g, v) with h = bit 4, g = bits 2-3,
+// v = bits 0-1 maps to (g, h, v). A permutation of each aligned group of 32 rows; the loads take B row col_of(r) for
+// LDS row r, and rows past N read as zeros through the descriptor's range whichever LDS row they land in.
+__host__ __device__ constexpr int col_of(int i) {
+  return (i & ~31) | (((i >> 2) & 3) << 3) | (((i >> 4) & 1) << 2) | (i & 3);
+}
+static_assert(col_of(3) == 3 && col_of(4) == 8 && col_of(16) == 4 && col_of(20) == 12 && col_of(31) == 31 &&
+                  col_of(32 + 17) == 32 + 5,
+              "col_of: tile bit 4 and row bits 2-3 of a pair of 16 x 16 tiles to column bits 2 and 3-4");
 
 // Raw buffer descriptor (stride 0) over [base, base + bytes): offsets at or past `bytes` read as zero.
 __device__ __forceinline__ v4i buffer_rsrc(const void *base, int bytes) {
@@ -144,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
                                                             int ksplit, int tiles_m, int tiles_n, int splits) {
   static_assert(kBNt == 256 || kBNt == 128, "tile widths: 256 or 128");
   constexpr int kWTNt = kBNt / 2;                 // wave tile columns
-  constexpr int kTNt = kWTNt / 32;                // 32-column MFMA tiles per wave: 4 or 2
+  constexpr int kTNt = kWTNt / 16;                // 16-column MFMA tiles per wave: 8 or 4
   constexpr int kHalfB = kBNt * kBK;              // one B K tile: 32 or 16 KiB
   constexpr int kLoadsB = kBNt / 8 / kLoaders;    // B loads per wave per K tile: 8 or 4
   constexpr int kRowB = kWTNt * 2;                // bytes of a row of a wave's bf16 C block: 256 or 128
@@ -169,14 +177,17 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // lane j writes 16-byte slot j & 15 of row 16 i + mrow, i.e. MN chunk (j & 15) ^ mn_swz(row), and mn_swz depends on
   // row & 7 = mrow & 7 only.
   const int mrow = (wave & 3) * 4 + (lane >> 4);
-  const int mchunk = (lane & 15) ^ mn_swz(mrow);
+  const int mchunk = (lane & 15) ^ mn_swz(mrow);   // for K rows with bit 5 clear (i & 2 == 0); else mchunk ^ 1
   // MN-major B of the narrow tile: instruction i fills K rows [R0, R0 + 8), R0 = (i * 4 + wave % 4) * 8 =
   // 32 i + mrowB - lane / 8; lane j writes slot j & 7 of row 32 i + mrowB, i.e. MN chunk (j & 7) ^ mn_swz_n(row), and
-  // mn_swz_n depends on (row / 2) & 3 = (mrowB / 2) & 3 only.
+  // mn_swz_n depends on (row / 2) & 3 = (mrowB / 2) & 3 and on bit 5 of the row, i & 1.
   const int mrowB = kBNt == 256 ? mrow : (wave & 3) * 8 + (lane >> 3);
   const int mchunkB = kBNt == 256 ? mchunk : (lane & 7) ^ mn_swz_n(mrowB);
   const int baseA = kMN ? mrow * lda + 16 * mchunk : lrow * lda + kchunk;
   const int baseB = kMN ? mrowB * ldb + 16 * mchunkB : col_of(lrow) * ldb + kchunk;
+  // MN-major: the same loads for K rows with bit 5 set, whose chunks are swizzled with one more bit
+  const int baseA1 = mrow * lda + 16 * (mchunk ^ 1);
+  const int baseB1 = mrowB * ldb + 16 * (mchunkB ^ 1);
   const float s = sa[0] * sb[0];
 
   // ---- persistent: work item `it` (a tile and a K split) goes to workgroup it % gridDim.x. The grid is a multiple
@@ -188,6 +199,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     int m0, n0, split, kbeg, kend, nk;
     v4i rA, rB;   // buffer descriptors over the item's rows of A and B (rows past M / N read as zero)
     int voA, voB; // MN-major: this lane's load offsets, or kOOB where its chunk lies past M / N
+    int voA1, voB1; // the same for K rows with bit 5 set
   };
   auto item = [&](int it) {
     Item w;
@@ -207,10 +219,12 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       w.rB = buffer_rsrc(B + w.n0, K * ldb - w.n0);
       w.voA = w.m0 + 16 * mchunk < M ? baseA : kOOB;
       w.voB = w.n0 + 16 * mchunkB < N ? baseB : kOOB;
+      w.voA1 = w.m0 + 16 * (mchunk ^ 1) < M ? baseA1 : kOOB;
+      w.voB1 = w.n0 + 16 * (mchunkB ^ 1) < N ? baseB1 : kOOB;
     } else {
       w.rA = buffer_rsrc(A + (int64_t)w.m0 * lda, min(M - w.m0, kBM) * lda);
       w.rB = buffer_rsrc(B + (int64_t)w.n0 * ldb, min(N - w.n0, kBNt) * ldb);
-      w.voA = w.voB = 0;
+      w.voA = w.voB = w.voA1 = w.voB1 = 0;
     }
     return w;
   };
@@ -223,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     if constexpr (kMN && kBNt == 128) {
       if (!isA) {   // the narrow B K tile: K rows k0 + 32 i + mrowB, 128 bytes each
         const int R0 = (i * kLoaders + (wave & 3)) * 8;
-        const int vo = w.voB + i * opaque(32 * ldb);
+        const int vo = ((i & 1) ? w.voB1 : w.voB) + i * opaque(32 * ldb);   // (K row bit 5 = i & 1)
         const uint32_t to = lds_addr(smem) + dst + R0 * 128;
         if (!kTail || k0 + kBK <= w.kend) lds_dma16(w.rB, vo, k0 * ldb, to);
         else lds_dma16(w.rB, k0 + 32 * i + mrowB < w.kend ? vo + k0 * ldb : kOOB, 0, to);
@@ -236,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       const int ld = isA ? lda : ldb;
       const int R0 = (i * kLoaders + (wave & 3)) * 4;
       // (kOOB + these offsets stays in [2^31, 2^32): still past the range, which is below 2^31)
-      const int vo = (isA ? w.voA : w.voB) + i * opaque(16 * ld);
+      const int vo = ((i & 2) ? (isA ? w.voA1 : w.voB1) : (isA ? w.voA : w.voB)) + i * opaque(16 * ld);   // (bit 5 = i & 2)
       const uint32_t to = lds_addr(smem) + dst + R0 * 256;
       if (!kTail || k0 + kBK <= w.kend) lds_dma16(isA ? w.rA : w.rB, vo, k0 * ld, to);
       else lds_dma16(isA ? w.rA : w.rB, k0 + 16 * i + mrow < w.kend ? vo + k0 * ld : kOOB, 0, to);
@@ -264,51 +278,50 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     }
   };
 
-  // ---- fragments of one K tile: 32 x 32 x 64 operands, row (lane & 31), 32 bytes at K 64 * step + 32 * (lane >> 5).
-  // Fragment j = 6 * step + f: f < kTM is A fragment f, otherwise B fragment f - kTM; two ds_read_b128 each.
-  v8i fa[2][kTM], fb[2][kTNt];
-  const int frow = lane & 31;
+  // ---- fragments of one K tile: 16 x 16 x 128 operands, row (lane & 15), 32 bytes at K 32 * (lane >> 4).
+  // Fragment j: j < kTM is A fragment j, otherwise B fragment j - kTM; two ds_read_b128 each.
+  v8i fa[kTM], fb[kTNt];
+  const int frow = lane & 15;
   const int fsw = swz(frow);                 // swz of every fragment row: the tile offsets are multiples of 16
-  const int c0 = 2 * (lane >> 5);
+  const int c0 = 2 * (lane >> 4);
   // MN-major: a fragment is 4 ds_read_b64_tr_b8. In each 16-lane group g = lane / 16, source lane s = lane % 16 reads
-  // 8 bytes of K row 32 (g / 2) + 8 q + s / 2 (+ 64 step), MN bytes mnb + 16 (g % 2) + 8 (s % 2) + [0, 8); the
-  // transposing read hands output lane j of the group byte r of source lane 2 r + j / 8, i.e. K row 8 q + r of MN
-  // index mnb + 16 (g % 2) + j: lane l gets MN index mnb + (l & 31) and K 32 (l / 32) + 8 q + [0, 8) in bytes
-  // 8 q .. 8 q + 7 of its operand -- the layout of the K-major fragment. The chunk index (mnb / 16 + g % 2) ^ 2 (s / 2)
-  // equals (mnb / 16) ^ tr_x since mnb / 16 is even.
+  // 8 bytes of K row 32 g + 8 q + s / 2, MN bytes mnb + 8 (s % 2) + [0, 8); the transposing read hands output lane j
+  // of the group byte r of source lane 2 r + j / 8, i.e. K row 32 g + 8 q + r of MN index mnb + j: lane l gets MN
+  // index mnb + (l & 15) and K 32 (l / 16) + 8 q + [0, 8) in bytes 8 q .. 8 q + 7 of its operand -- the layout of the
+  // K-major fragment. The chunk mnb / 16 of K row 32 g + 8 q + s / 2 sits in slot (mnb / 16) ^ mn_swz(row), and
+  // mn_swz of those rows does not depend on q.
   const int tr_g = lane >> 4, tr_s = lane & 15;
-  const int tr_row = 32 * (tr_g >> 1) + (tr_s >> 1);
+  const int tr_row = 32 * tr_g + (tr_s >> 1);
   const int tr_off = tr_row * 256 + 8 * (tr_s & 1);
-  const int tr_x = 16 * ((tr_g & 1) | mn_swz(tr_row));
-  // (the narrow tile's B: rows of 128 bytes, chunk (mnb / 16 + g % 2) ^ mn_swz_n(row), mn_swz_n even as well)
+  const int tr_x = 16 * mn_swz(tr_row);
+  // (the narrow tile's B: rows of 128 bytes, chunk (mnb / 16) ^ mn_swz_n(row))
   const int tr_offB = kBNt == 256 ? tr_off : tr_row * 128 + 8 * (tr_s & 1);
-  const int tr_xB = kBNt == 256 ? tr_x : 16 * ((tr_g & 1) | mn_swz_n(tr_row));
+  const int tr_xB = kBNt == 256 ? tr_x : 16 * mn_swz_n(tr_row);
   auto read_frag = [&](int ast, int bst, int j) {
-    const int step = j / (kTM + kTNt), f = j % (kTM + kTNt);
+    const int f = j;
     if constexpr (kMN) {
-      const int mnb = f < kTM ? wm * kWTM + f * 32 : wn * kWTNt + (f - kTM) * 32;
+      const int mnb = f < kTM ? wm * kWTM + f * 16 : wn * kWTNt + (f - kTM) * 16;
       const int rowb = f < kTM ? 256 : kBNt;   // bytes per K row of the operand's K tile
       const GPIC_LDS uint8_t *p =
-          kBNt == 256 ? (const GPIC_LDS uint8_t *)smem + (f < kTM ? a_half(ast) : b_half(bst)) + step * 64 * 256 +
-                            tr_off + (mnb ^ tr_x)
-                      : (const GPIC_LDS uint8_t *)smem + step * 64 * rowb +
+          kBNt == 256 ? (const GPIC_LDS uint8_t *)smem + (f < kTM ? a_half(ast) : b_half(bst)) + tr_off + (mnb ^ tr_x)
+                      : (const GPIC_LDS uint8_t *)smem +
                             (f < kTM ? a_half(ast) + tr_off + (mnb ^ tr_x) : b_half(bst) + tr_offB + (mnb ^ tr_xB));
       v2i r[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) r[q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GPIC_LDS v2i *)(p + q * 8 * rowb));
       const v8i v{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
-      if (f < kTM) fa[step][f] = v;
-      else fb[step][f - kTM] = v;
+      if (f < kTM) fa[f] = v;
+      else fb[f - kTM] = v;
       return;
     }
-    const int lo = 16 * ((4 * step + c0) ^ fsw), hi = 16 * ((4 * step + c0 + 1) ^ fsw);
+    const int lo = 16 * (c0 ^ fsw), hi = 16 * ((c0 + 1) ^ fsw);
     const GPIC_LDS uint8_t *p = (const GPIC_LDS uint8_t *)smem +
-                                (f < kTM ? a_half(ast) + (wm * kWTM + f * 32 + frow) * kBK
-                                         : b_half(bst) + (wn * kWTNt + (f - kTM) * 32 + frow) * kBK);
+                                (f < kTM ? a_half(ast) + (wm * kWTM + f * 16 + frow) * kBK
+                                         : b_half(bst) + (wn * kWTNt + (f - kTM) * 16 + frow) * kBK);
     const u32x4 x0 = *(const GPIC_LDS u32x4 *)(p + lo), x1 = *(const GPIC_LDS u32x4 *)(p + hi);
     const v8i v{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-    if (f < kTM) fa[step][f] = v;
-    else fb[step][f - kTM] = v;
+    if (f < kTM) fa[f] = v;
+    else fb[f - kTM] = v;
   };
   // A memory phase: the wave's 12 fragment reads of K tile (ast, bst), with its 8 loads of one operand's later K
   // tile between them when `send`. A load issue waits while the texture unit's queue is full; with the reads in
@@ -316,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
   // (The narrow tile: 8 fragment reads, with the 8 A or 4 B loads spread evenly between them.)
   auto mem_phase = [&](const Item &w, int ast, int bst, bool send, bool isA, int dst, int k0) {
     if constexpr (kBNt == 256) {
-      static_assert(2 * (kTM + kTNt) == 12 && kLoads == 8 && kLoadsB == 8, "interleave pattern: 3 fragments per 2 loads");
+      static_assert(kTM + kTNt == 12 && kLoads == 8 && kLoadsB == 8, "interleave pattern: 3 fragments per 2 loads");
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         read_frag(ast, bst, 3 * j);
@@ -326,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
         if (send) load(w, isA, dst, k0, 2 * j + 1);
       }
     } else {
-      constexpr int R = 2 * (kTM + kTNt);
+      constexpr int R = kTM + kTNt;
 #pragma unroll
       for (int j = 0; j < R; j++) {
         read_frag(ast, bst, j);
@@ -373,19 +386,19 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
     }
   };
-  constexpr int kStoresBF16 = kTM * kTNt * 2;         // bf16 epilogue: 16 (narrow: 8) buffer stores per wave, always issued
-  constexpr int kStoresF32 = kTNt * kTM * 4;          // split-K partials: 32 (narrow: 16)
+  constexpr int kStoresBF16 = (kTM / 2) * (32 * kRowB / 1024);   // bf16 epilogue: 16 (narrow: 8) buffer stores per wave, always issued
+  constexpr int kStoresF32 = kTNt * kTM;                         // split-K partials: 32 (narrow: 16)
 
   int it = blockIdx.x;
   Item cur = item(it);
   if (group == 0) send_prologue(cur);
   int pend = 0;   // stores group 0 issued after the current item's prologue loads
   for (;;) {
-    v16f acc[kTNt][kTM];
+    v4f acc[kTNt][kTM];
 #pragma unroll
     for (int i = 0; i < kTNt; i++)
 #pragma unroll
-      for (int j = 0; j < kTM; j++) acc[i][j] = v16f{};
+      for (int j = 0; j < kTM; j++) acc[i][j] = v4f{};
 
     // K tile t: A half in A stage t % 3, B half in B stage t % 2. Group 0 reads tile kt in phase 2 kt and multiplies
     // in 2 kt + 1; group 1 reads it in 2 kt + 1 and multiplies in 2 kt + 2. The loads are spread over both kinds of
@@ -418,13 +431,10 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
       phase_barrier();
       // MFMA phase
 #pragma unroll
-      for (int step = 0; step < 2; step++)
+      for (int ni = 0; ni < kTNt; ni++)
 #pragma unroll
-        for (int ni = 0; ni < kTNt; ni++)
-#pragma unroll
-          for (int mi = 0; mi < kTM; mi++)
-            acc[ni][mi] =
-                __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[step][ni], fa[step][mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
+        for (int mi = 0; mi < kTM; mi++)
+          acc[ni][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fb[ni], fa[mi], acc[ni][mi], 0, 0, 0, 0, 0, 0);
       if (group == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // B(kt + 1) (and A(1)) have landed
       phase_barrier();
       ast = ast == 2 ? 0 : ast + 1;
@@ -437,41 +447,35 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
     const bool more = nit < work;
     if (more && group == 0) send_prologue(item(nit));
 
-    // ---- epilogue: acc[ni][mi] lane l holds C[m][n] for m = mi * 32 + (l & 31) and, through col_of,
-    // n = ni * 32 + 16 * (r / 8) + 8 * (l >> 5) + r % 8, r = 0..15: two runs of 8 consecutive columns, each one
-    // 16-byte bf16 store (or two fp32 ones) straight from the accumulators; the lanes l and l + 32 of a row fill 32
-    // contiguous bytes of it. Every store is a buffer store issued by every wave (lanes outside M x N get an offset
-    // past the descriptor's range and write nothing), so group 0 knows exactly how many stores follow its prologue
-    // loads.
+    // ---- epilogue: acc[ni][mi] lane l holds C[m][n + v], v = 0..3, for m = mi * 16 + (l & 15) and, through col_of,
+    // n = 32 (ni / 2) + 8 (l >> 4) + 4 (ni % 2) (MN-major, in natural order: n = 16 ni + 4 (l >> 4)): 4 consecutive
+    // columns per tile, a run of 8 per pair of tiles in the K-major instance. Every store is a buffer store issued by
+    // every wave (lanes outside M x N get an offset past the descriptor's range and write nothing), so group 0 knows
+    // exactly how many stores follow its prologue loads.
     const int el = opaque_v(lane);
     const int rows_c = min(M - cur.m0, kBM);
-    const int wr = el & 31, wh = el >> 5;
+    const int wr = el & 15, wg = el >> 4;
     if (P) {   // split-K fp32 partials
       const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(P + ((int64_t)cur.split * M + cur.m0) * N), 0, rows_c * N * 4, kBufferFlags);
 #pragma unroll
       for (int ni = 0; ni < kTNt; ni++)
 #pragma unroll
-        for (int mi = 0; mi < kTM; mi++)
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int r = wm * kWTM + mi * 32 + wr;
-            const int n = cur.n0 + wn * kWTNt + ni * 32 +
-                          (kMN ? 8 * q + 4 * wh : 16 * (q >> 1) + 8 * wh + 4 * (q & 1));
-            const v16f &v = acc[ni][mi];
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(u32x4, v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}), rP,
-                r < rows_c && n < N ? (r * N + n) * 4 : kOOB, 0, 0);
-          }
+        for (int mi = 0; mi < kTM; mi++) {
+          const int r = wm * kWTM + mi * 16 + wr;
+          const int n = cur.n0 + wn * kWTNt + (kMN ? 16 * ni + 4 * wg : 32 * (ni >> 1) + 8 * wg + 4 * (ni & 1));
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[ni][mi]), rP,
+                                                 r < rows_c && n < N ? (r * N + n) * 4 : kOOB, 0, 0);
+        }
       pend = kStoresF32;
     } else {
       // bf16 output through LDS: each lane rounds its runs of 8 columns (scaled) to bf16 and writes them to LDS as
-      // 16 bytes, one 32 x 128 block (an mi tile row) of the wave at a time; each lane then reads back 16 bytes of
-      // one row, adds the bias (a second rounding, as the reference) and stores them, 16 lanes to a 256-byte row
-      // segment of C. A block row is 256 bytes; 16-byte chunk c of row r sits in slot c ^ (r & 15) (conflict-free
-      // both ways). Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in B stage 1. The next item's
-      // prologue loads go to A stages 0, 1 and B stage 0; the first loads into A stage 2 and B stage 1 come after the
-      // next item's first barrier, which group 1 reaches only when its epilogue is done.
+      // 16 bytes (MN-major: its runs of 4 as 8 bytes), one 32 x 128 block (two 16-row tile rows) of the wave at a
+      // time; each lane then reads back 16 bytes of one row, adds the bias (a second rounding, as the reference) and
+      // stores them, 16 lanes to a 256-byte row segment of C. A block row is 256 bytes; 16-byte chunk c of row r sits
+      // in slot c ^ (r & 15) (conflict-free both ways). Each wave uses its own 8 KiB: group 0 in A stage 2, group 1 in
+      // B stage 1. The next item's prologue loads go to A stages 0, 1 and B stage 0; the first loads into A stage 2
+      // and B stage 1 come after the next item's first barrier, which group 1 reaches only when its epilogue is done.
       // The narrow tile's block rows are 128 bytes (8 chunks): chunk c of row r sits in slot c ^ ((r / 2) & 7), so the
       // 16 lanes of a write (rows r..r+15 at one chunk) or of a read-back (two rows) cover all 64 banks.
       GPIC_LDS uint8_t *cst =
@@ -488,25 +492,27 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
         b[0] = b0.x, b[1] = b0.y, b[2] = b1.x, b[3] = b1.y;
       }
 #pragma unroll
-      for (int mi = 0; mi < kTM; mi++) {
+      for (int mq = 0; mq < kTM / 2; mq++) {
 #pragma unroll
-        for (int ni = 0; ni < kTNt; ni++) {
-          const v16f &v = acc[ni][mi];
+        for (int h2 = 0; h2 < 2; h2++) {   // the block's two 16-row tile rows
+          const int mi = 2 * mq + h2, row = 16 * h2 + wr;
           if constexpr (kMN) {
-            // natural column order: runs of 4 (columns 32 ni + 8 q + 4 wh + [0, 4)), 8 bytes each, into half
-            // wh ^ (wr / 16) of the chunk (rows wr and wr + 16 share a slot: the halves keep them apart)
+            // natural column order: a run of 4 (columns 16 ni + 4 wg + [0, 4)) per tile, 8 bytes into half wg % 2 of
+            // chunk 2 ni + wg / 2
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-              *(GPIC_LDS st8_t *)(cst + wr * kRowB + 16 * slot(4 * ni + q, wr) + 8 * (wh ^ (wr >> 4))) =
-                  st8_t{pack_bf16(v[4 * q] * s, v[4 * q + 1] * s), pack_bf16(v[4 * q + 2] * s, v[4 * q + 3] * s)};
+            for (int ni = 0; ni < kTNt; ni++) {
+              const v4f &v = acc[ni][mi];
+              *(GPIC_LDS st8_t *)(cst + row * kRowB + 16 * slot(2 * ni + (wg >> 1), row) + 8 * (wg & 1)) =
+                  st8_t{pack_bf16(v[0] * s, v[1] * s), pack_bf16(v[2] * s, v[3] * s)};
+            }
           } else {
+            // tiles 2 p and 2 p + 1: columns 32 p + 8 wg + [0, 8), chunk 4 p + wg
 #pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-              st16_t w;
-#pragma unroll
-              for (int e = 0; e < 4; e++)
-                w[e] = pack_bf16(v[8 * hh + 2 * e] * s, v[8 * hh + 2 * e + 1] * s);
-              *(GPIC_LDS st16_t *)(cst + wr * kRowB + 16 * slot(4 * ni + 2 * hh + wh, wr)) = w;
+            for (int pp = 0; pp < kTNt / 2; pp++) {
+              const v4f &a = acc[2 * pp][mi], &b2 = acc[2 * pp + 1][mi];
+              *(GPIC_LDS st16_t *)(cst + row * kRowB + 16 * slot(4 * pp + wg, row)) =
+                  st16_t{pack_bf16(a[0] * s, a[1] * s), pack_bf16(a[2] * s, a[3] * s), pack_bf16(b2[0] * s, b2[1] * s),
+                         pack_bf16(b2[2] * s, b2[3] * s)};
             }
           }
         }
@@ -520,12 +526,11 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const uint8_t *__rest
           wv[j] = *(const GPIC_LDS st16_t *)(cst + r * kRowB + 16 * slot(rc, r));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read back before the next block overwrites it
-        const int rl0 = wm * kWTM + mi * 32 + rr;   // row within the tile of j = 0; row j is rl0 + kRPI j
+        const int rl0 = wm * kWTM + mq * 32 + rr;   // row within the tile of j = 0; row j is rl0 + kRPI j
         int off = (rl0 * (int)ldc + n) * 2;
 #pragma unroll
         for (int j = 0; j < kNI; j++) {
           st16_t w = wv[j];
-          if (kMN && kRPI * j >= 16) w = st16_t{w[2], w[3], w[0], w[1]};   // rows 16..31: halves exchanged
           if (bias) {   // bf16(bf16(acc * s) + bias)
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = pack_bf16(bf16_lo(w[e]) + bf16_lo(b[e]), bf16_hi(w[e]) + bf16_hi(b[e]));

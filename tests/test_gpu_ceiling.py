@@ -1,7 +1,8 @@
-"""The MFMA ceiling measurement (tests/hip/mfma_ceiling.hip): every SIMD issuing v_mfma_f32_32x32x64_f8f6f4 back to
-back on LDS-fed operands. Checks that the loop is MFMA-bound cycle for cycle and that its FLOP rate agrees with the
-clock the waves measured; prints the rates on constant and on random e4m3 operands (random ones draw enough power
-that the clock drops: that rate, not the published peak, is what a GEMM on real data can reach)."""
+"""The MFMA ceiling measurement (tests/hip/mfma_ceiling.hip): every SIMD issuing FP8 MFMAs back to back, in the
+16 x 16 x 128 form the GEMM uses and in the 32 x 32 x 64 form. Checks that the loop is MFMA-bound cycle for cycle and
+that its FLOP rate agrees with the clock the waves measured; prints the rates on constant and on random e4m3 operands
+(random ones draw enough power that the clock drops: that rate, not the published peak, is what a GEMM on real data
+can reach)."""
 import ctypes
 import os
 
@@ -9,30 +10,40 @@ import pytest
 import torch
 
 LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "hip", "libmfma_ceiling.so")
-FLOPS_PER_MFMA = 2 * 32 * 32 * 64
-CYCLES_PER_MFMA = 64
+FLOPS_PER_CYCLE_PER_SIMD = 2 * 32 * 32 * 64 / 64    # either form: 2048 FP8 FLOP per cycle and SIMD
 
 
-def probe(random, steps=8000):
+def probe(shape, random, src=None, steps=8000):
     lib = ctypes.CDLL(LIB)
     d = ctypes.c_double
-    lib.gpic_probe_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.POINTER(d)] * 4
+    lib.gpic_probe_mfma_ceiling.argtypes = ([ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int] +
+                                            [ctypes.POINTER(d)] * 4)
     ms, tf, ghz, busy = d(), d(), d(), d()
-    rc = lib.gpic_probe_mfma_ceiling(int(random), steps, ms, tf, ghz, busy)
+    rc = lib.gpic_probe_mfma_ceiling(shape, int(random), None if src is None else src.data_ptr(),
+                                     0 if src is None else src.numel(), steps, ms, tf, ghz, busy)
     assert rc == 0, rc
     return ms.value, tf.value, ghz.value, busy.value
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("random", [False, True], ids=["const", "random"])
-def test_mfma_ceiling(random):
+@pytest.mark.parametrize("shape", [16, 32], ids=["16x16x128", "32x32x64"])
+@pytest.mark.parametrize("data", ["const", "random", "tcast"])
+def test_mfma_ceiling(shape, data):
     if not os.path.exists(LIB):
         pytest.fail(f"{LIB} is missing: run __graft_entry__.build()")
     torch.cuda.init()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    ms, tf, ghz, busy = probe(random)
-    print(f"\n{'random' if random else 'const'} e4m3: {tf:.0f} TFLOP/s, clock {ghz:.2f} GHz, MFMA busy {busy:.3f} "
-          f"({ms:.2f} ms)", flush=True)
-    assert busy > 0.95                       # the loop issues an MFMA every 64 cycles on every SIMD
-    expect = ghz * 1e9 * busy * cus * 4 * FLOPS_PER_MFMA / CYCLES_PER_MFMA / 1e12
+    src = None
+    if data == "tcast":   # the e4m3 bytes of an N(0, 1) tensor, as a GEMM's operands
+        import gpic_fp8 as G
+        g = torch.Generator(device="cuda").manual_seed(0)
+        src = G.tcast(torch.randn(2048, 4096, generator=g, device="cuda").to(torch.bfloat16))[0].view(torch.uint8)
+    ms, tf, ghz, busy = probe(shape, data == "random", src)
+    print(f"\n{shape}x{shape}x{2048 // shape} {data} e4m3: {tf:.0f} TFLOP/s, clock {ghz:.2f} GHz, "
+          f"MFMA busy {busy:.3f} ({ms:.2f} ms)", flush=True)
+    assert busy > 0.95                       # the loop keeps every SIMD's MFMA pipe busy
+    expect = ghz * 1e9 * busy * cus * 4 * FLOPS_PER_CYCLE_PER_SIMD / 1e12
     assert abs(tf / expect - 1) < 0.05, (tf, expect)
+
+    with pytest.raises(AssertionError):      # a form the probe does not know is refused
+        probe(24, False, None, 2)
