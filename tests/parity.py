@@ -37,11 +37,13 @@ def ref_fp32(a, sa, b, sb):
     return (a.float() * float(sa)) @ (b.float() * float(sb)).t()
 
 
-# The FP8 MFMA (v_mfma_*_f8f6f4) does not sum the 64 products of one instruction exactly: with a few large products
-# in a block (activations with x50 outlier channels) the result of a single instruction (K = 64) was measured up to
-# 1.6e-4 of the sum of |terms| away from the exact sum, and hipBLASLt's FP8 GEMM gives the same errors on the same
-# operands. Data without such outliers stays within 2^-16 of the sum of |terms|. OUTLIER_SLACK is the allowance for
-# operands with outlier channels (3x the largest error measured).
+# The FP8 MFMA (v_mfma_*_f8f6f4) does not sum the products of one instruction exactly: with a few large products in
+# a block (activations with x50 outlier channels) the result of a single 32 x 32 x 64 instruction (K = 64) was measured
+# up to 1.6e-4 of the sum of |terms| away from the exact sum, and hipBLASLt's FP8 GEMM gives the same errors on the
+# same operands; the 16 x 16 x 128 form the GEMM now uses (K = 128 per instruction) showed the same largest errors as
+# two 32 x 32 x 64 instructions on the same random and outlier blocks. Data without such outliers stays within 2^-16
+# of the sum of |terms|. OUTLIER_SLACK is the allowance for operands with outlier channels (3x the largest error
+# measured).
 OUTLIER_SLACK = 2.0 ** -11
 
 
