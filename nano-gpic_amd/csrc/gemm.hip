@@ -7,9 +7,10 @@
 //  * Macro tile 256 x 256 x 128 per workgroup of 8 waves, two per SIMD. Wave w owns the 64 x 128 sub-tile
 //    (rows 64 * (w >> 1), columns 128 * (w & 1)) as 4 x 8 MFMA tiles of v_mfma_f32_16x16x128_f8f6f4, one instruction
 //    per tile and K tile (both operands e4m3, fp32 accumulators in VGPRs, so the epilogue's VALU work reads them
-//    without AGPR copies). The 16 x 16 x 128 form does the 32 x 32 x 64 form's work per cycle at lower power: on random
-//    e4m3 operands an MFMA-only loop held the clock at 1.87-1.95 GHz against 1.59-1.68 (3.9-4.1 against 3.3-3.5
-//    PFLOP/s), and this kernel is power-bound on real data.
+//    without AGPR copies). The 16 x 16 x 128 form does the 32 x 32 x 64 form's work per cycle at lower power, and this
+//    kernel is power-bound on real data: repeated back-to-back MFMA-only loops on random e4m3 operands held the clock
+//    at 1.87-1.95 GHz against 1.59-1.68 (single runs: within ~3%); this kernel, 20 calls per d12 shape, ran each shape
+//    0.13-0.24 GHz faster and in 3-5% less time than with the 32 x 32 x 64 form.
 //  * A narrow class, 256 x 128, for shapes whose 256 x 256 tiles leave CUs idle: each wave then owns 64 x 64, the B
 //    K tile is 16 KiB; the host picks the width and the K split per shape, the same for both operand layouts.
 //  * Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share the SIMDs pairwise and run one phase apart. In each
