@@ -98,6 +98,8 @@ int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8
  *   z        [M, 2H] bf16, row stride sz (H % 8 == 0, sz % 8 == 0)
  *   q        [M, H] e4m3 of a = bf16(bf16(z1 * sigmoid(z1)) * z2), row stride sq (sq % 8 == 0)
  *   dequant  1 fp32
+ * With sq == H and a product of at most 96 MiB (on 256 CUs) one single-pass launch (see gpic_fp8_tcast: the
+ * workspace carries its call counter); otherwise an amax pass and a cast pass that recomputes the product.
  */
 int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, float *dequant,
                           void *ws, void *stream);
@@ -118,9 +120,11 @@ int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_
  * M..ldt-1 zero): the K-major operand of w3's FP8 wgrad. Same bytes and scale as gpic_fp8_swiglu_tcast.
  *   a  [M, H] bf16, contiguous, or NULL: when given, the SwiGLU product is written there by the amax pass and the
  *      cast reads it instead of recomputing it (the same bytes; faster: the product is computed once)
- *   qt may be NULL (then ldt == 0, and H % 8 == 0 suffices): q only. With `a` and sq == H the cast is a flat pass
- *      over the product -- the same bytes as gpic_fp8_swiglu_tcast, which recomputes the product instead (and is the
- *      slower of the two: measured 270 vs 225 us on d12's [32768, 8192]).
+ *   qt may be NULL (then ldt == 0, and H % 8 == 0 suffices): q only. With sq == H the single pass: one launch that
+ *      holds up to 96 MiB of the product on chip (on 256 CUs) and, given `a`, streams the rest through a -- up to 8x
+ *      that (d12's [32768, 8192]: 190 us against 246 for the amax pass writing a and a flat cast of it, flushed
+ *      caches); the same bytes as gpic_fp8_swiglu_tcast. With single-pass casts disabled (gpic_fp8_set_single_pass)
+ *      or past 8x: the two-pass casts, through `a` when given.
  * No counterpart in the reference (its w3 wgrad is bf16, fp8_native.py:225,265); the FP8-wgrad extension.
  */
 int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint16_t *a, uint8_t *q, int64_t sq,

@@ -1087,17 +1087,189 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
   }
 }
 
+// ------------------------------------------------------------------------------------------- single-pass SwiGLU
+
+// Single-pass SwiGLU product cast, flat (q [M, H] contiguous): one launch of one 1024-thread workgroup per CU. Word i
+// of the product (8 values: row i / (H / 8), columns 8 (i % (H / 8)) + [0, 8)) is computed from 16 bytes of z1 and
+// 16 of z2. The words go in groups of 1024, one word per thread; workgroup b takes groups j G + b, j = 0, 1, ...: at
+// each step the grid reads one contiguous window of z. Groups j < wpt are held as bf16 until the fold: j < kSwHeldR in
+// registers, the rest in LDS (128 KiB beside the 24 KiB sigmoid table; 96 MiB over 256 CUs). A product larger than the
+// grid holds is a hybrid: the sgroups groups
+// past wpt G are streamed -- computed, taken into the maximum and written to `a`; after the fold read back, last
+// first, and cast. Moved per element: 4 B of z read and 1 B of q written, plus 2 B written and 2 B read back for the
+// streamed part (the two-pass cast: 4 + 2 + 2 + 1).
+constexpr int kSwThreads = 1024;   // 16 waves, 4 per SIMD: at most 128 VGPRs each
+constexpr int kSwHeldR = 16;       // product words a thread holds in registers (64 VGPRs)
+constexpr int kSwHeldL = 8;        // product words a thread holds in LDS (128 KiB per workgroup)
+constexpr int kSwHeld = kSwHeldR + kSwHeldL;
+constexpr int kSwBatch = 2;        // words whose z loads are issued together (4 spills at 128 VGPRs)
+constexpr int kSwHybrid = 8;   // the single pass takes products up to this many times what the grid holds
+static_assert(kSwHeldR % kSwBatch == 0 && kSwHeldL % kSwBatch == 0, "a batch lies in registers or in LDS");
+
+// Row and 8-column unit of product word i, stepped along words a fixed distance apart: one division at the start,
+// then per step an add and at most one wrap (the step's remainder is below `units`).
+struct SwCursor {
+  uint32_t r, u;
+  __device__ __forceinline__ SwCursor(uint32_t i, uint32_t units) : r(i / units), u(i % units) {}
+  __device__ __forceinline__ void step(uint32_t dq, uint32_t dr, uint32_t units) {
+    r += dq;
+    u += dr;
+    if (u >= units) {
+      u -= units;
+      r++;
+    }
+  }
+};
+
+// nw = M H / 8 product words (below 2^31: the host bounds it); a is needed only when sgroups > 0.
+__global__ __launch_bounds__(kSwThreads) void swiglu_once_kernel(const uint16_t *__restrict__ z, int64_t H, int64_t sz,
+                                                                  uint32_t nw, int wpt, uint32_t sgroups,
+                                                                  uint16_t *__restrict__ a, uint8_t *__restrict__ q,
+                                                                  float *__restrict__ dequant, void *ws,
+                                                                  uint32_t wait_ticks) {
+  __shared__ float lut[kLutLds];
+  __shared__ u32x4 held[kSwHeldL * kSwThreads];
+  lut_build(lut);
+  const uint32_t t = threadIdx.x, units = (uint32_t)(H / 8), G = gridDim.x;
+  const uint32_t base_s = G * kSwThreads * (uint32_t)wpt;   // the first streamed word
+  // word of thread t in held group j of workgroup b
+  auto hword = [&](uint32_t b, int j) { return ((uint32_t)j * G + b) * kSwThreads + t; };
+  const u32x4 zero{0u, 0u, 0u, 0u};
+  auto zp = [&](uint32_t r, uint32_t u) { return z + (int64_t)r * sz + 8 * u; };
+  auto ld = [](const uint16_t *p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p)); };
+  auto product = [&](uint32_t i) {
+    const uint32_t r = i / units;
+    const uint16_t *p = zp(r, i - r * units);
+    return swiglu8_words(lut, ld(p), ld(p + H));
+  };
+
+  // held words, kSwBatch at a time: loads branch-free (a word past the product reads z's first word and is then
+  // zeroed), products kept (registers, then LDS) and folded into m. The 16 waves of the workgroup overlap one
+  // another's loads and arithmetic (2 waves per SIMD holding twice the words, with a software pipeline: 3.7 TB/s
+  // against ~6 here).
+  u32x4 w[kSwHeldR];
+#pragma unroll
+  for (int j = 0; j < kSwHeldR; j++) w[j] = zero;
+  uint32_t m = 0;
+  {
+    SwCursor c(hword(blockIdx.x, 0), units);
+    const uint32_t d = kSwThreads * G, dq = d / units, dr = d % units;
+#pragma unroll
+    for (int j0 = 0; j0 < kSwHeld; j0 += kSwBatch) {
+      if (j0 < wpt) {   // (a small product: fewer words per thread)
+        u32x4 z1[kSwBatch], z2[kSwBatch];
+        bool ok[kSwBatch];
+#pragma unroll
+        for (int k = 0; k < kSwBatch; k++) {
+          ok[k] = j0 + k < wpt && hword(blockIdx.x, j0 + k) < nw;
+          const uint16_t *p = ok[k] ? zp(c.r, c.u) : z;
+          z1[k] = ld(p);
+          z2[k] = ld(p + H);
+          c.step(dq, dr, units);
+        }
+        u32x4 A[kSwBatch];
+#pragma unroll
+        for (int k = 0; k < kSwBatch; k++)
+          A[k] = swiglu8_words(lut, ok[k] ? z1[k] : zero, ok[k] ? z2[k] : zero);   // zero words: zero products
+        m = max(m, words_amax<uint16_t, kSwBatch>(A));
+#pragma unroll
+        for (int k = 0; k < kSwBatch; k++) {
+          if (j0 + k < kSwHeldR) w[j0 + k] = A[k];
+          else held[(j0 + k - kSwHeldR) * kSwThreads + t] = A[k];
+        }
+      }
+    }
+  }
+  // hybrid: this workgroup's streamed groups s = b, b + G, ..., computed, folded into m and written to a
+  if (blockIdx.x < sgroups) {
+    SwCursor c(base_s + kSwThreads * blockIdx.x + t, units);
+    const uint32_t d = kSwThreads * G, dq = d / units, dr = d % units;
+    for (uint32_t s0 = blockIdx.x; s0 < sgroups; s0 += kSwBatch * G) {
+      u32x4 z1[kSwBatch], z2[kSwBatch];
+      bool ok[kSwBatch];
+#pragma unroll
+      for (int k = 0; k < kSwBatch; k++) {
+        const uint32_t s = s0 + k * G, i = base_s + kSwThreads * s + t;
+        ok[k] = s < sgroups && i < nw;
+        const uint16_t *p = zp(c.r, c.u);
+        z1[k] = ok[k] ? ld(p) : zero;
+        z2[k] = ok[k] ? ld(p + H) : zero;
+        c.step(dq, dr, units);
+      }
+      u32x4 A[kSwBatch];
+#pragma unroll
+      for (int k = 0; k < kSwBatch; k++) A[k] = swiglu8_words(lut, z1[k], z2[k]);
+      m = max(m, words_amax<uint16_t, kSwBatch>(A));
+#pragma unroll
+      for (int k = 0; k < kSwBatch; k++)
+        if (ok[k]) reinterpret_cast<u32x4 *>(a)[base_s + kSwThreads * (s0 + k * G) + t] = A[k];
+    }
+  }
+
+  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int cb) {
+    uint32_t v = 0;
+    for (int j = 0; j < wpt; j++) {
+      const uint32_t i = hword((uint32_t)cb, j);
+      if (i < nw) v = max(v, word_amax_exact<uint16_t>(product(i)));
+    }
+    for (uint32_t s = cb; s < sgroups; s += G) {
+      const uint32_t i = base_s + kSwThreads * s + t;
+      if (i < nw) v = max(v, word_amax_exact<uint16_t>(product(i)));
+    }
+    return block_max_u32(v);
+  });
+  hold(w);
+  float scale, deq;
+  scales_from_amax(g, scale, deq);
+  if (blockIdx.x == 0 && t == 0) *dequant = deq;
+  u32x2 *qv = reinterpret_cast<u32x2 *>(q);
+  const uint32_t b2 = (uint32_t)opaque_s64(blockIdx.x);   // store addresses recomputed, not kept from the loads
+#pragma unroll
+  for (int j = 0; j < kSwHeldR; j++) {
+    const uint32_t i = hword(b2, j);
+    if (j < wpt && i < nw) __builtin_nontemporal_store(cast8_bf16(w[j], scale), qv + i);
+  }
+  if (wpt > kSwHeldR) {
+    u32x4 L[kSwHeldL];
+#pragma unroll
+    for (int j = 0; j < kSwHeldL; j++) L[j] = held[j * kSwThreads + t];
+#pragma unroll
+    for (int j = 0; j < kSwHeldL; j++) {
+      const uint32_t i = hword(b2, kSwHeldR + j);
+      if (kSwHeldR + j < wpt && i < nw) __builtin_nontemporal_store(cast8_bf16(L[j], scale), qv + i);
+    }
+  }
+  // hybrid: the streamed groups back from a, this workgroup's last first, kStream loads in flight
+  if (blockIdx.x < sgroups) {
+    const u32x4 *av = reinterpret_cast<const u32x4 *>(a);
+    const int64_t cnt = (sgroups - 1 - blockIdx.x) / G + 1;
+    for (int64_t k0 = cnt - 1; k0 >= 0; k0 -= kStream) {
+      u32x4 S[kStream];
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const uint32_t i = base_s + kSwThreads * (uint32_t)(blockIdx.x + (k0 - k) * G) + t;
+        S[k] = k0 - k >= 0 && i < nw ? __builtin_nontemporal_load(av + i) : zero;
+      }
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const uint32_t i = base_s + kSwThreads * (uint32_t)(blockIdx.x + (k0 - k) * G) + t;
+        if (k0 - k >= 0 && i < nw) __builtin_nontemporal_store(cast8_bf16(S[k], scale), qv + i);
+      }
+    }
+  }
+}
+
 // Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and
 // the wait bound in microseconds. Atomic: a call on another thread reads either the old or the new setting.
 static std::atomic<int> g_once_enabled{1};
 static std::atomic<int> g_once_wait_us{kOnceWaitUs};
 
-// Workgroups of `kernel` (256 threads) the current device holds at once, capped at kMaxOnceBlocks; cached per device
-// in `cache` (one per kernel, slots initialised to -1).
-int once_capacity(const void *kernel, DeviceCache &cache) {
-  return per_device(cache, [kernel](int dev) {
+// Workgroups of `kernel` (`threads` threads each) the current device holds at once, capped at kMaxOnceBlocks; cached
+// per device in `cache` (one per kernel, slots initialised to -1).
+int once_capacity(const void *kernel, DeviceCache &cache, int threads) {
+  return per_device(cache, [kernel, threads](int dev) {
     int per = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess) per = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess) per = 0;
     (void)hipGetLastError();
     return std::min(per * device_cus(dev), kMaxOnceBlocks);
   });
@@ -1108,10 +1280,10 @@ uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(st
 
 bool once_enabled() { return g_once_enabled.load(std::memory_order_relaxed) != 0; }
 
-static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t;
+static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw;
 struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
   DeviceCacheInit() {
-    for (int i = 0; i < kMaxDevices; i++) g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = -1;
+    for (int i = 0; i < kMaxDevices; i++) g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = -1;
   }
 };
 static DeviceCacheInit g_device_cache_init;
@@ -1120,7 +1292,7 @@ static DeviceCacheInit g_device_cache_init;
 template <typename T>
 static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant, void *ws, hipStream_t st) {
   const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T>),
-                                sizeof(T) == 2 ? g_cap_flat_bf16 : g_cap_flat_f32);
+                                sizeof(T) == 2 ? g_cap_flat_bf16 : g_cap_flat_f32, 256);
   constexpr int kE = 16 / sizeof(T);
   const int64_t nw = n / kE;
   const int64_t held = (int64_t)kOnceWords<T> * 256 * cap;   // words the grid holds in registers
@@ -1137,10 +1309,34 @@ static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant,
   return true;
 }
 
+// The single-pass SwiGLU product cast of z [M, 2H] (row stride sz) into q [M, H] contiguous, when the product fits the
+// grid, or as a hybrid up to kSwHybrid times that when the product buffer `a` is given (false, nothing launched,
+// otherwise).
+static bool launch_swiglu_once(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint16_t *a, uint8_t *q,
+                               float *dequant, void *ws, hipStream_t st) {
+  const int cap = once_capacity(reinterpret_cast<const void *>(&swiglu_once_kernel), g_cap_sw, kSwThreads);
+  const int64_t nw = M * (H / 8);
+  const int64_t held = (int64_t)kSwHeld * kSwThreads * cap;   // words the grid holds
+  if (!once_enabled() || cap <= 0 || nw <= 0 || nw > kSwHybrid * held) return false;
+  if (nw > held) {   // hybrid: every workgroup holds its full share, the rest goes through a
+    if (!a) return false;
+    const int64_t sgroups = (nw - held + kSwThreads - 1) / kSwThreads;
+    swiglu_once_kernel<<<cap, kSwThreads, 0, st>>>(z, H, sz, (uint32_t)nw, kSwHeld, (uint32_t)sgroups, a, q, dequant,
+                                                   ws, once_wait_ticks());
+    return true;
+  }
+  const int64_t groups = (nw + kSwThreads - 1) / kSwThreads;   // groups of kSwThreads words
+  const int grid = (int)std::min<int64_t>(groups, cap);
+  const int wpt = (int)((groups + grid - 1) / grid);
+  swiglu_once_kernel<<<grid, kSwThreads, 0, st>>>(z, H, sz, (uint32_t)nw, wpt, 0u, a, q, dequant, ws,
+                                                  once_wait_ticks());
+  return true;
+}
+
 // The single-pass transposing cast of a bf16 source when it fits (false, nothing launched, otherwise).
 static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,
                                 float *dequant, void *ws, hipStream_t st) {
-  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), g_cap_t);
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_once_kernel), g_cap_t, 256);
   const int64_t tiles = ((cols + kTT - 1) / kTT) * ((ldt + kTT - 1) / kTT);
   if (!once_enabled() || cap <= 0 || tiles <= 0 || tiles > (int64_t)kHybridTiles * cap)
     return false;
@@ -1270,6 +1466,7 @@ int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, u
   if (H % 8 != 0 || sz % 8 != 0 || sq % 8 != 0 || sz < 2 * H || sq < H) return GPIC_ESHAPE;
   if (!aligned16(z) || !aligned16(q) || !aligned16(ws)) return GPIC_EALIGN;
   hipStream_t st = (hipStream_t)stream;
+  if (sq == H && launch_swiglu_once(z, M, H, sz, nullptr, q, dequant, ws, st)) return (int)hipGetLastError();
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
   swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws), nullptr);
@@ -1289,7 +1486,9 @@ int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz,
   hipStream_t st = (hipStream_t)stream;
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  if (!qt) {   // q only: with `a` (and q contiguous) the product is written once and cast flat; else recomputed
+  if (!qt) {   // q only, contiguous: the single pass (a hybrid through `a` when the product is larger than the grid
+               // holds); else, with `a`, the product written once and cast flat; else recomputed
+    if (sq == H && launch_swiglu_once(z, M, H, sz, a, q, dequant, ws, st)) return (int)hipGetLastError();
     const bool flat = a && sq == H;
     swiglu_amax_kernel<<<g, kCastThreads, 0, st>>>(z, M, H, sz, partial, ws_table(ws), flat ? a : nullptr);
     if (flat) {

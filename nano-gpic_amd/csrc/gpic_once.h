@@ -118,10 +118,10 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wai
   return g;
 }
 
-// Host side (cast.hip): workgroups of `kernel` (256 threads) the current device holds at once, capped at
+// Host side (cast.hip): workgroups of `kernel` (`threads` threads each) the current device holds at once, capped at
 // kMaxOnceBlocks and cached per device in `cache`; the wait bound in s_memrealtime ticks; whether single-pass
 // launches are enabled (gpic_fp8_set_single_pass).
-int once_capacity(const void *kernel, DeviceCache &cache);
+int once_capacity(const void *kernel, DeviceCache &cache, int threads);
 uint32_t once_wait_ticks();
 bool once_enabled();
 

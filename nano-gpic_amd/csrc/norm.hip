@@ -395,7 +395,7 @@ template <int kJ, bool kUni, bool kRes>
 static bool launch_norm_once_t(const NormArgs &p, void *ws, hipStream_t st) {
   constexpr int kR = kRowsOnce<kJ>;
   const int cap = once_capacity(reinterpret_cast<const void *>(&norm_q_once_kernel<kJ, kR, kUni, kRes>),
-                                g_cap_norm[kJ][kUni][kRes]);
+                                g_cap_norm[kJ][kUni][kRes], 256);
   const int64_t wgs = (p.rows + 4 * kR - 1) / (4 * kR);
   if (cap <= 0 || wgs > cap) return false;
   norm_q_once_kernel<kJ, kR, kUni, kRes><<<(int)wgs, 256, 0, st>>>(p, ws, once_wait_ticks());

@@ -111,8 +111,9 @@ def _swiglu_prep(z):
 @torch.library.custom_op("gpic::fp8_swiglu_tcast", mutates_args=())
 def swiglu_tcast(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """z [M, 2H] bf16 (w12's output) -> silu(z1) * z2 as e4m3 [M, H] and its tensorwise scale [1] fp32.
-    (fp8_native.py:130-144). The product goes through a temporary bf16 buffer (written by the amax pass, cast flat)
-    rather than being computed twice: gpic_fp8_swiglu_tcast_t with qt = NULL, the same bytes."""
+    (fp8_native.py:130-144). gpic_fp8_swiglu_tcast_t with qt = NULL: the single pass, which holds up to 96 MiB of the
+    product on chip and streams the rest through the temporary bf16 buffer; with single-pass casts disabled, the
+    product written to the buffer by the amax pass and cast flat. The same bytes either way."""
     zc = _swiglu_prep(z)
     M, H2 = zc.shape
     H = H2 // 2

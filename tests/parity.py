@@ -72,3 +72,24 @@ def sample_rows(m, n, seed):
     r = torch.randperm(m, generator=g)[:n]
     r[0], r[1] = 0, m - 1
     return torch.unique(r)
+
+
+# The single-pass casts write their tagged partial maxima from byte 28672 of the cast workspace (one 64-bit word per
+# workgroup, the call tag in the high half), count partials a workgroup had to compute from x itself at byte 36864,
+# keep the last call's tag (the epoch) at byte 36868, the groups of 32 workgroups of a call that are done folding at
+# byte 36872 and each group's count of its workgroups done from byte 40960, one word every 128 bytes (cast.hip:
+# kOnceTagged, kOnceFallback, kOnceEpoch, kOnceDone, kOnceGroupDone).
+ONCE_WORD0, ONCE_FALLBACK, ONCE_EPOCH, ONCE_DONE = 28672 // 8, 36864 // 4, 36868 // 4, 36872 // 4
+ONCE_GROUP_DONE = [(40960 + 128 * g) // 4 for g in range(32)]
+
+
+def once_state(dev):
+    """(workgroup 0's tagged partial word, the count of partials computed by waiters) after the stream's work."""
+    from gpic_fp8 import _lib as L
+    ws = L.cast_workspace(dev)
+    torch.cuda.synchronize()
+    w0 = int(ws.view(torch.int64)[ONCE_WORD0].item())
+    # after a single-pass call the epoch holds its tag (the high half of workgroup 0's word) and the counter is back to 0
+    assert int(ws[ONCE_DONE].item()) == 0 and not ws[ONCE_GROUP_DONE].any()
+    assert int(ws[ONCE_EPOCH].item()) & 0xffffffff == (w0 >> 32) & 0xffffffff or w0 == 0
+    return w0, int(ws[ONCE_FALLBACK].item())

@@ -106,9 +106,9 @@ def test_bwd_matches_oracle(dev, M, H):
 
 @pytest.mark.parametrize("M,H", [(300, 512), (33, 8), (4096, 4096)])
 def test_flat_product_cast_paths_agree(dev, M, H):
-    """The three flat product casts give the same bytes and scale: the op's (the product written once to a buffer,
-    then cast flat), gpic_fp8_swiglu_tcast (the product recomputed by the cast) and gpic_fp8_swiglu_tcast_t with
-    qt = NULL, with no buffer and with a buffer but a strided q (both recompute). H = 8 leaves a flat tail."""
+    """The flat product casts give the same bytes and scale: the op's, gpic_fp8_swiglu_tcast (no product buffer) and
+    gpic_fp8_swiglu_tcast_t with qt = NULL and no buffer -- all three the single pass here -- and
+    gpic_fp8_swiglu_tcast_t into a strided q (the two-pass cast recomputing the product). H = 8: one word per row."""
     from gpic_fp8 import _lib as L
     z = rand_bf16((M, 2 * H), 3.0, seed=M + 3 * H).to(dev)
     q0, s0 = G.swiglu_tcast(z)
@@ -131,6 +131,96 @@ def test_flat_product_cast_paths_agree(dev, M, H):
         assert torch.equal(q, q0.view(torch.uint8)), mode
     oq, od, _ = O.swiglu_tcast(bits(z))
     assert s0.item() == od and np.array_equal(qb(q0), oq)
+
+
+@pytest.fixture
+def single_pass_default():
+    from gpic_fp8 import _lib as L
+    L.set_single_pass(True, -1)
+    yield
+    L.set_single_pass(True, -1)
+
+
+# (M, H): one workgroup; rows of 130 words across groups of 1024; 8 words per thread (registers only); the grid's
+# exact capacity on 256 CUs (24 words per thread, 8 of them in LDS); hybrids at 1.33x, d12 (2.67x) and d18 (4.67x)
+# past it.
+@pytest.mark.parametrize("M,H", [(33, 64), (4100, 1040), (4096, 4096), (12288, 4096), (16384, 4096), (32768, 4096),
+                                 (32768, 7168)])
+def test_single_pass_product_cast(dev, M, H, single_pass_default):
+    """The single-pass product cast (one launch: the product held in registers and LDS, past the grid's capacity
+    streamed through the product buffer) against the forced two-pass path and the zero-wait path (a partial not yet
+    published is computed by the waiting workgroup from z, streamed part included): the same bytes and scale, with a
+    NaN product (excluded from the amax) and an outlier planted; the call writes a new tag. Up to 12288 rows also
+    against the oracle; gpic_fp8_swiglu_tcast (no product buffer) agrees wherever the product fits."""
+    from gpic_fp8 import _lib as L
+    from parity import once_state
+    g = torch.Generator(device=dev).manual_seed(M + H)
+    z = (torch.randn(M, 2 * H, generator=g, device=dev) * 2).to(torch.bfloat16)
+    z[M // 3, H // 5] = float("nan")                   # z1 NaN: a NaN product
+    z[M - 1, 2 * H - 1] = 300.0                         # z2 outlier: the largest product
+    outs = []
+    for enabled, wait in ((True, -1), (True, 0), (False, -1)):
+        L.set_single_pass(enabled, wait)
+        w0, f0 = once_state(dev)
+        q, s = G.swiglu_tcast(z)
+        w1, f1 = once_state(dev)
+        if enabled:
+            assert w1 >> 32 != w0 >> 32                  # the single pass ran
+        else:
+            assert w1 == w0
+        if enabled and wait == 0 and M * H // 8 > 512:
+            assert f1 > f0                               # the direct computation did run (more than one workgroup)
+        outs.append((q.view(torch.uint8).clone(), s.item()))
+        del q
+    L.set_single_pass(True, -1)
+    q0, s0 = outs[0]
+    for q, s in outs[1:]:
+        assert s == s0 and torch.equal(q, q0)
+    if M * H <= 4096 * 12288:
+        oq, od, _ = O.swiglu_tcast(bits(z))
+        assert s0 == od and np.array_equal(q0.cpu().numpy(), oq)
+    if M * H // 8 <= 12288 * 512:
+        q = torch.zeros(M, H, dtype=torch.uint8, device=dev)
+        s = torch.empty(1, device=dev)
+        assert L.lib().gpic_fp8_swiglu_tcast(z.data_ptr(), M, H, 2 * H, q.data_ptr(), H, s.data_ptr(),
+                                             L.cast_workspace(dev).data_ptr(), L.stream_ptr(dev)) == 0
+        assert s.item() == s0 and torch.equal(q, q0)
+
+
+def test_single_pass_product_cast_beside_a_persistent_gemm(dev, single_pass_default):
+    """The single-pass product cast (one 1024-thread workgroup per CU, all of its LDS) on one stream while a
+    persistent GEMM holds every CU from another: its workgroups start only as the GEMM's leave, the bounded waits run
+    out and missing partials are computed from z. Every result equals the one computed alone, for a product that fits
+    and one that streams, issued before, during and after the GEMMs."""
+    g = torch.Generator(device=dev).manual_seed(29)
+    zs = [(torch.randn(m, 8192, generator=g, device=dev) * (1 + i)).to(torch.bfloat16)
+          for i, m in enumerate((4096, 16384))]
+    ref = [G.swiglu_tcast(z) for z in zs]
+    a = torch.randn(32768, 1024, generator=g, device=dev).to(torch.bfloat16)
+    b = (torch.randn(8192, 1024, generator=g, device=dev) / 32).to(torch.bfloat16)
+    aq, sa = G.tcast(a)
+    bq, sb = G.tcast(b)
+    y0 = G.fp8_gemm(aq, sa, bq, sb)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    outs, ys = [], []
+    for order in range(2):
+        if order == 0:          # casts first, the GEMMs right behind them
+            with torch.cuda.stream(s2):
+                outs += [G.swiglu_tcast(z) for z in zs]
+            with torch.cuda.stream(s1):
+                ys += [G.fp8_gemm(aq, sa, bq, sb) for _ in range(2)]
+        else:                   # GEMMs first
+            with torch.cuda.stream(s1):
+                ys += [G.fp8_gemm(aq, sa, bq, sb) for _ in range(2)]
+            with torch.cuda.stream(s2):
+                outs += [G.swiglu_tcast(z) for z in zs]
+        torch.cuda.synchronize()
+    for i, (q, s) in enumerate(outs):
+        rq, rs = ref[i % 2]
+        assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8)), i
+    for y in ys:
+        assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
 
 
 def test_transposing_variants(dev):
