@@ -539,7 +539,11 @@ def main():
     sw_held = min(M_TOK * H * 2, 384 * 1024 * torch.cuda.get_device_properties(dev).multi_processor_count)
     sw_min = M_TOK * H * 5
     sw_moved = sw_min + 2 * (M_TOK * H * 2 - sw_held)
-    swb_min, swb_moved = M_TOK * H * 8, M_TOK * H * 14            # min: read z, da, write dzq; as built: z, da twice
+    # backward dz cast, min: read z, da, write dzq; as built: the single pass holds 320 KiB of dz per CU (read once)
+    # and reads z and da twice for the rest
+    swb_held = min(M_TOK * H * 4, 320 * 1024 * torch.cuda.get_device_properties(dev).multi_processor_count)
+    swb_min = M_TOK * H * 8
+    swb_moved = swb_min + (M_TOK * H * 4 - swb_held) * 6 // 4
 
     # ---- the norm sites' producer with the cast folded in: site 1 (RMSNorm + modulation -> qkv_x) and site 2 (x + gate
     # * a, RMSNorm + modulation -> the MLP) at d12, h's e4m3 bytes from the norm kernel (fused) against the norm

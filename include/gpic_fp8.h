@@ -110,7 +110,10 @@ int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, u
  *   z [M, 2H] (row stride sz), da [M, H] (row stride sda) bf16 ->
  *   dz [M, 2H] bf16 contiguous, dzq [M, 2H] e4m3 contiguous, dequant 1 fp32
  *   dz may be NULL: dz is not written and dzq is cast from dz recomputed from z and da (the same bytes; less memory
- *      traffic than writing dz and reading it back) -- for a caller whose weight gradient takes dzq, not dz.
+ *      traffic than writing dz and reading it back) -- for a caller whose weight gradient takes dzq, not dz. Then one
+ *      single-pass launch (see gpic_fp8_tcast: the workspace carries its call counter) holds up to 80 MiB of dz on
+ *      chip (on 256 CUs) and computes the rest twice, up to 16x that (d12's [32768, 4096]: 307 us against 336 for an
+ *      amax pass and a recomputing cast pass, flushed caches); beyond, or with single-pass casts disabled, the latter.
  */
 int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                         uint16_t *dz, uint8_t *dzq, float *dequant, void *ws, void *stream);

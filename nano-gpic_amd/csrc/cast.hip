@@ -1259,6 +1259,189 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_once_kernel(const uint16_t 
   }
 }
 
+// Single-pass SwiGLU backward cast without dz in memory (dzq [M, 2H] contiguous): one launch of one 1024-thread
+// workgroup per CU. Unit i (row i / (H / 8), columns 8 (i % (H / 8)) + [0, 8) of each half) takes 16 bytes each of
+// z1, z2 and da and gives two dz words (d1, d2: 8 bf16 each, dz_words). Units go in groups of 1024, one per thread;
+// workgroup b takes groups j G + b. Groups j < wpt are held as dz words until the fold: j < kBwHeldR in registers,
+// the rest in LDS (128 KiB beside the 24 KiB sigmoid table; 80 MiB of dz over 256 CUs). Past that (sgroups further
+// groups) the units are computed for the maximum only and computed again from z and da after the fold, as the
+// two-pass cast does. Moved per unit: 48 B read and 16 B written held, 96 B read and 16 B written streamed (the
+// two-pass cast: 96 + 16).
+constexpr int kBwHeldR = 6;     // units a thread holds in registers (2 words each: 48 VGPRs)
+constexpr int kBwHeldL = 4;     // units a thread holds in LDS (128 KiB per workgroup)
+constexpr int kBwHeld = kBwHeldR + kBwHeldL;
+constexpr int kBwBatch = 2;     // units whose loads are issued together
+constexpr int kBwHybrid = 16;   // the single pass takes up to this many times what the grid holds (d18: 11x)
+static_assert(kBwHeldR % kBwBatch == 0 && kBwHeldL % kBwBatch == 0, "a batch lies in registers or in LDS");
+
+// nu = M H / 8 units (below 2^31: the host bounds it).
+__global__ __launch_bounds__(kSwThreads) void swiglu_bwd_once_kernel(const uint16_t *__restrict__ z,
+                                                                      const uint16_t *__restrict__ da, int64_t H,
+                                                                      int64_t sz, int64_t sda, uint32_t nu, int wpt,
+                                                                      uint32_t sgroups, uint8_t *__restrict__ dzq,
+                                                                      float *__restrict__ dequant, void *ws,
+                                                                      uint32_t wait_ticks) {
+  __shared__ float lut[kLutLds];
+  __shared__ u32x4 held[2 * kBwHeldL * kSwThreads];
+  lut_build(lut);
+  const uint32_t t = threadIdx.x, units = (uint32_t)(H / 8), G = gridDim.x;
+  const uint32_t base_s = G * kSwThreads * (uint32_t)wpt;   // the first streamed unit
+  const u32x4 zero{0u, 0u, 0u, 0u};
+  auto hunit = [&](uint32_t b, int j) { return ((uint32_t)j * G + b) * kSwThreads + t; };
+  auto ld = [](const uint16_t *p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p)); };
+  // the three input words of the unit at (r, u), or of unit 0 when !ok (then zeroed by the caller)
+  auto load3 = [&](bool ok, uint32_t r, uint32_t u, u32x4 &z1, u32x4 &z2, u32x4 &d) {
+    const uint16_t *zr = ok ? z + (int64_t)r * sz + 8 * u : z;
+    z1 = ld(zr);
+    z2 = ld(zr + H);
+    d = ld(ok ? da + (int64_t)r * sda + 8 * u : da);
+  };
+  auto dz_of = [&](uint32_t i, u32x4 &h1, u32x4 &h2) {
+    const uint32_t r = i / units, u = i - r * units;
+    u32x4 z1, z2, d;
+    load3(true, r, u, z1, z2, d);
+    dz_words(lut, z1, z2, d, h1, h2);
+  };
+
+  // held units, kBwBatch at a time: loads branch-free, dz kept (registers, then LDS) and folded into m
+  u32x4 w1[kBwHeldR], w2[kBwHeldR];
+#pragma unroll
+  for (int j = 0; j < kBwHeldR; j++) w1[j] = w2[j] = zero;
+  uint32_t m = 0;
+  {
+    SwCursor c(hunit(blockIdx.x, 0), units);
+    const uint32_t d = kSwThreads * G, dq = d / units, dr = d % units;
+#pragma unroll
+    for (int j0 = 0; j0 < kBwHeld; j0 += kBwBatch) {
+      if (j0 < wpt) {   // (a small tensor: fewer units per thread)
+        u32x4 Z1[kBwBatch], Z2[kBwBatch], D[kBwBatch];
+        bool ok[kBwBatch];
+#pragma unroll
+        for (int k = 0; k < kBwBatch; k++) {
+          ok[k] = j0 + k < wpt && hunit(blockIdx.x, j0 + k) < nu;
+          load3(ok[k], c.r, c.u, Z1[k], Z2[k], D[k]);
+          c.step(dq, dr, units);
+        }
+        u32x4 Hh[2 * kBwBatch];
+#pragma unroll
+        for (int k = 0; k < kBwBatch; k++)
+          dz_words(lut, ok[k] ? Z1[k] : zero, ok[k] ? Z2[k] : zero, ok[k] ? D[k] : zero, Hh[2 * k], Hh[2 * k + 1]);
+        m = max(m, words_amax<uint16_t, 2 * kBwBatch>(Hh));   // zero inputs: zero dz
+#pragma unroll
+        for (int k = 0; k < kBwBatch; k++) {
+          const int j = j0 + k;
+          if (j < kBwHeldR) {
+            w1[j] = Hh[2 * k];
+            w2[j] = Hh[2 * k + 1];
+          } else {
+            held[(2 * (j - kBwHeldR)) * kSwThreads + t] = Hh[2 * k];
+            held[(2 * (j - kBwHeldR) + 1) * kSwThreads + t] = Hh[2 * k + 1];
+          }
+        }
+      }
+    }
+  }
+  // hybrid: this workgroup's streamed groups s = b, b + G, ..., computed and folded into m (not kept)
+  if (blockIdx.x < sgroups) {
+    SwCursor c(base_s + kSwThreads * blockIdx.x + t, units);
+    const uint32_t d = kSwThreads * G, dq = d / units, dr = d % units;
+    for (uint32_t s0 = blockIdx.x; s0 < sgroups; s0 += kBwBatch * G) {
+      u32x4 Z1[kBwBatch], Z2[kBwBatch], D[kBwBatch];
+      bool ok[kBwBatch];
+#pragma unroll
+      for (int k = 0; k < kBwBatch; k++) {
+        const uint32_t s = s0 + k * G;
+        ok[k] = s < sgroups && base_s + kSwThreads * s + t < nu;
+        load3(ok[k], c.r, c.u, Z1[k], Z2[k], D[k]);
+        c.step(dq, dr, units);
+      }
+      u32x4 Hh[2 * kBwBatch];
+#pragma unroll
+      for (int k = 0; k < kBwBatch; k++)
+        dz_words(lut, ok[k] ? Z1[k] : zero, ok[k] ? Z2[k] : zero, ok[k] ? D[k] : zero, Hh[2 * k], Hh[2 * k + 1]);
+      m = max(m, words_amax<uint16_t, 2 * kBwBatch>(Hh));
+    }
+  }
+
+  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int cb) {
+    uint32_t v = 0;
+    for (int j = 0; j < wpt; j++) {
+      const uint32_t i = hunit((uint32_t)cb, j);
+      if (i < nu) {
+        u32x4 h1, h2;
+        dz_of(i, h1, h2);
+        v = max(v, max(word_amax_exact<uint16_t>(h1), word_amax_exact<uint16_t>(h2)));
+      }
+    }
+    for (uint32_t s = cb; s < sgroups; s += G) {
+      const uint32_t i = base_s + kSwThreads * s + t;
+      if (i < nu) {
+        u32x4 h1, h2;
+        dz_of(i, h1, h2);
+        v = max(v, max(word_amax_exact<uint16_t>(h1), word_amax_exact<uint16_t>(h2)));
+      }
+    }
+    return block_max_u32(v);
+  });
+  hold(w1);
+  hold(w2);
+  float scale, deq;
+  scales_from_amax(g, scale, deq);
+  if (blockIdx.x == 0 && t == 0) *dequant = deq;
+  auto out = [&](uint32_t i) {   // dzq bytes of unit i's d1 (d2: + H)
+    const uint32_t r = i / units;
+    return dzq + (int64_t)r * 2 * H + 8 * (i - r * units);
+  };
+  auto emit = [&](uint32_t i, u32x4 h1, u32x4 h2) {
+    uint8_t *o = out(i);
+    __builtin_nontemporal_store(cast8_bf16(h1, scale), reinterpret_cast<u32x2 *>(o));
+    __builtin_nontemporal_store(cast8_bf16(h2, scale), reinterpret_cast<u32x2 *>(o + H));
+  };
+  const uint32_t b2 = (uint32_t)opaque_s64(blockIdx.x);   // addresses recomputed, not kept from the loads
+#pragma unroll
+  for (int j = 0; j < kBwHeldR; j++) {
+    const uint32_t i = hunit(b2, j);
+    if (j < wpt && i < nu) emit(i, w1[j], w2[j]);
+  }
+  if (wpt > kBwHeldR) {
+    u32x4 L1[kBwHeldL], L2[kBwHeldL];
+#pragma unroll
+    for (int j = 0; j < kBwHeldL; j++) {
+      L1[j] = held[(2 * j) * kSwThreads + t];
+      L2[j] = held[(2 * j + 1) * kSwThreads + t];
+    }
+#pragma unroll
+    for (int j = 0; j < kBwHeldL; j++) {
+      const uint32_t i = hunit(b2, kBwHeldR + j);
+      if (kBwHeldR + j < wpt && i < nu) emit(i, L1[j], L2[j]);
+    }
+  }
+  // hybrid: the streamed groups again, this workgroup's last first, dz computed again from z and da and cast
+  if (blockIdx.x < sgroups) {
+    const int64_t cnt = (sgroups - 1 - blockIdx.x) / G + 1;
+    for (int64_t k0 = cnt - 1; k0 >= 0; k0 -= kBwBatch) {
+      u32x4 Z1[kBwBatch], Z2[kBwBatch], D[kBwBatch];
+      bool ok[kBwBatch];
+      uint32_t ii[kBwBatch];
+#pragma unroll
+      for (int k = 0; k < kBwBatch; k++) {
+        ii[k] = base_s + kSwThreads * (uint32_t)(blockIdx.x + (k0 - k) * G) + t;
+        ok[k] = k0 - k >= 0 && ii[k] < nu;
+        const uint32_t r = ok[k] ? ii[k] / units : 0u;
+        load3(ok[k], r, ok[k] ? ii[k] - r * units : 0u, Z1[k], Z2[k], D[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < kBwBatch; k++) {
+        if (ok[k]) {
+          u32x4 h1, h2;
+          dz_words(lut, Z1[k], Z2[k], D[k], h1, h2);
+          emit(ii[k], h1, h2);
+        }
+      }
+    }
+  }
+}
+
 // Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and
 // the wait bound in microseconds. Atomic: a call on another thread reads either the old or the new setting.
 static std::atomic<int> g_once_enabled{1};
@@ -1280,10 +1463,11 @@ uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(st
 
 bool once_enabled() { return g_once_enabled.load(std::memory_order_relaxed) != 0; }
 
-static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw;
+static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw;
 struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
   DeviceCacheInit() {
-    for (int i = 0; i < kMaxDevices; i++) g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = -1;
+    for (int i = 0; i < kMaxDevices; i++)
+      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = -1;
   }
 };
 static DeviceCacheInit g_device_cache_init;
@@ -1330,6 +1514,28 @@ static bool launch_swiglu_once(const uint16_t *z, int64_t M, int64_t H, int64_t 
   const int wpt = (int)((groups + grid - 1) / grid);
   swiglu_once_kernel<<<grid, kSwThreads, 0, st>>>(z, H, sz, (uint32_t)nw, wpt, 0u, a, q, dequant, ws,
                                                   once_wait_ticks());
+  return true;
+}
+
+// The single-pass SwiGLU backward cast of z [M, 2H], da [M, H] into dzq [M, 2H] contiguous (no dz), up to kBwHybrid
+// times what the grid holds (false, nothing launched, above).
+static bool launch_swiglu_bwd_once(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz,
+                                   int64_t sda, uint8_t *dzq, float *dequant, void *ws, hipStream_t st) {
+  const int cap = once_capacity(reinterpret_cast<const void *>(&swiglu_bwd_once_kernel), g_cap_bw, kSwThreads);
+  const int64_t nu = M * (H / 8);
+  const int64_t held = (int64_t)kBwHeld * kSwThreads * cap;   // units the grid holds
+  if (!once_enabled() || cap <= 0 || nu <= 0 || nu > kBwHybrid * held) return false;
+  int grid = cap, wpt = kBwHeld;
+  int64_t sgroups = 0;
+  if (nu > held) {   // hybrid: every workgroup holds its full share, the rest is computed twice
+    sgroups = (nu - held + kSwThreads - 1) / kSwThreads;
+  } else {
+    const int64_t groups = (nu + kSwThreads - 1) / kSwThreads;
+    grid = (int)std::min<int64_t>(groups, cap);
+    wpt = (int)((groups + grid - 1) / grid);
+  }
+  swiglu_bwd_once_kernel<<<grid, kSwThreads, 0, st>>>(z, da, H, sz, sda, (uint32_t)nu, wpt, (uint32_t)sgroups, dzq,
+                                                      dequant, ws, once_wait_ticks());
   return true;
 }
 
@@ -1516,7 +1722,8 @@ static int swiglu_bwd_common(const uint16_t *z, const uint16_t *da, int64_t M, i
                              hipStream_t st) {
   uint32_t *partial = static_cast<uint32_t *>(ws);
   const int g = swiglu_grid(M);
-  if (!dz && !dzqt) {   // dzq straight from z and da: an amax pass, then the recomputing flat cast
+  if (!dz && !dzqt) {   // dzq straight from z and da: the single pass, or an amax pass and the recomputing flat cast
+    if (launch_swiglu_bwd_once(z, da, M, H, sz, sda, dzq, dequant, ws, st)) return (int)hipGetLastError();
     swiglu_bwd_kernel<false><<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, nullptr, 0, partial, ws_table(ws));
     swiglu_bwd_cast_kernel<<<g, kCastThreads, 0, st>>>(z, da, M, H, sz, sda, partial, g, ws_table(ws), dzq, dequant);
     return (int)hipGetLastError();

@@ -200,8 +200,10 @@ def _(z, da):
 
 @torch.library.custom_op("gpic::fp8_swiglu_bwd_q", mutates_args=())
 def swiglu_bwd_q(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """swiglu_bwd without dz in memory: (dzq [M, 2H] e4m3, scale [1] fp32), the same bytes, cast from dz recomputed
-    from z and da -- for phase 3, whose w12 wgrad takes dzq instead of dz (an extension of the reference)."""
+    """swiglu_bwd without dz in memory: (dzq [M, 2H] e4m3, scale [1] fp32), the same bytes -- for phase 3, whose w12
+    wgrad takes dzq instead of dz (an extension of the reference). One single-pass launch holds up to 80 MiB of dz on
+    chip and computes the rest from z and da twice (for the amax, then for the cast); with single-pass casts disabled,
+    an amax pass and a cast pass that recomputes dz."""
     _, dq, s = _swiglu_bwd(z, da, False)
     return dq, s
 

@@ -187,15 +187,59 @@ def test_single_pass_product_cast(dev, M, H, single_pass_default):
         assert s.item() == s0 and torch.equal(q, q0)
 
 
-def test_single_pass_product_cast_beside_a_persistent_gemm(dev, single_pass_default):
-    """The single-pass product cast (one 1024-thread workgroup per CU, all of its LDS) on one stream while a
-    persistent GEMM holds every CU from another: its workgroups start only as the GEMM's leave, the bounded waits run
-    out and missing partials are computed from z. Every result equals the one computed alone, for a product that fits
-    and one that streams, issued before, during and after the GEMMs."""
+# (M, H): one workgroup; rows of 258 units across groups of 1024; 2 units per thread (registers only); the grid's
+# exact capacity on 256 CUs (10 units per thread, 4 of them in LDS); hybrids at 1.6x, d12 (6.4x) and d18 (11.2x) past
+# it.
+@pytest.mark.parametrize("M,H", [(33, 16), (1000, 2064), (8192, 512), (5120, 4096), (8192, 4096), (32768, 4096),
+                                 (32768, 7168)])
+def test_single_pass_bwd_cast(dev, M, H, single_pass_default):
+    """The single-pass cast of dz without dz in memory (one launch: dz held in registers and LDS, past the grid's
+    capacity computed for the maximum and again after the fold) against the forced two-pass path (an amax pass, then
+    the recomputing cast) and the zero-wait path: the same bytes and scale, with NaN and infinity planted in z and da;
+    the call writes a new tag. Up to 5120 x 4096 also against the oracle."""
+    from gpic_fp8 import _lib as L
+    from parity import once_state
+    g = torch.Generator(device=dev).manual_seed(M + 2 * H)
+    z = (torch.randn(M, 2 * H, generator=g, device=dev) * 2).to(torch.bfloat16)
+    da = (torch.randn(M, H, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    z[M // 3, H // 5] = float("nan")
+    da[M // 2, H - 1] = float("inf")
+    z[M - 1, 2 * H - 1] = 300.0
+    outs = []
+    for enabled, wait in ((True, -1), (True, 0), (False, -1)):
+        L.set_single_pass(enabled, wait)
+        w0, f0 = once_state(dev)
+        q, s = G.swiglu_bwd_q(z, da)
+        w1, f1 = once_state(dev)
+        if enabled:
+            assert w1 >> 32 != w0 >> 32                  # the single pass ran
+        else:
+            assert w1 == w0
+        if enabled and wait == 0 and M * H // 8 > 1024:
+            assert f1 > f0                               # the direct computation did run (more than one workgroup)
+        outs.append((q.view(torch.uint8).clone(), s.item()))
+        del q
+    L.set_single_pass(True, -1)
+    q0, s0 = outs[0]
+    for q, s in outs[1:]:
+        assert s == s0 and torch.equal(q, q0)
+    if M * H <= 5120 * 4096:
+        _, oq, od, _ = O.swiglu_bwd(bits(z), bits(da))
+        assert s0 == od and np.array_equal(q0.cpu().numpy(), oq)
+
+
+def test_single_pass_casts_beside_a_persistent_gemm(dev, single_pass_default):
+    """The single-pass SwiGLU casts (one 1024-thread workgroup per CU, all of its LDS) on one stream while a
+    persistent GEMM holds every CU from another: their workgroups start only as the GEMM's leave, the bounded waits
+    run out and missing partials are computed from z (and da). Every result equals the one computed alone -- product
+    casts of a product that fits and of one that streams, the backward's cast of a hybrid -- issued before and after
+    the GEMMs."""
     g = torch.Generator(device=dev).manual_seed(29)
     zs = [(torch.randn(m, 8192, generator=g, device=dev) * (1 + i)).to(torch.bfloat16)
           for i, m in enumerate((4096, 16384))]
-    ref = [G.swiglu_tcast(z) for z in zs]
+    da = (torch.randn(8192, 4096, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    calls = [lambda: G.swiglu_tcast(zs[0]), lambda: G.swiglu_tcast(zs[1]), lambda: G.swiglu_bwd_q(zs[1][:8192], da)]
+    ref = [f() for f in calls]
     a = torch.randn(32768, 1024, generator=g, device=dev).to(torch.bfloat16)
     b = (torch.randn(8192, 1024, generator=g, device=dev) / 32).to(torch.bfloat16)
     aq, sa = G.tcast(a)
@@ -207,17 +251,17 @@ def test_single_pass_product_cast_beside_a_persistent_gemm(dev, single_pass_defa
     for order in range(2):
         if order == 0:          # casts first, the GEMMs right behind them
             with torch.cuda.stream(s2):
-                outs += [G.swiglu_tcast(z) for z in zs]
+                outs += [f() for f in calls]
             with torch.cuda.stream(s1):
                 ys += [G.fp8_gemm(aq, sa, bq, sb) for _ in range(2)]
         else:                   # GEMMs first
             with torch.cuda.stream(s1):
                 ys += [G.fp8_gemm(aq, sa, bq, sb) for _ in range(2)]
             with torch.cuda.stream(s2):
-                outs += [G.swiglu_tcast(z) for z in zs]
+                outs += [f() for f in calls]
         torch.cuda.synchronize()
     for i, (q, s) in enumerate(outs):
-        rq, rs = ref[i % 2]
+        rq, rs = ref[i % len(calls)]
         assert s.item() == rs.item() and torch.equal(q.view(torch.uint8), rq.view(torch.uint8)), i
     for y in ys:
         assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
