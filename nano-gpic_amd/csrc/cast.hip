@@ -2,13 +2,15 @@
 // dgrad / wgrad operands), the SwiGLU product cast and the SwiGLU backward.
 //
 // Two designs, chosen per call by size:
-//  * Single pass (bf16 tensors of at most 64 MiB, fp32 of 48 MiB; hybrids up to 8x that): ONE launch. Each workgroup
-//    holds its share of x in registers, publishes a partial maximum tagged with the call's number, folds every
-//    workgroup's partial and casts from its registers (3 B/elem moved for bf16). The call number lives in the
+//  * Single pass (flat bf16 tensors of at most 100 MiB, fp32 of 48 MiB, transposing bf16 casts of 64 MiB; hybrids up
+//    to 8x that; the SwiGLU casts, whose limits are stated with their kernels): ONE launch. Each workgroup holds its
+//    share of x on chip, publishes a partial maximum tagged with the call's number, folds every workgroup's partial and
+//    casts from what it holds (3 B/elem moved for bf16). The call number lives in the
 //    workspace (an epoch word the last workgroup of each call advances), so the workspace carries state from call to
 //    call: it is zeroed once when created, and calls that may run at the same time (different streams) need
 //    different workspaces. Graph capture is fine: a replayed launch reads the epoch the previous call left.
-//  * Two passes (larger tensors, the SwiGLU kernels, fp32 transposing casts): two stream-ordered launches,
+//  * Two passes (larger tensors, the SwiGLU kernels past their single passes, fp32 transposing casts): two
+//    stream-ordered launches,
 //      1. an amax pass: each workgroup reduces its share to one partial maximum (|x| bit patterns, NaN ignored) and
 //         writes it to partial[blockIdx.x] -- no atomics, so nothing has to be zeroed beforehand;
 //      2. a cast pass: each workgroup folds all partials (<= kMaxParts words, served from L2), derives the scale with
@@ -1442,6 +1444,116 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_bwd_once_kernel(const uint1
   }
 }
 
+// Single-pass flat cast of a bf16 tensor above 48 MiB (cast_once_kernel holds 64 MiB): one 1024-thread workgroup per
+// CU, each thread holding kWideR words in registers and kWideL in LDS -- 400 KiB per CU, 100 MiB over 256 CUs. Words
+// go in groups of 1024, one per thread, workgroup b taking groups j G + b (j < wpt held); a larger x is a hybrid as in
+// cast_once_kernel: the sgroups groups past wpt G, workgroup s % G taking group s, are read for the maximum and read
+// again, last first, for the cast. The n % 8 tail elements: folded into every workgroup's partial, cast by workgroup 0.
+constexpr int kWideR = 16;   // words a thread holds in registers (64 VGPRs)
+constexpr int kWideL = 9;    // words a thread holds in LDS (144 KiB per workgroup)
+constexpr int kWide = kWideR + kWideL;
+
+__global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *__restrict__ x, int64_t n, int wpt,
+                                                                uint32_t sgroups, uint8_t *__restrict__ q,
+                                                                float *__restrict__ dequant, void *ws,
+                                                                uint32_t wait_ticks) {
+  __shared__ u32x4 held[kWideL * kSwThreads];
+  const uint32_t nw = (uint32_t)(n / 8), t = threadIdx.x, G = gridDim.x;
+  const int tail = (int)(n % 8);
+  const u32x4 *xv = reinterpret_cast<const u32x4 *>(x);
+  const uint32_t base_s = G * kSwThreads * (uint32_t)wpt;   // the first streamed word
+  const u32x4 zero{0u, 0u, 0u, 0u};
+  auto hword = [&](uint32_t b, int j) { return ((uint32_t)j * G + b) * kSwThreads + t; };
+  auto sword = [&](uint32_t s) { return base_s + kSwThreads * s + t; };
+  // branch-free: a word past x reads word 0 and is zeroed
+  auto ld = [&](bool ok, uint32_t i) {
+    const u32x4 v = __builtin_nontemporal_load(xv + (ok ? i : 0u));
+    return ok ? v : zero;
+  };
+  auto tail_amax = [&]() {
+    uint32_t a = 0;
+    if ((int)t < tail) {
+      a = __float_as_uint(bf16_lo(x[(int64_t)nw * 8 + t])) & 0x7fffffffu;
+      a = a <= 0x7f800000u ? a : 0u;
+    }
+    return a;
+  };
+  u32x4 w[kWideR], L[kWideL];
+#pragma unroll
+  for (int j = 0; j < kWideR; j++) w[j] = ld(j < wpt && hword(blockIdx.x, j) < nw, hword(blockIdx.x, j));
+#pragma unroll
+  for (int j = 0; j < kWideL; j++)
+    L[j] = ld(kWideR + j < wpt && hword(blockIdx.x, kWideR + j) < nw, hword(blockIdx.x, kWideR + j));
+  uint32_t m = max(max(words_amax<uint16_t, kWideR>(w), words_amax<uint16_t, kWideL>(L)), tail_amax());
+#pragma unroll
+  for (int j = 0; j < kWideL; j++) held[j * kSwThreads + t] = L[j];
+  // the streamed groups' maximum of workgroup b, kStream words in flight
+  auto stream_amax = [&](uint32_t b) {
+    uint32_t a = 0;
+    for (uint32_t s0 = b; s0 < sgroups; s0 += kStream * G) {
+      u32x4 S[kStream];
+#pragma unroll
+      for (int k = 0; k < kStream; k++) S[k] = ld(s0 + k * G < sgroups && sword(s0 + k * G) < nw, sword(s0 + k * G));
+      a = max(a, words_amax<uint16_t, kStream>(S));
+    }
+    return a;
+  };
+  if (blockIdx.x < sgroups) m = max(m, stream_amax(blockIdx.x));
+  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int cb) {
+    uint32_t a = tail_amax();
+    for (int j = 0; j < wpt; j++) {
+      const uint32_t i = hword((uint32_t)cb, j);
+      if (i < nw) a = max(a, word_amax_exact<uint16_t>(__builtin_nontemporal_load(xv + i)));
+    }
+    for (uint32_t s = cb; s < sgroups; s += G) {
+      const uint32_t i = sword(s);
+      if (i < nw) a = max(a, word_amax_exact<uint16_t>(__builtin_nontemporal_load(xv + i)));
+    }
+    return block_max_u32(a);
+  });
+  hold(w);
+  float scale, deq;
+  scales_from_amax(g, scale, deq);
+  if (blockIdx.x == 0 && t == 0) *dequant = deq;
+  u32x2 *qv = reinterpret_cast<u32x2 *>(q);
+  const uint32_t b2 = (uint32_t)opaque_s64(blockIdx.x);   // store addresses recomputed, not kept from the loads
+#pragma unroll
+  for (int j = 0; j < kWideR; j++) {
+    const uint32_t i = hword(b2, j);
+    if (j < wpt && i < nw) __builtin_nontemporal_store(cast8_bf16(w[j], scale), qv + i);
+  }
+  if (wpt > kWideR) {
+#pragma unroll
+    for (int j = 0; j < kWideL; j++) L[j] = held[j * kSwThreads + t];
+#pragma unroll
+    for (int j = 0; j < kWideL; j++) {
+      const uint32_t i = hword(b2, kWideR + j);
+      if (kWideR + j < wpt && i < nw) __builtin_nontemporal_store(cast8_bf16(L[j], scale), qv + i);
+    }
+  }
+  if (blockIdx.x == 0 && (int)t < tail) {
+    const int64_t i = (int64_t)nw * 8 + t;
+    q[i] = (uint8_t)e4m3x4(sat(bf16_lo(x[i]) * scale), 0.f, 0.f, 0.f);
+  }
+  // hybrid: the streamed groups again, this workgroup's last first, kStream loads in flight
+  if (blockIdx.x < sgroups) {
+    const int64_t cnt = (sgroups - 1 - blockIdx.x) / G + 1;
+    for (int64_t k0 = cnt - 1; k0 >= 0; k0 -= kStream) {
+      u32x4 S[kStream];
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const uint32_t i = sword((uint32_t)(blockIdx.x + (k0 - k) * G));
+        S[k] = ld(k0 - k >= 0 && i < nw, i);
+      }
+#pragma unroll
+      for (int k = 0; k < kStream; k++) {
+        const uint32_t i = sword((uint32_t)(blockIdx.x + (k0 - k) * G));
+        if (k0 - k >= 0 && i < nw) __builtin_nontemporal_store(cast8_bf16(S[k], scale), qv + i);
+      }
+    }
+  }
+}
+
 // Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and
 // the wait bound in microseconds. Atomic: a call on another thread reads either the old or the new setting.
 static std::atomic<int> g_once_enabled{1};
@@ -1463,11 +1575,11 @@ uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(st
 
 bool once_enabled() { return g_once_enabled.load(std::memory_order_relaxed) != 0; }
 
-static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw;
+static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw, g_cap_wide;
 struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
   DeviceCacheInit() {
     for (int i = 0; i < kMaxDevices; i++)
-      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = -1;
+      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = g_cap_wide[i] = -1;
   }
 };
 static DeviceCacheInit g_device_cache_init;
@@ -1480,7 +1592,29 @@ static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant,
   constexpr int kE = 16 / sizeof(T);
   const int64_t nw = n / kE;
   const int64_t held = (int64_t)kOnceWords<T> * 256 * cap;   // words the grid holds in registers
-  if (!once_enabled() || cap <= 0 || n <= 0 || nw > kHybridFlat * held) return false;
+  if (!once_enabled() || cap <= 0 || n <= 0) return false;
+  if constexpr (sizeof(T) == 2) {   // bf16 past 3/4 of what this kernel holds (48 MiB): the wide kernel, up to
+                                     // kHybridFlat x its hold (flushed caches: 64 MiB 23.8 us against 24.8, 32 MiB
+                                     // 18.3 against 16.4, 192 MiB 74 against 88 as this kernel's hybrid)
+    if (4 * nw > 3 * held) {
+      const int capw = once_capacity(reinterpret_cast<const void *>(&cast_wide_kernel), g_cap_wide, kSwThreads);
+      const int64_t heldw = (int64_t)kWide * kSwThreads * capw;
+      if (capw <= 0 || nw > kHybridFlat * heldw) return false;
+      int grid = capw, wpt = kWide;
+      int64_t sgroups = 0;
+      if (nw > heldw) {
+        sgroups = (nw - heldw + kSwThreads - 1) / kSwThreads;
+      } else {
+        const int64_t groups = (nw + kSwThreads - 1) / kSwThreads;
+        grid = (int)std::min<int64_t>(groups, capw);
+        wpt = (int)((groups + grid - 1) / grid);
+      }
+      cast_wide_kernel<<<grid, kSwThreads, 0, st>>>(reinterpret_cast<const uint16_t *>(x), n, wpt, (uint32_t)sgroups,
+                                                    q, dequant, ws, once_wait_ticks());
+      return true;
+    }
+  }
+  if (nw > kHybridFlat * held) return false;
   if (nw > held) {   // hybrid: every workgroup holds its full share, the rest is streamed
     const int64_t sgroups = (nw - held + 255) / 256;
     cast_once_kernel<T><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_wait_ticks());

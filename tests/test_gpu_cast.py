@@ -180,11 +180,12 @@ def single_pass_default():
 
 
 def test_single_pass_taken_when_the_tensor_fits(dev, single_pass_default):
-    """Config 2 ([32768 x 1024] bf16) fits the single-pass kernels (64 MiB held in registers): the flat and the
-    transposing cast each write new tagged partials and match the oracle; a tensor of 3x the size takes the flat
-    hybrid (held + streamed, new tags) with the oracle's bytes; one of 9x (past the hybrid's 8x) takes the two-pass
-    path (the partial words unchanged): three copies of the 3x tensor, so its bytes are three copies of the 3x result.
-    No partial had to be computed from x."""
+    """Config 2 ([32768 x 1024] bf16) fits the single-pass kernels (the flat cast's wide kernel holds 100 MiB in
+    registers and LDS, the transposing one 64 MiB in registers): the flat and the transposing cast each write new
+    tagged partials and match the oracle; a tensor of 3x the size takes the flat hybrid (held + streamed, new tags)
+    with the oracle's bytes; one of 15x (960 MiB, past the hybrid's 8 x 100 MiB) takes the two-pass path (the partial
+    words unchanged): five copies of the 3x tensor, so its bytes are five copies of the 3x result. No partial had to
+    be computed from x."""
     x = config2_input()
     xh = bits(x)
     oq, od, _ = O.tcast(xh)
@@ -205,12 +206,12 @@ def test_single_pass_taken_when_the_tensor_fits(dev, single_pass_default):
     assert w3 >> 32 != w2 >> 32 and f3 == f0
     oq, od, _ = O.tcast(bits(big.cpu()))
     assert s.item() == od and np.array_equal(qb(q), oq)
-    huge = big.repeat(1, 3)
+    huge = big.repeat(1, 5)
     qh, sh = G.tcast(huge)
     w4, f4 = once_state(dev)
     assert w4 == w3 and f4 == f0
     assert sh.item() == s.item()
-    assert torch.equal(qh.view(torch.uint8).view(32768, 3, 3072), q.view(torch.uint8).unsqueeze(1).expand(-1, 3, -1))
+    assert torch.equal(qh.view(torch.uint8).view(32768, 5, 3072), q.view(torch.uint8).unsqueeze(1).expand(-1, 5, -1))
 
 
 def test_single_pass_direct_fallback_and_two_pass_agree(dev, single_pass_default):
@@ -361,12 +362,16 @@ def test_single_pass_beside_a_persistent_gemm(dev, single_pass_default):
 
 
 @pytest.mark.parametrize("shape,dtype", [((32768, 3072), torch.bfloat16), ((41_000_009,), torch.bfloat16),
-                                         ((8192, 4096), torch.float32), ((4_194_304 * 8 * 8,), torch.bfloat16)])
+                                         ((100_000_007,), torch.bfloat16), ((8192, 4096), torch.float32),
+                                         ((6_553_600 * 8 * 8,), torch.bfloat16)])
 def test_flat_hybrid_matches_two_pass(dev, shape, dtype, single_pass_default):
-    """Flat casts above the single-pass capacity and up to 8x it take the hybrid (every workgroup holds its share,
-    the rest is streamed twice): the same bytes and scale as the forced two-pass path and as the zero-wait path
-    (missing partials, streamed part included, computed from x), with a NaN, an infinity and an odd tail; the
-    [32768 x 3072] dY of qkv and the exact 8x edge (268M elements) included, the first also against the oracle."""
+    """Flat bf16 casts above 48 MiB take the wide single-pass kernel (one 1024-thread workgroup per CU holding
+    100 MiB in registers and LDS), and past its capacity, up to 8x it, its hybrid (every workgroup holds its share,
+    the rest is streamed twice); fp32 above 48 MiB the 256-thread kernel's hybrid. The same bytes and scale as the
+    forced two-pass path and as the zero-wait path (missing partials, streamed part included, computed from x), with
+    a NaN, an infinity and an odd tail: the [32768 x 3072] dY of qkv (also against the oracle), 41M elements (held
+    whole, a tail of 1), 100M (a hybrid with a tail of 7), an fp32 weight-gradient-sized tensor and the wide hybrid's
+    exact 8x edge (419M elements, 800 MiB)."""
     g = torch.Generator(device=dev).manual_seed(len(shape) + shape[0])
     x = (torch.randn(*shape, generator=g, device=dev) * 4).to(dtype)
     flat = x.view(-1)
