@@ -87,6 +87,54 @@ def test_casts_replayed(dev, knob, xs, ws, wait):
         assert np.array_equal(qb(wqt)[:, :ws[0]], oq.T)
 
 
+@pytest.mark.parametrize("M", [2048, 16384])
+@pytest.mark.parametrize("wait", [-1, 0])
+def test_swiglu_casts_replayed(dev, knob, M, wait):
+    """The single-pass SwiGLU casts (the product cast and the backward's dz cast, H = 4096) captured on a stream that
+    has already run them and replayed 4 times with new z and da copied in (maxima alternating by orders of magnitude),
+    eager SwiGLU casts between the replays on the same stream: every replay equals the eager result of the same
+    inputs through the forced two-pass path. M = 2048 holds everything on chip; M = 16384 is a hybrid of both (the
+    product streamed through the op's buffer, dz computed twice); M = 2048 also against the oracle."""
+    H = 4096
+    L.set_single_pass(True, wait)
+    z = torch.empty(M, 2 * H, dtype=torch.bfloat16, device=dev)
+    da = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    fill(z, 1, 1.0)
+    fill(da, 2, 0.01)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            G.swiglu_tcast(z)
+            G.swiglu_bwd_q(z, da)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        aq, sa = G.swiglu_tcast(z)
+        dq, sd = G.swiglu_bwd_q(z, da)
+    zo = torch.randn(1024, 2 * H, device=dev).to(torch.bfloat16)
+    dao = torch.randn(1024, H, device=dev).to(torch.bfloat16)
+    for rep, scale in enumerate((1e2, 1e-2, 3e1, 2e-2)):
+        fill(z, 10 + rep, scale)
+        fill(da, 20 + rep, 1e-2 / scale)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+            G.swiglu_tcast(zo)             # eager work on the graph's workspace, in stream order
+            G.swiglu_bwd_q(zo, dao)
+        torch.cuda.synchronize()
+        L.set_single_pass(False, -1)
+        raq, rsa = G.swiglu_tcast(z)
+        rdq, rsd = G.swiglu_bwd_q(z, da)
+        L.set_single_pass(True, wait)
+        assert sa.item() == rsa.item() and torch.equal(aq.view(torch.uint8), raq.view(torch.uint8)), f"replay {rep}"
+        assert sd.item() == rsd.item() and torch.equal(dq.view(torch.uint8), rdq.view(torch.uint8)), f"replay {rep}"
+        if M == 2048:
+            oq, od, _ = O.swiglu_tcast(bits(z))
+            assert sa.item() == od and np.array_equal(qb(aq), oq), f"replay {rep}: product bytes differ"
+
+
 def test_cast_captured_on_a_new_stream(dev, knob):
     """A stream with no workspace yet: the workspace is created during the capture (from the capture's memory pool,
     its zero fill recorded as a kernel node that clears it again on each replay) and every replay still matches the
