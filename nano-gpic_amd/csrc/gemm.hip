@@ -109,7 +109,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // LDS DMA: lane j loads 16 bytes at buffer offset voffset + soffset (range-checked on voffset) and the wave writes
 // them to LDS [lds, lds + 1 KiB) in lane order. Written as asm so the compiler does not count it as an LDS store it
 // has to order against later LDS reads: it would otherwise wait for every load in flight before reading the other
-// stage. The waits these loads need are explicit at their uses (s_waitcnt vmcnt then a barrier).
+// stage. The waits these loads need are explicit at their uses (s_waitcnt vmcnt then a barrier). hipcc warns that
+// the clobbered m0 is a reserved register: the compiler keeps no value in m0 across instructions (it sets m0 right
+// before each instruction that reads it), so the clobber only states what the asm does.
 __device__ __forceinline__ void lds_dma16(v4i rsrc, int voffset, int soffset, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
