@@ -170,7 +170,7 @@ template <int kJ, int kR, bool kUni, bool kRes>
 __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int lane, u32x2 (&X)[kR][kJ]) {
   const int64_t C = p.C;
   auto rowi = [&](int r) { return min(row0 + r, p.rows - 1); };
-  auto bat = [&](int r) { return (kUni ? row0 : rowi(r)) / p.ntok; };
+  auto bat = [&](int r) { return (kUni ? rowi(0) : rowi(r)) / p.ntok; };   // (a wave past the end: the last batch)
 #pragma unroll
   for (int r = 0; r < kR; r++)
 #pragma unroll

@@ -77,6 +77,22 @@ def test_norm_against_oracle(dev, B, N, C, res):
     check(x, a, gate, w, shift, scale, 1e-6, res)
 
 
+@pytest.mark.parametrize("res", [False, True])
+def test_norm_wave_past_the_end(dev, res):
+    """24 rows of 8 tokens (3 batches) at C = 1024: one workgroup of 4 waves x 8 rows, the fourth wave wholly past the
+    end. Its rows re-read the last row and count in the maximum, so they must take the last batch's modulation, not
+    the next batch row's: the row after the modulation slice (inside the same allocation) holds 1000s here, which
+    would set the scale."""
+    B, N, C = 3, 8, 1024
+    x, a, _, w, _, _ = inputs(B, N, C, 31, dev, res)
+    g = torch.Generator(device=dev).manual_seed(32)
+    mod_full = (torch.randn(B + 1, 1, 6 * C, generator=g, device=dev) * 0.2).to(torch.bfloat16)
+    mod_full[B] = 1000.0
+    mod = mod_full[:B]
+    shift, scale, gate = mod[..., :C], mod[..., C:2 * C], mod[..., 2 * C:3 * C]
+    check(x, a if res else x, gate if res else x, w, shift, scale, 1e-6, res)
+
+
 def test_norm_single_two_pass_and_zero_wait_agree(dev, knob):
     """The d12 site 2 through the single pass, its zero-wait path (partials not yet published computed from the rows)
     and the forced two-pass path: the same bytes, equal to the oracle's."""
