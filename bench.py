@@ -581,6 +581,30 @@ def main():
     # Its kernels are short (12-60 us GEMMs): Python's autograd issues a step in about as long as the GPU runs it, so
     # the wall time above depends on the host CPU; the device time is measured with the launches queued ahead.
     ms_t_dev = time_device(run_text, 10, 0)
+    # and captured in a CUDA graph, as the reference runs its blocks (reduce-overhead): the same step replayed, its
+    # gradients checked bit for bit against an eager step's
+    ms_t_graph = None
+    try:
+        run_text()
+        ref = {k: v.grad.clone() for k, v in tt.items() if v.grad is not None}
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                run_text()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        for v in tt.values():
+            v.grad = None
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(G, tt)
+        graph.replay()
+        torch.cuda.synchronize()
+        if all(torch.equal(tt[k].grad.view(torch.int16), r.view(torch.int16)) for k, r in ref.items()):
+            ms_t_graph = time_region(graph.replay, 10, 3)
+        del graph
+    except RuntimeError as e:   # reported as null, with the reason on stderr
+        print(f"text block graph capture failed: {e}", file=sys.stderr, flush=True)
     del tt
 
     # ---- comparator: hipBLASLt FP8 GEMM (torch._scaled_mm) on the same shapes
@@ -657,7 +681,9 @@ def main():
                                    f"M = {MT} (128 captions x 51.5 tokens)", "ms": round(ms_t, 4),
                        "gemm_tflop": round(fl_t / 1e12, 4), "tflops": round(fl_t / ms_t / 1e9, 1),
                        "device_ms": round(ms_t_dev, 4) if ms_t_dev else None,
-                       "device_tflops": round(fl_t / ms_t_dev / 1e9, 1) if ms_t_dev else None},
+                       "device_tflops": round(fl_t / ms_t_dev / 1e9, 1) if ms_t_dev else None,
+                       "graph_ms": round(ms_t_graph, 4) if ms_t_graph else None,
+                       "graph_tflops": round(fl_t / ms_t_graph / 1e9, 1) if ms_t_graph else None},
         "hipblaslt_compare": hip,
         "cpu_baseline": cpu,
     }
