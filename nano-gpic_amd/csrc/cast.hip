@@ -1096,16 +1096,16 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
 // 16 of z2. The words go in groups of 1024, one word per thread; workgroup b takes groups j G + b, j = 0, 1, ...: at
 // each step the grid reads one contiguous window of z. Groups j < wpt are held as bf16 until the fold: j < kSwHeldR in
 // registers, the rest in LDS (128 KiB beside the 24 KiB sigmoid table; 96 MiB over 256 CUs). A product larger than the
-// grid holds is a hybrid: the sgroups groups
-// past wpt G are streamed -- computed, taken into the maximum and written to `a`; after the fold read back, last
-// first, and cast. Moved per element: 4 B of z read and 1 B of q written, plus 2 B written and 2 B read back for the
-// streamed part (the two-pass cast: 4 + 2 + 2 + 1).
+// grid holds is a hybrid: the sgroups groups past wpt G are streamed -- computed, taken into the maximum and written
+// to `a`; after the fold read back, last first, and cast. Moved per element: 4 B of z read and 1 B of q written, plus
+// 2 B written and 2 B read back for the streamed part (the two-pass cast: 4 + 2 + 2 + 1). The thread that writes a
+// streamed word is the one that reads it back: the XCDs' L2 caches are not coherent with each other within a kernel.
 constexpr int kSwThreads = 1024;   // 16 waves, 4 per SIMD: at most 128 VGPRs each
 constexpr int kSwHeldR = 16;       // product words a thread holds in registers (64 VGPRs)
 constexpr int kSwHeldL = 8;        // product words a thread holds in LDS (128 KiB per workgroup)
 constexpr int kSwHeld = kSwHeldR + kSwHeldL;
-constexpr int kSwBatch = 2;        // words whose z loads are issued together (4 spills at 128 VGPRs)
-constexpr int kSwHybrid = 8;   // the single pass takes products up to this many times what the grid holds
+constexpr int kSwBatch = 2;        // words whose z loads are issued together (4 words' loads spill at 128 VGPRs)
+constexpr int kSwHybrid = 8;       // the single pass takes products up to this many times what the grid holds
 static_assert(kSwHeldR % kSwBatch == 0 && kSwHeldL % kSwBatch == 0, "a batch lies in registers or in LDS");
 
 // Row and 8-column unit of product word i, stepped along words a fixed distance apart: one division at the start,
