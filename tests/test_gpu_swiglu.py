@@ -228,6 +228,30 @@ def test_single_pass_bwd_cast(dev, M, H, single_pass_default):
         assert s0 == od and np.array_equal(q0.cpu().numpy(), oq)
 
 
+@pytest.mark.parametrize("M,H", [(1024, 1040), (16384, 4096)])
+def test_single_pass_casts_strided_rows(dev, M, H, single_pass_default):
+    """z and da as column slices of wider tensors (row strides 2H + 72 and H + 40, as a view of a fused projection
+    would give): both single passes -- held whole, and past the grid's capacity (the product's hybrid through its
+    buffer, dz computed twice) -- give the bytes and scale of the same values made contiguous; the smaller also
+    against the oracle."""
+    g = torch.Generator(device=dev).manual_seed(M + H + 7)
+    zw = (torch.randn(M, 2 * H + 72, generator=g, device=dev) * 2).to(torch.bfloat16)
+    dw = (torch.randn(M, H + 40, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    z, da = zw[:, 8:8 + 2 * H], dw[:, 16:16 + H]
+    assert z.stride(0) == 2 * H + 72 and da.stride(0) == H + 40
+    q, s = G.swiglu_tcast(z)
+    q0, s0 = G.swiglu_tcast(z.contiguous())
+    assert s.item() == s0.item() and torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
+    dq, sd = G.swiglu_bwd_q(z, da)
+    dq0, sd0 = G.swiglu_bwd_q(z.contiguous(), da.contiguous())
+    assert sd.item() == sd0.item() and torch.equal(dq.view(torch.uint8), dq0.view(torch.uint8))
+    if M * H <= 1024 * 1040:
+        oq, od, _ = O.swiglu_tcast(bits(z))
+        assert s.item() == od and np.array_equal(qb(q), oq)
+        _, oq, od, _ = O.swiglu_bwd(bits(z), bits(da))
+        assert sd.item() == od and np.array_equal(qb(dq), oq)
+
+
 def test_single_pass_casts_beside_a_persistent_gemm(dev, single_pass_default):
     """The single-pass SwiGLU casts (one 1024-thread workgroup per CU, all of its LDS) on one stream while a
     persistent GEMM holds every CU from another: their workgroups start only as the GEMM's leave, the bounded waits
