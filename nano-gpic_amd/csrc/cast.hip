@@ -928,6 +928,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
                                                            int64_t sgroups, uint8_t *__restrict__ q,
                                                            float *__restrict__ dequant, void *ws,
                                                            uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   constexpr int kE = 16 / sizeof(T);   // elements per word
   const int64_t nw = n / kE;
   const int tail = (int)(n % kE);
@@ -972,7 +973,8 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
   uint32_t m0 = max(words_amax<T, kW>(w), tail_amax());
   if (sgroups > 0) m0 = max(m0, stream_amax(blockIdx.x));
   const uint32_t m = block_max_u32(m0);
-  const uint32_t g = once_fold(m, ws, wait_ticks, [&](int c) {
+  uint32_t tk;
+  const uint32_t g = once_fold(m, ws, ep, wait_ticks, tk, [&](int c) {
     uint32_t a = tail_amax();
     for (int j = 0; j < wpt; j++) {
       const int64_t i = word(c, j);
@@ -1019,6 +1021,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
       }
     }
   }
+  once_done(ws, tk);
 }
 
 // Transposing single-pass cast of a bf16 source: workgroup b holds tiles b and b + G (when there is one) in registers.
@@ -1030,6 +1033,7 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
                                                              uint8_t *__restrict__ qt, int64_t ldt,
                                                              float *__restrict__ dequant, void *ws,
                                                              uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   static_assert(kOnceTiles == 2, "two tiles per workgroup");
   __shared__ uint32_t tile[kTT * kTPitch];
   const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
@@ -1053,7 +1057,8 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
     load_tile_bf16(x, ld, rows, cols, r0_of(t), c0_of(t), S);
     m = max(m, words_amax<uint16_t, kTPer>(S));
   }
-  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int c) {
+  uint32_t tk;
+  const uint32_t g = once_fold(block_max_u32(m), ws, ep, wait_ticks, tk, [&](int c) {
     uint32_t a = 0;
     for (int64_t t = c; t < tiles; t += G) {
       const int64_t r0 = r0_of(t), c0 = c0_of(t);
@@ -1087,6 +1092,7 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
     if (ts - G >= 2 * G) load_tile_bf16(x, ld, rows, cols, r0_of(ts - G), c0_of(ts - G), S);
     emit_tile(E, r0_of(ts), c0_of(ts), rows, cols, q, ldq, qt, ldt, tile);
   }
+  once_done(ws, tk);
 }
 
 // ------------------------------------------------------------------------------------------- single-pass SwiGLU
@@ -1129,6 +1135,7 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_once_kernel(const uint16_t 
                                                                   uint16_t *__restrict__ a, uint8_t *__restrict__ q,
                                                                   float *__restrict__ dequant, void *ws,
                                                                   uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   __shared__ float lut[kLutLds];
   __shared__ u32x4 held[kSwHeldL * kSwThreads];
   lut_build(lut);
@@ -1208,7 +1215,8 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_once_kernel(const uint16_t 
     }
   }
 
-  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int cb) {
+  uint32_t tk;
+  const uint32_t g = once_fold(block_max_u32(m), ws, ep, wait_ticks, tk, [&](int cb) {
     uint32_t v = 0;
     for (int j = 0; j < wpt; j++) {
       const uint32_t i = hword((uint32_t)cb, j);
@@ -1259,6 +1267,7 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_once_kernel(const uint16_t 
       }
     }
   }
+  once_done(ws, tk);
 }
 
 // Single-pass SwiGLU backward cast without dz in memory (dzq [M, 2H] contiguous): one launch of one 1024-thread
@@ -1283,6 +1292,7 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_bwd_once_kernel(const uint1
                                                                       uint32_t sgroups, uint8_t *__restrict__ dzq,
                                                                       float *__restrict__ dequant, void *ws,
                                                                       uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   __shared__ float lut[kLutLds];
   __shared__ u32x4 held[2 * kBwHeldL * kSwThreads];
   lut_build(lut);
@@ -1365,7 +1375,8 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_bwd_once_kernel(const uint1
     }
   }
 
-  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int cb) {
+  uint32_t tk;
+  const uint32_t g = once_fold(block_max_u32(m), ws, ep, wait_ticks, tk, [&](int cb) {
     uint32_t v = 0;
     for (int j = 0; j < wpt; j++) {
       const uint32_t i = hunit((uint32_t)cb, j);
@@ -1442,6 +1453,7 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_bwd_once_kernel(const uint1
       }
     }
   }
+  once_done(ws, tk);
 }
 
 // Single-pass flat cast of a bf16 tensor above 48 MiB (cast_once_kernel holds 64 MiB): one 1024-thread workgroup per
@@ -1457,6 +1469,7 @@ __global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *_
                                                                 uint32_t sgroups, uint8_t *__restrict__ q,
                                                                 float *__restrict__ dequant, void *ws,
                                                                 uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   __shared__ u32x4 held[kWideL * kSwThreads];
   const uint32_t nw = (uint32_t)(n / 8), t = threadIdx.x, G = gridDim.x;
   const int tail = (int)(n % 8);
@@ -1499,7 +1512,8 @@ __global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *_
     return a;
   };
   if (blockIdx.x < sgroups) m = max(m, stream_amax(blockIdx.x));
-  const uint32_t g = once_fold(block_max_u32(m), ws, wait_ticks, [&](int cb) {
+  uint32_t tk;
+  const uint32_t g = once_fold(block_max_u32(m), ws, ep, wait_ticks, tk, [&](int cb) {
     uint32_t a = tail_amax();
     for (int j = 0; j < wpt; j++) {
       const uint32_t i = hword((uint32_t)cb, j);
@@ -1552,6 +1566,7 @@ __global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *_
       }
     }
   }
+  once_done(ws, tk);
 }
 
 // Host side. The single-pass settings (a process-wide tuning and test knob, gpic_fp8_set_single_pass): on / off and

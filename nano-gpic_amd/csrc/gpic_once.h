@@ -8,16 +8,22 @@
 namespace gpic {
 
 // Partials: one 64-bit word per workgroup, (call tag << 32) | amax bits, in the workspace. The tag is the workspace's
-// epoch + 1 (0 skipped): every workgroup reads the epoch at its fold, and the last workgroup of the call to finish its
-// fold (a counter in the workspace reaches the grid size) stores the tag as the new epoch and clears the counter. So
+// epoch + 1 (0 skipped): thread 0 of every workgroup reads the epoch as the kernel starts (once_epoch, its latency
+// hidden behind the kernel's first loads) and, once it has the value, counts its workgroup done; the last workgroup of
+// the call to be counted (a counter in the workspace reaching the grid size) stores the tag as the new epoch at its end
+// (once_done) and clears the counter. So the epoch cannot change before every workgroup of the call has read it, and
 // the next call on the workspace -- stream-ordered after this one, or the next replay of a captured graph -- uses the
-// next tag, and a word left by an earlier call never matches. The workspace is zeroed once, when it is created, and
-// tag 0 is never used; the tag repeats after 2^32 calls on one workspace.
+// next tag: a word left by an earlier call never matches, and a word this call's waiters publish late carries this
+// call's tag, which the next call does not use. The workspace is zeroed once, when it is created, and tag 0 is never
+// used; the tag repeats after 2^32 calls on one workspace.
 // No workgroup waits on another without a bound: a partial that has not appeared within the wait bound (kOnceWaitUs by
 // default, about 8x a whole call) is computed by the waiting workgroup itself, from that workgroup's share of x, and
 // published for the other waiters. So the launch needs no co-residency guarantee (a plain launch; the cooperative one
 // costs ~17 us per call here), never deadlocks when other work holds CUs, and the amax is exact either way. The
 // workspace's fallback word counts such direct computations (0 in normal runs).
+// A single-pass kernel calls once_epoch before its first loads, once_fold once, and once_done as its last statement
+// (every thread reaches it). The done counts are issued in once_fold and their results looked at only later, so their
+// round trips pass while the workgroup waits for the other partials and casts, instead of delaying the casts.
 constexpr int kMaxOnceBlocks = 1024;
 constexpr size_t kOnceTagged = 28 * 1024;                         // uint64_t[kMaxOnceBlocks] tagged partials
 constexpr size_t kOnceFallback = kOnceTagged + 8 * kMaxOnceBlocks;  // uint32_t: partials computed by a waiter
@@ -32,28 +38,47 @@ static_assert(kOnceGroupDone + 128 * ((kMaxOnceBlocks + kDoneGroup - 1) / kDoneG
               "cast workspace too small");
 constexpr int kOnceWaitUs = 200;   // the default bound of a wait for another workgroup's partial (about 8x a cast)
 
+// The call's tag, kept in LDS between once_fold and once_done.
+__device__ __forceinline__ uint32_t &once_tag_slot() {
+  __shared__ uint32_t tag;
+  return tag;
+}
+// The epoch, read by thread 0 (the other threads return 0). Relaxed atomics throughout: the epoch is written only by
+// the previous call's last workgroup, which ended before this kernel started, and an acquire / release at agent scope
+// would write back or invalidate whole caches on this multi-XCD part in each of the 1024 workgroups.
+__device__ __forceinline__ uint32_t once_epoch(void *ws) {
+  return threadIdx.x == 0 ? __hip_atomic_load(reinterpret_cast<uint32_t *>((char *)ws + kOnceEpoch), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : 0u;
+}
 // Publishes this workgroup's maximum m (held by every thread) as this call's partial, then returns the maximum over
-// all G partials to every thread. share_max(c) must return (to every thread of the workgroup) workgroup c's maximum
-// computed from x; it runs only for a partial that did not appear within wait_ticks. The call's tag comes from the
-// workspace's epoch; the last workgroup to finish its fold advances the epoch (see above).
+// all G partials to every thread. epoch: once_epoch's value (used by thread 0). share_max(c) must return (to every
+// thread of the workgroup) workgroup c's maximum computed from x; it runs only for a partial that did not appear within
+// wait_ticks. ticket: for once_done (thread 0's count of groups done, or ~0 where this workgroup completes no group).
+// The done count has two levels: the last workgroup of each group of kDoneGroup counts its group done (atomic
+// read-modify-writes of one address are totally ordered, so exactly one workgroup sees each count complete); every
+// counter is back at zero when the call ends.
 template <class ShareMax>
-__device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wait_ticks, ShareMax share_max) {
+__device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t epoch, uint32_t wait_ticks,
+                                              uint32_t &ticket, ShareMax share_max) {
   __shared__ int missing[kMaxOnceBlocks];
   __shared__ int nmissing;
-  __shared__ uint32_t stag;
+  uint32_t &stag = once_tag_slot();
   uint64_t *tagged = reinterpret_cast<uint64_t *>((char *)ws + kOnceTagged);
-  uint32_t *epoch = reinterpret_cast<uint32_t *>((char *)ws + kOnceEpoch);
-  uint32_t *done = reinterpret_cast<uint32_t *>((char *)ws + kOnceDone);
   const int G = gridDim.x;
+  const int grp = blockIdx.x / kDoneGroup;
+  uint32_t *gdone = reinterpret_cast<uint32_t *>((char *)ws + kOnceGroupDone + 128 * grp);
+  uint32_t gticket = 0;
   if (threadIdx.x == 0) {
-    // The epoch cannot change before this workgroup has counted itself done (below). Relaxed atomics throughout: the
-    // epoch is read by the next call, which starts after this kernel has completed, and an acquire / release at
-    // agent scope would write back or invalidate whole caches on this multi-XCD part in each of the 1024 workgroups.
-    uint32_t t = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    uint32_t t = epoch + 1u;
     t = t ? t : 1u;
     stag = t;
     __hip_atomic_store(tagged + blockIdx.x, ((uint64_t)t << 32) | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     nmissing = 0;
+    // Counted done: issued after the tag (so after the epoch load has returned: the tag's stores wait for it), its
+    // result looked at only after the partials have been read. (The compiler does not move atomics past each other.)
+    asm volatile("" ::: "memory");
+    gticket = __hip_atomic_fetch_add(gdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   const uint32_t tag = stag;
@@ -97,25 +122,23 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t wai
       __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceFallback), (uint32_t)computed,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // Done with the partials: every value this workgroup read from them has been consumed before the barriers above,
-  // so no read of them is outstanding. The last of the G workgroups to get here ends the call's use of the words: the
-  // next call takes the next tag. Counted in two levels: the last workgroup of each group of kDoneGroup counts its
-  // group done (atomic read-modify-writes of one address are totally ordered, so exactly one workgroup sees each
-  // count complete); every counter is back at zero when the call ends.
-  if (threadIdx.x == 0) {
-    const int grp = blockIdx.x / kDoneGroup;
-    const uint32_t gsize = (uint32_t)min(kDoneGroup, G - grp * kDoneGroup);
-    uint32_t *gdone = reinterpret_cast<uint32_t *>((char *)ws + kOnceGroupDone + 128 * grp);
-    if (__hip_atomic_fetch_add(gdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1u) {
-      __hip_atomic_store(gdone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t groups = (uint32_t)((G + kDoneGroup - 1) / kDoneGroup);
-      if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1u) {
-        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+  ticket = ~0u;
+  if (threadIdx.x == 0 && gticket == (uint32_t)min(kDoneGroup, G - grp * kDoneGroup) - 1u) {   // this group is done
+    __hip_atomic_store(gdone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>((char *)ws + kOnceDone), 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
   }
   return g;
+}
+// The last statement of a single-pass kernel (ticket: once_fold's): the workgroup that completed the last group
+// clears the count and stores the call's tag as the new epoch.
+__device__ __forceinline__ void once_done(void *ws, uint32_t ticket) {
+  if (threadIdx.x == 0 && ticket == (uint32_t)((gridDim.x + kDoneGroup - 1) / kDoneGroup) - 1u) {
+    __hip_atomic_store(reinterpret_cast<uint32_t *>((char *)ws + kOnceDone), 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reinterpret_cast<uint32_t *>((char *)ws + kOnceEpoch), once_tag_slot(), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Host side (cast.hip): workgroups of `kernel` (`threads` threads each) the current device holds at once, capped at

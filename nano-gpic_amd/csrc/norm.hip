@@ -285,13 +285,15 @@ __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int 
 // maxima (gpic_once.h), and each casts its rows from its registers.
 template <int kJ, int kR, bool kUni, bool kRes>
 __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *ws, uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * kR;
   const int64_t C = p.C;
   const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);   // rows of this wave that exist
   u32x2 X[kR][kJ];
   const float mf = norm_rows<kJ, kR, kUni, kRes>(p, row0, lane, X);
-  const uint32_t g = once_fold(block_max_u32(__float_as_uint(bf16_round(mf))), ws, wait_ticks, [&](int cb) {
+  uint32_t tk;
+  const uint32_t g = once_fold(block_max_u32(__float_as_uint(bf16_round(mf))), ws, ep, wait_ticks, tk, [&](int cb) {
     // workgroup cb's maximum from its rows (nothing stored): for a partial that did not appear in time
     uint32_t v = 0;
     for (int r = 0; r < kR; r++) {
@@ -311,6 +313,7 @@ __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *w
         __builtin_nontemporal_store(cast4_packed(X[r][j], scale),
                                     reinterpret_cast<uint32_t *>(p.hq + (row0 + r) * C + 4 * (lane + 64 * j)));
     }
+  once_done(ws, tk);
 }
 
 // Two passes, 1 (rows of at most 2048): workgroup g takes the groups of 4 kR rows g, g + G, ... through norm_rows,
