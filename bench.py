@@ -93,10 +93,13 @@ def make_inputs(dev, seed=0, C=C, H=H, outliers=0.0, M=M_TOK):
 
 
 def step(G, t):
+    """The block's four weights are cast together first (one launch; the same bytes as casting each inside its
+    linear), then the FP8 linears fwd + bwd."""
     import torch
-    y1 = G.fp8_linear_f8(t["x_qkv"], t["w_qkv"])
-    y2 = G.fp8_linear_f8(t["x_proj"], t["w_proj"])
-    y3 = G.fp8_mlp_f8(t["x_mlp"], t["w12"], t["w3"])
+    c_qkv, c_proj, c12, c3 = G.weight_casts(t["w_qkv"], t["w_proj"], t["w12"], t["w3"])
+    y1 = G.fp8_linear_f8(t["x_qkv"], t["w_qkv"], wcast=c_qkv)
+    y2 = G.fp8_linear_f8(t["x_proj"], t["w_proj"], wcast=c_proj)
+    y3 = G.fp8_mlp_f8(t["x_mlp"], t["w12"], t["w3"], w12cast=c12, w3cast=c3)
     torch.autograd.backward([y1, y2, y3], [t["dy_qkv"], t["dy_proj"], t["dy_mlp"]])
 
 

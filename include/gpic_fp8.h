@@ -93,6 +93,19 @@ int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8
                      float *dequant, void *ws, void *stream);
 
 /*
+ * count transposing casts in one call: tensor i is x[i] [rows[i], cols[i]] -> q[i] (or NULL), qt[i] [cols[i], ldt[i]],
+ * dequant[i], each with its own amax: the same bytes and scales as gpic_fp8_tcast_t on each tensor in order. No
+ * counterpart in the reference, whose linears cast their weights one at a time inside each forward; this is for a
+ * caller that casts a block's weights together before the block runs. bf16 tensors that fit the device together
+ * (d12: the four weights, 1024 tiles of 128 x 128) are cast in ONE launch, each tensor over its own workgroups;
+ * otherwise (fp32, more than 8 tensors, empty or larger tensors) the call makes the per-tensor calls. Every tensor is
+ * checked first, as gpic_fp8_tcast_t checks it; on an error nothing is launched.
+ */
+int gpic_fp8_tcast_t_group(int count, const void *const *x, int dtype, const int64_t *rows, const int64_t *cols,
+                           uint8_t *const *q, uint8_t *const *qt, const int64_t *ldt, float *const *dequant, void *ws,
+                           void *stream);
+
+/*
  * SwiGLU product cast. Replaces gpic::fp8_swiglu_tcast (fp8_native.py:130-144; _swiglu_tile :53-58,
  * _swiglu_amax_kernel :61-66, _swiglu_cast_kernel :69-78).
  *   z        [M, 2H] bf16, row stride sz (H % 8 == 0, sz % 8 == 0)

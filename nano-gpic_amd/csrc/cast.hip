@@ -1024,21 +1024,19 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
   once_done(ws, tk);
 }
 
-// Transposing single-pass cast of a bf16 source: workgroup b holds tiles b and b + G (when there is one) in registers.
+// Transposing single-pass cast of a bf16 source, run by the G workgroups [first, first + G) of a launch: workgroup b of
+// them holds tiles b and b + G (when there is one) in registers.
 // A larger x (at most kHybridTiles tiles) takes the same kernel as a hybrid: workgroup b's further tiles b + k G,
 // k >= 2, are streamed once for the maximum and once more, last first, for the cast, so only the part of x that does
 // not fit is read twice.
-__global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows,
-                                                             int64_t cols, uint8_t *__restrict__ q, int64_t ldq,
-                                                             uint8_t *__restrict__ qt, int64_t ldt,
-                                                             float *__restrict__ dequant, void *ws,
-                                                             uint32_t wait_ticks) {
-  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
+__device__ __forceinline__ void cast_t_once_run(const uint16_t *__restrict__ x, int64_t ld, int64_t rows, int64_t cols,
+                                                uint8_t *__restrict__ q, int64_t ldq, uint8_t *__restrict__ qt,
+                                                int64_t ldt, float *__restrict__ dequant, void *ws, uint32_t wait_ticks,
+                                                uint32_t ep, int64_t b, int64_t G, int first) {
   static_assert(kOnceTiles == 2, "two tiles per workgroup");
   __shared__ uint32_t tile[kTT * kTPitch];
   const int64_t tiles_c = (cols + kTT - 1) / kTT, tiles = tiles_c * ((ldt + kTT - 1) / kTT);
-  const int64_t G = gridDim.x;
-  const int64_t t0 = blockIdx.x, t1 = blockIdx.x + G;   // t0 < tiles: the grid never exceeds the tile count
+  const int64_t t0 = b, t1 = b + G;   // t0 < tiles: the grid never exceeds the tile count
   auto r0_of = [&](int64_t t) { return (t / tiles_c) * kTT; };
   auto c0_of = [&](int64_t t) { return (t % tiles_c) * kTT; };
   u32x4 R[2 * kTPer];
@@ -1052,13 +1050,13 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
     for (int i = 0; i < kTPer; i++) R1[i] = u32x4{0u, 0u, 0u, 0u};
   }
   uint32_t m = words_amax<uint16_t, 2 * kTPer>(R);
-  for (int64_t t = blockIdx.x + 2 * G; t < tiles; t += G) {   // hybrid: the tiles that are not held
+  for (int64_t t = b + 2 * G; t < tiles; t += G) {   // hybrid: the tiles that are not held
     u32x4 S[kTPer];
     load_tile_bf16(x, ld, rows, cols, r0_of(t), c0_of(t), S);
     m = max(m, words_amax<uint16_t, kTPer>(S));
   }
   uint32_t tk;
-  const uint32_t g = once_fold(block_max_u32(m), ws, ep, wait_ticks, tk, [&](int c) {
+  const uint32_t g = once_fold_range(block_max_u32(m), ws, ep, wait_ticks, tk, first, (int)G, [&](int c) {
     uint32_t a = 0;
     for (int64_t t = c; t < tiles; t += G) {
       const int64_t r0 = r0_of(t), c0 = c0_of(t);
@@ -1073,13 +1071,13 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
   hold(R);
   float scale, deq;
   scales_from_amax(g, scale, deq);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *dequant = deq;
+  if (b == 0 && threadIdx.x == 0) *dequant = deq;
   u32x2 E0[kTPer], E1[kTPer];   // both tiles narrowed first: 32 VGPRs live instead of 64
   cvt_tile_bf16(R0, scale, E0);
   cvt_tile_bf16(R1, scale, E1);
   // hybrid: the streamed tiles again, last first (the most recently read are the likeliest still in the MALL), the
   // next one's loads in flight while the current one is cast
-  int64_t ts = blockIdx.x + 2 * G;
+  int64_t ts = b + 2 * G;
   if (ts < tiles) ts += ((tiles - 1 - ts) / G) * G;   // the last tile of this workgroup
   u32x4 S[kTPer];
   if (ts < tiles) load_tile_bf16(x, ld, rows, cols, r0_of(ts), c0_of(ts), S);
@@ -1093,6 +1091,39 @@ __global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__r
     emit_tile(E, r0_of(ts), c0_of(ts), rows, cols, q, ldq, qt, ldt, tile);
   }
   once_done(ws, tk);
+}
+
+__global__ __launch_bounds__(256, 4) void cast_t_once_kernel(const uint16_t *__restrict__ x, int64_t ld, int64_t rows,
+                                                             int64_t cols, uint8_t *__restrict__ q, int64_t ldq,
+                                                             uint8_t *__restrict__ qt, int64_t ldt,
+                                                             float *__restrict__ dequant, void *ws,
+                                                             uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
+  cast_t_once_run(x, ld, rows, cols, q, ldq, qt, ldt, dequant, ws, wait_ticks, ep, blockIdx.x, gridDim.x, 0);
+}
+
+// Several transposing casts in one launch: tensor i takes workgroups [first[i], first[i + 1]), each holding at most
+// two of its tiles (no hybrid), and folds over its own workgroups' partials; one epoch and one done count for the
+// launch. The same bytes and scales as one cast_t_once_kernel launch per tensor.
+constexpr int kMaxTGroup = 8;
+struct TGroup {
+  const uint16_t *x[kMaxTGroup];
+  uint8_t *q[kMaxTGroup];
+  uint8_t *qt[kMaxTGroup];
+  float *dequant[kMaxTGroup];
+  int64_t rows[kMaxTGroup], cols[kMaxTGroup], ldt[kMaxTGroup];
+  int first[kMaxTGroup + 1];
+  int count;
+};
+__global__ __launch_bounds__(256, 4) void cast_t_group_kernel(const TGroup g, void *ws,
+                                                              uint32_t wait_ticks) {
+  const uint32_t ep = once_epoch(ws);
+  int i = 0;
+  while (i + 1 < g.count && (int)blockIdx.x >= g.first[i + 1]) i++;
+  i = __builtin_amdgcn_readfirstlane(i);
+  const int first = g.first[i];
+  cast_t_once_run(g.x[i], g.cols[i], g.rows[i], g.cols[i], g.q[i], g.cols[i], g.qt[i], g.ldt[i], g.dequant[i], ws,
+                  wait_ticks, ep, (int)blockIdx.x - first, g.first[i + 1] - first, first);
 }
 
 // ------------------------------------------------------------------------------------------- single-pass SwiGLU
@@ -1590,11 +1621,11 @@ uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(st
 
 bool once_enabled() { return g_once_enabled.load(std::memory_order_relaxed) != 0; }
 
-static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw, g_cap_wide;
+static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw, g_cap_wide, g_cap_tg;
 struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
   DeviceCacheInit() {
     for (int i = 0; i < kMaxDevices; i++)
-      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = g_cap_wide[i] = -1;
+      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = g_cap_wide[i] = g_cap_tg[i] = -1;
   }
 };
 static DeviceCacheInit g_device_cache_init;
@@ -1700,6 +1731,38 @@ static bool launch_tcast_t_once(const uint16_t *x, int64_t rows, int64_t cols, u
   return true;
 }
 
+// The grouped transposing cast when every tensor fits (false, nothing launched, otherwise): one tile per workgroup
+// when the tiles fit the device at once, else two.
+static bool launch_tcast_t_group(int count, const uint16_t *const *x, const int64_t *rows, const int64_t *cols,
+                                 uint8_t *const *q, uint8_t *const *qt, const int64_t *ldt, float *const *dequant,
+                                 void *ws, hipStream_t st) {
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_t_group_kernel), g_cap_tg, 256);
+  if (!once_enabled() || cap <= 0 || count < 1 || count > kMaxTGroup) return false;
+  int64_t tiles[kMaxTGroup], all = 0, halves = 0;
+  for (int i = 0; i < count; i++) {
+    tiles[i] = ((cols[i] + kTT - 1) / kTT) * ((ldt[i] + kTT - 1) / kTT);
+    if (rows[i] <= 0 || tiles[i] <= 0) return false;
+    all += tiles[i];
+    halves += (tiles[i] + 1) / 2;
+  }
+  if (halves > cap) return false;
+  TGroup g{};
+  g.count = count;
+  g.first[0] = 0;
+  for (int i = 0; i < count; i++) {
+    g.x[i] = x[i];
+    g.q[i] = q[i];
+    g.qt[i] = qt[i];
+    g.dequant[i] = dequant[i];
+    g.rows[i] = rows[i];
+    g.cols[i] = cols[i];
+    g.ldt[i] = ldt[i];
+    g.first[i + 1] = g.first[i] + (int)(all <= cap ? tiles[i] : (tiles[i] + 1) / 2);
+  }
+  cast_t_group_kernel<<<g.first[count], 256, 0, st>>>(g, ws, once_wait_ticks());
+  return true;
+}
+
 // ------------------------------------------------------------------------------------------- allocation-free cast
 //
 // gpic_fp8_tcast_noalloc: gpic_fp8_tcast with its workspace in this file's static device array `scratch` (one copy per
@@ -1784,6 +1847,29 @@ int gpic_fp8_tcast_noalloc(const void *x, int dtype, int64_t n, uint8_t *q, floa
   const int rc = scratch_address((hipStream_t)stream, &ws);
   if (rc != GPIC_OK) return rc;
   return gpic_fp8_tcast(x, dtype, n, q, dequant, ws, stream);
+}
+
+int gpic_fp8_tcast_t_group(int count, const void *const *x, int dtype, const int64_t *rows, const int64_t *cols,
+                           uint8_t *const *q, uint8_t *const *qt, const int64_t *ldt, float *const *dequant, void *ws,
+                           void *stream) {
+  if (count < 0 || (count > 0 && (!x || !rows || !cols || !q || !qt || !ldt || !dequant))) return GPIC_EINVAL;
+  for (int i = 0; i < count; i++) {   // every tensor checked as gpic_fp8_tcast_t checks it, before anything is launched
+    if (rows[i] < 0 || cols[i] < 0 || !dequant[i] || !ws || (rows[i] > 0 && cols[i] > 0 && !x[i]) ||
+        (cols[i] > 0 && ldt[i] > 0 && !qt[i]))
+      return GPIC_EINVAL;
+    if (cols[i] % 16 != 0 || ldt[i] % 16 != 0 || ldt[i] < rows[i]) return GPIC_ESHAPE;
+    if (dtype != GPIC_DTYPE_BF16 && dtype != GPIC_DTYPE_F32) return GPIC_EDTYPE;
+    if (!aligned16(x[i]) || (q[i] && !aligned16(q[i])) || !aligned16(qt[i]) || !aligned16(ws)) return GPIC_EALIGN;
+  }
+  if (dtype == GPIC_DTYPE_BF16 &&
+      launch_tcast_t_group(count, reinterpret_cast<const uint16_t *const *>(x), rows, cols, q, qt, ldt, dequant, ws,
+                           (hipStream_t)stream))
+    return (int)hipGetLastError();
+  for (int i = 0; i < count; i++) {   // otherwise one call per tensor, in order
+    const int rc = gpic_fp8_tcast_t(x[i], dtype, rows[i], cols[i], q[i], qt[i], ldt[i], dequant[i], ws, stream);
+    if (rc != GPIC_OK) return rc;
+  }
+  return GPIC_OK;
 }
 
 int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,

@@ -58,9 +58,11 @@ __device__ __forceinline__ uint32_t once_epoch(void *ws) {
 // The done count has two levels: the last workgroup of each group of kDoneGroup counts its group done (atomic
 // read-modify-writes of one address are totally ordered, so exactly one workgroup sees each count complete); every
 // counter is back at zero when the call ends.
+// once_fold_range: the same over the partials of workgroups [first, first + count) only (a launch that casts several
+// tensors, each over its own range of workgroups); share_max then takes the index within the range.
 template <class ShareMax>
-__device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t epoch, uint32_t wait_ticks,
-                                              uint32_t &ticket, ShareMax share_max) {
+__device__ __forceinline__ uint32_t once_fold_range(uint32_t m, void *ws, uint32_t epoch, uint32_t wait_ticks,
+                                                    uint32_t &ticket, int first, int count, ShareMax share_max) {
   __shared__ int missing[kMaxOnceBlocks];
   __shared__ int nmissing;
   uint32_t &stag = once_tag_slot();
@@ -84,7 +86,7 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t epo
   const uint32_t tag = stag;
   uint32_t g = m;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  for (int i = threadIdx.x; i < G; i += blockDim.x) {
+  for (int i = first + (int)threadIdx.x; i < first + count; i += blockDim.x) {
     uint64_t w = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     while ((uint32_t)(w >> 32) != tag && __builtin_amdgcn_s_memrealtime() - t0 < wait_ticks) {
       __builtin_amdgcn_s_sleep(2);
@@ -111,7 +113,7 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t epo
       if ((uint32_t)(w >> 32) == tag) {
         g = max(g, (uint32_t)w);
       } else {
-        const uint32_t v = share_max(c);
+        const uint32_t v = share_max(c - first);
         g = max(g, v);
         computed++;
         if (threadIdx.x == 0)
@@ -129,6 +131,11 @@ __device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t epo
                                     __HIP_MEMORY_SCOPE_AGENT);
   }
   return g;
+}
+template <class ShareMax>
+__device__ __forceinline__ uint32_t once_fold(uint32_t m, void *ws, uint32_t epoch, uint32_t wait_ticks,
+                                              uint32_t &ticket, ShareMax share_max) {
+  return once_fold_range(m, ws, epoch, wait_ticks, ticket, 0, (int)gridDim.x, share_max);
 }
 // The last statement of a single-pass kernel (ticket: once_fold's): the workgroup that completed the last group
 // clears the count and stores the call's tag as the new epoch.

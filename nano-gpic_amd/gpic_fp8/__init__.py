@@ -5,7 +5,8 @@ kernels in libgpic_fp8.so (C ABI: include/gpic_fp8.h). GPU only: no CPU fallback
 """
 from .fp8_native import (E4, FMAX, TINY, Fp8Linear, Fp8LinearF8, convert_native, fp8_gemm, fp8_gemm_mn,
                          fp8_linear, fp8_linear_f8, fp8_mlp, fp8_mlp_f8, fp8_swiglu_w3, reference, swiglu_bwd,
-                         swiglu_bwd_q, swiglu_bwd_t, swiglu_tcast, swiglu_tcast_t, tcast, tcast_t, _mm)
+                         swiglu_bwd_q, swiglu_bwd_t, swiglu_tcast, swiglu_tcast_t, tcast, tcast_t, tcast_t_group,
+                         weight_casts, _mm)
 from .fp8 import KEEP, convert_fp8, fp8_filter
 from .norm import (fp8_mod_rmsnorm_linear, fp8_res_mod_rmsnorm_mlp, mod_rmsnorm, res_mod_rmsnorm,
                    res_mod_rmsnorm_q)
@@ -13,6 +14,7 @@ from .norm import reference as norm_reference
 
 __all__ = ["E4", "FMAX", "TINY", "Fp8Linear", "Fp8LinearF8", "convert_native", "convert_fp8", "fp8_filter", "KEEP",
            "fp8_gemm", "fp8_gemm_mn", "fp8_linear", "fp8_linear_f8", "fp8_mlp", "fp8_mlp_f8", "fp8_swiglu_w3", "reference",
-           "swiglu_bwd", "swiglu_bwd_q", "swiglu_bwd_t", "swiglu_tcast", "swiglu_tcast_t", "tcast", "tcast_t", "_mm",
+           "swiglu_bwd", "swiglu_bwd_q", "swiglu_bwd_t", "swiglu_tcast", "swiglu_tcast_t", "tcast", "tcast_t", "tcast_t_group",
+           "weight_casts", "_mm",
            "mod_rmsnorm", "res_mod_rmsnorm", "res_mod_rmsnorm_q", "norm_reference", "fp8_mod_rmsnorm_linear",
            "fp8_res_mod_rmsnorm_mlp"]

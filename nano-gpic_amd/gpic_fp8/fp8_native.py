@@ -20,6 +20,8 @@ Phases (convert_native / convert_fp8 recipes):
 """
 from typing import Optional
 
+import ctypes
+
 import torch
 
 from . import _lib as L
@@ -97,6 +99,60 @@ def _(x, want_q=True):
     R, C = x.shape
     return (x.new_empty((R, C) if want_q else (0,), dtype=E4), x.new_empty(C, _r16(R), dtype=E4),
             x.new_empty(1, dtype=torch.float32))
+
+
+@torch.library.custom_op("gpic::fp8_tcast_t_group", mutates_args=())
+def tcast_t_group(xs: list[torch.Tensor]) -> list[torch.Tensor]:
+    """tcast_t of each 2-D tensor in xs, in one call: [q0, qt0, s0, q1, qt1, s1, ...], the same bytes and scales as
+    tcast_t(x) for each x. bf16 tensors that fit the device together (a d12 block's four weights) are cast in one
+    launch (gpic_fp8_tcast_t_group), each with its own amax. An extension of the reference, whose linears cast their
+    weights one at a time inside each forward (fp8_native.py:187,245,248): the weight casts of a block, done together
+    before it runs, for fp8_linear_f8(..., wcast=) and fp8_mlp_f8(..., w12cast=, w3cast=)."""
+    if not xs:
+        return []
+    L.require_gpu(*xs)
+    dev = xs[0].device
+    if any(x.device != dev for x in xs):
+        raise ValueError("tcast_t_group: every tensor must be on the same device")
+    for x in xs:
+        if x.dim() != 2 or x.shape[1] % 16:
+            raise ValueError(f"tcast_t_group needs 2-D tensors with a multiple of 16 columns, got {tuple(x.shape)}")
+    xc = [_prep(x) for x in xs]
+    if len({x.dtype for x in xc}) != 1:   # one dtype per call: mixed lists widen to fp32, as tcast_t would read them
+        xc = [L.aligned(x.float().contiguous()) for x in xc]
+    out = []
+    for x in xc:
+        R, C = x.shape
+        out += [torch.empty(R, C, dtype=E4, device=dev), torch.empty(C, _r16(R), dtype=E4, device=dev),
+                torch.empty(1, dtype=torch.float32, device=dev)]
+    n = len(xc)
+    arr = lambda t, v: (t * n)(*v)
+    with torch.cuda.device(dev):
+        ws = L.cast_workspace(dev)
+        L.check(L.lib().gpic_fp8_tcast_t_group(
+            n, arr(ctypes.c_void_p, [x.data_ptr() for x in xc]), L.DTYPE_CODE[xc[0].dtype],
+            arr(ctypes.c_int64, [x.shape[0] for x in xc]), arr(ctypes.c_int64, [x.shape[1] for x in xc]),
+            arr(ctypes.c_void_p, [out[3 * i].data_ptr() for i in range(n)]),
+            arr(ctypes.c_void_p, [out[3 * i + 1].data_ptr() for i in range(n)]),
+            arr(ctypes.c_int64, [out[3 * i + 1].shape[1] for i in range(n)]),
+            arr(ctypes.c_void_p, [out[3 * i + 2].data_ptr() for i in range(n)]), ws.data_ptr(),
+            L.stream_ptr(dev)), "gpic_fp8_tcast_t_group")
+    return out
+
+
+@tcast_t_group.register_fake
+def _(xs):
+    out = []
+    for x in xs:
+        R, C = x.shape
+        out += [x.new_empty(R, C, dtype=E4), x.new_empty(C, _r16(R), dtype=E4), x.new_empty(1, dtype=torch.float32)]
+    return out
+
+
+def weight_casts(*ws):
+    """The (q, qt, dequant) triples of tcast_t_group(ws), one per weight, in order."""
+    o = tcast_t_group(list(ws))
+    return [tuple(o[3 * i:3 * i + 3]) for i in range(len(ws))]
 
 
 def _swiglu_prep(z):
@@ -380,11 +436,11 @@ class _Fp8LinearF8(torch.autograd.Function):
     """Phase 3: forward, dgrad and wgrad GEMMs all in FP8. The forward keeps x's e4m3 bytes (the wgrad's B operand,
     read with the tokens as its K rows) and w's transposed bytes (the dgrad's B operand) instead of bf16 copies."""
     @staticmethod
-    def forward(ctx, x, w, b):
+    def forward(ctx, x, w, b, wcast=None):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         xq, sx = tcast(x2)
-        wq, wqt, sw = tcast_t(w)
+        wq, wqt, sw = tcast_t(w) if wcast is None else wcast
         y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
         ctx.save_for_backward(xq, sx, wqt, sw)
         ctx.has_b, ctx.shape, ctx.wdt = b is not None, shape, w.dtype
@@ -398,7 +454,7 @@ class _Fp8LinearF8(torch.autograd.Function):
         dx = fp8_gemm(dyq, sdy, wqt, sw, None, False).view(ctx.shape)     # [M, N] . [K, N]^T
         dw = fp8_gemm_mn(dyq, sdy, xq, sx).to(ctx.wdt)                   # [M, N]^T . [M, K]
         db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
-        return dx, dw, db
+        return dx, dw, db, None
 
 
 class _SwiGLUw3(torch.autograd.Function):
@@ -467,14 +523,14 @@ class _Fp8MLPF8(torch.autograd.Function):
     and the SwiGLU product's e4m3 bytes (the wgrads' B operands, read with the tokens as K rows), z, and the weights'
     transposed bytes (the dgrads' B operands)."""
     @staticmethod
-    def forward(ctx, x, w12, w3):
+    def forward(ctx, x, w12, w3, w12cast=None, w3cast=None):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         xq, sx = tcast(x2)
-        w12q, w12qt, s12 = tcast_t(w12)
+        w12q, w12qt, s12 = tcast_t(w12) if w12cast is None else w12cast
         z = fp8_gemm(xq, sx, w12q, s12)
         aq, sa = swiglu_tcast(z)
-        w3q, w3qt, s3 = tcast_t(w3)
+        w3q, w3qt, s3 = tcast_t(w3) if w3cast is None else w3cast
         y = fp8_gemm(aq, sa, w3q, s3)
         ctx.save_for_backward(xq, sx, z, aq, sa, w12qt, s12, w3qt, s3)
         ctx.shape, ctx.dt = shape, (w12.dtype, w3.dtype)
@@ -490,7 +546,7 @@ class _Fp8MLPF8(torch.autograd.Function):
         dzq, sdz = swiglu_bwd_q(z, da)                           # dz itself is not needed: never written
         dx = fp8_gemm(dzq, sdz, w12qt, s12, None, False)         # [M, C]
         dw12 = fp8_gemm_mn(dzq, sdz, xq, sx)                     # [M, 2H]^T . [M, C] = [2H, C]
-        return dx.view(ctx.shape), dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1])
+        return dx.view(ctx.shape), dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1]), None, None
 
 
 def fp8_mlp(x, w12, w3):
@@ -508,16 +564,24 @@ def fp8_swiglu_w3(z, w3):
         return _SwiGLUw3.apply(z.to(torch.bfloat16), w3)
 
 
-def fp8_linear_f8(x, w, b=None):
-    """Phase 3 fp8_linear: FP8 dgrad and wgrad as well."""
-    with torch.autocast("cuda", enabled=False):
-        return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b)
+def _check_cast(name, w, c):
+    if c is not None and (len(c) != 3 or c[0].shape != w.shape or c[1].shape[0] != w.shape[1]):
+        raise ValueError(f"{name}: a (q, qt, dequant) triple of tcast_t(weight) [{tuple(w.shape)}] expected")
+    return c
 
 
-def fp8_mlp_f8(x, w12, w3):
-    """Phase 3 fp8_mlp: every GEMM of the SwiGLU MLP in FP8."""
+def fp8_linear_f8(x, w, b=None, wcast=None):
+    """Phase 3 fp8_linear: FP8 dgrad and wgrad as well. wcast: w's (q, qt, dequant) from weight_casts (the same bytes
+    tcast_t(w) would give, cast beforehand with the block's other weights), else w is cast here."""
     with torch.autocast("cuda", enabled=False):
-        return _Fp8MLPF8.apply(x.to(torch.bfloat16), w12, w3)
+        return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b, _check_cast("wcast", w, wcast))
+
+
+def fp8_mlp_f8(x, w12, w3, w12cast=None, w3cast=None):
+    """Phase 3 fp8_mlp: every GEMM of the SwiGLU MLP in FP8. w12cast / w3cast: as fp8_linear_f8's wcast."""
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8MLPF8.apply(x.to(torch.bfloat16), w12, w3, _check_cast("w12cast", w12, w12cast),
+                               _check_cast("w3cast", w3, w3cast))
 
 
 class Fp8Linear(torch.nn.Linear):

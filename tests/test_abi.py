@@ -58,6 +58,18 @@ def test_validation_codes():
     assert na(wsp + 2, 0, 16, wsp, wsp, None) == -4
     # transposing cast: columns must be a multiple of 16, ldt >= rows
     assert lib.gpic_fp8_tcast_t(wsp, 0, 4, 24, wsp, wsp, 16, wsp, wsp, None) == -3
+    # grouped transposing casts: a negative count or null arrays; each tensor checked as gpic_fp8_tcast_t checks it
+    tg = lib.gpic_fp8_tcast_t_group
+    assert tg(-1, None, 0, None, None, None, None, None, None, wsp, None) == -1
+    assert tg(1, None, 0, None, None, None, None, None, None, wsp, None) == -1
+    assert tg(0, None, 0, None, None, None, None, None, None, wsp, None) == 0
+    P = lambda *v: (ctypes.c_void_p * len(v))(*v)
+    I = lambda *v: (ctypes.c_int64 * len(v))(*v)
+    good = (P(wsp, wsp), 0, I(4, 4), I(16, 16), P(wsp, wsp), P(wsp, wsp), I(16, 16), P(wsp, wsp), wsp, None)
+    assert tg(2, good[0], 7, *good[2:]) == -2                                    # unsupported dtype
+    assert tg(2, good[0], 0, I(4, 4), I(16, 24), *good[4:]) == -3                # the second tensor's columns
+    assert tg(2, good[0], 0, I(4, 20), I(16, 16), good[4], good[5], I(16, 16), *good[7:]) == -3   # ldt < rows
+    assert tg(2, P(wsp, wsp + 2), 0, *good[2:]) == -4                           # misaligned second source
     assert lib.gpic_fp8_tcast_t(wsp, 0, 40, 32, wsp, wsp, 32, wsp, wsp, None) == -3
     # SwiGLU: H % 8, strides
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 12, 24, wsp, 12, wsp, wsp, None) == -3
