@@ -572,7 +572,8 @@ def _check_cast(name, w, c):
 
 def fp8_linear_f8(x, w, b=None, wcast=None):
     """Phase 3 fp8_linear: FP8 dgrad and wgrad as well. wcast: w's (q, qt, dequant) from weight_casts (the same bytes
-    tcast_t(w) would give, cast beforehand with the block's other weights), else w is cast here."""
+    tcast_t(w) would give, cast beforehand with the block's other weights), else w is cast here. A wcast must come
+    from w's current values: cast again after every update of w (an optimizer step); only its shapes are checked."""
     with torch.autocast("cuda", enabled=False):
         return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b, _check_cast("wcast", w, wcast))
 
