@@ -44,11 +44,12 @@ GROUPS = [
 
 
 @pytest.mark.parametrize("shapes", GROUPS, ids=lambda s: f"{len(s)}x{s[0][0]}x{s[0][1]}")
-@pytest.mark.parametrize("wait", [-1, 0])
+@pytest.mark.parametrize("wait", [-1, 0, None])
 def test_group_matches_per_tensor(dev, knob, shapes, wait):
     """Every (q, qt, dequant) equals tcast_t's, bit for bit; with a zero wait bound every partial not yet published is
-    computed by the waiting workgroup from its own tensor (the ranged fold's index within the tensor)."""
-    L.set_single_pass(True, wait)
+    computed by the waiting workgroup from its own tensor (the ranged fold's index within the tensor); with the single
+    pass switched off (None) the group makes the two-pass per-tensor calls."""
+    L.set_single_pass(wait is not None, -1 if wait is None else wait)
     xs = tensors(dev, shapes, 5)
     if len(xs) > 2 and xs[2].numel():
         xs[2][0, 0] = float("nan")                  # a NaN leaves that tensor's amax (and no other's) unchanged
