@@ -116,8 +116,9 @@ def config2_input(dev):
 def cast_traffic(G, dev):
     """Each cast once, for counter collection (one row per dispatch, in this order): config 2 (a warm-up call, then a
     warm one, then one after a 512 MB write that flushes L2 / MALL), an fp32 weight [3072 x 1024] (DDP weights are
-    fp32), the dY of qkv [32768 x 3072] (the step's largest flat cast) and the d12 SwiGLU casts of the step: the
-    product cast of z [32768 x 8192] and the backward's dz cast."""
+    fp32), the dY of qkv [32768 x 3072] (the step's largest flat cast), the d12 SwiGLU casts of the step: the
+    product cast of z [32768 x 8192] and the backward's dz cast, and the step's four bf16 weights in one grouped
+    transposing cast."""
     import torch
     xc = config2_input(dev)
     flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
@@ -126,13 +127,16 @@ def cast_traffic(G, dev):
     z = torch.randn(M_TOK, 2 * H, generator=g, device=dev).to(torch.bfloat16)
     da = (torch.randn(M_TOK, H, generator=g, device=dev) * 0.1).to(torch.bfloat16)
     dqkv = (torch.randn(M_TOK, 3 * C, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    wts = [(torch.randn(r, c, generator=g, device=dev) * c ** -0.5).to(torch.bfloat16)
+           for r, c in ((3 * C, C), (C, C), (2 * H, C), (C, H))]
     order = []
     for name, fn in (("config2 warm-up", lambda: G.tcast(xc)), ("config2 warm", lambda: G.tcast(xc)),
                      ("flush", lambda: flush.fill_(1)), ("config2 flushed", lambda: G.tcast(xc)),
                      ("fp32 weight [3072 x 1024]", lambda: G.tcast(w32)),
                      ("qkv dY [32768 x 3072]", lambda: G.tcast(dqkv)),
                      ("swiglu product cast z [32768 x 8192]", lambda: G.swiglu_tcast(z)),
-                     ("swiglu backward dz cast", lambda: G.swiglu_bwd_q(z, da))):
+                     ("swiglu backward dz cast", lambda: G.swiglu_bwd_q(z, da)),
+                     ("d12 weights, grouped transposing cast", lambda: G.tcast_t_group(wts))):
         fn()
         torch.cuda.synchronize()
         order.append(name)
