@@ -1822,6 +1822,7 @@ void gpic_fp8_set_single_pass(int enabled, int wait_us) {
 }
 
 int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *ws, void *stream) {
+  status_scope();
   if (n < 0 || !dequant || !ws || (n > 0 && (!x || !q))) return GPIC_EINVAL;
   if (dtype != GPIC_DTYPE_BF16 && dtype != GPIC_DTYPE_F32) return GPIC_EDTYPE;
   if (!aligned16(x) || !aligned16(q) || !aligned16(ws)) return GPIC_EALIGN;
@@ -1838,6 +1839,7 @@ int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequa
 }
 
 int gpic_fp8_tcast_noalloc(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *stream) {
+  status_scope();
   // the arguments gpic_fp8_tcast checks, before the first call on a device sets its scratch up
   if (n < 0 || !dequant || (n > 0 && (!x || !q))) return GPIC_EINVAL;
   if (dtype != GPIC_DTYPE_BF16 && dtype != GPIC_DTYPE_F32) return GPIC_EDTYPE;
@@ -1852,6 +1854,7 @@ int gpic_fp8_tcast_noalloc(const void *x, int dtype, int64_t n, uint8_t *q, floa
 int gpic_fp8_tcast_t_group(int count, const void *const *x, int dtype, const int64_t *rows, const int64_t *cols,
                            uint8_t *const *q, uint8_t *const *qt, const int64_t *ldt, float *const *dequant, void *ws,
                            void *stream) {
+  status_scope();
   if (count < 0 || (count > 0 && (!x || !rows || !cols || !q || !qt || !ldt || !dequant))) return GPIC_EINVAL;
   for (int i = 0; i < count; i++) {   // every tensor checked as gpic_fp8_tcast_t checks it, before anything is launched
     if (rows[i] < 0 || cols[i] < 0 || !dequant[i] || !ws || (rows[i] > 0 && cols[i] > 0 && !x[i]) ||
@@ -1874,6 +1877,7 @@ int gpic_fp8_tcast_t_group(int count, const void *const *x, int dtype, const int
 
 int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, uint8_t *qt, int64_t ldt,
                      float *dequant, void *ws, void *stream) {
+  status_scope();
   if (rows < 0 || cols < 0 || !dequant || !ws || (rows > 0 && cols > 0 && !x) || (cols > 0 && ldt > 0 && !qt))
     return GPIC_EINVAL;
   if (cols % 16 != 0 || ldt % 16 != 0 || ldt < rows) return GPIC_ESHAPE;
@@ -1903,6 +1907,7 @@ int gpic_fp8_tcast_t(const void *x, int dtype, int64_t rows, int64_t cols, uint8
 
 int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint8_t *q, int64_t sq, float *dequant,
                           void *ws, void *stream) {
+  status_scope();
   if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !q))) return GPIC_EINVAL;
   if (H % 8 != 0 || sz % 8 != 0 || sq % 8 != 0 || sz < 2 * H || sq < H) return GPIC_ESHAPE;
   if (!aligned16(z) || !aligned16(q) || !aligned16(ws)) return GPIC_EALIGN;
@@ -1917,6 +1922,7 @@ int gpic_fp8_swiglu_tcast(const uint16_t *z, int64_t M, int64_t H, int64_t sz, u
 
 int gpic_fp8_swiglu_tcast_t(const uint16_t *z, int64_t M, int64_t H, int64_t sz, uint16_t *a, uint8_t *q, int64_t sq,
                             uint8_t *qt, int64_t ldt, float *dequant, void *ws, void *stream) {
+  status_scope();
   if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !q)) || (H > 0 && ldt > 0 && !qt))
     return GPIC_EINVAL;
   if (!qt && ldt != 0) return GPIC_EINVAL;
@@ -1984,6 +1990,7 @@ static int swiglu_bwd_common(const uint16_t *z, const uint16_t *da, int64_t M, i
 
 int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                         uint16_t *dz, uint8_t *dzq, float *dequant, void *ws, void *stream) {
+  status_scope();
   if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !da || !dzq))) return GPIC_EINVAL;
   if (H % 8 != 0 || sz % 8 != 0 || sda % 8 != 0 || sz < 2 * H || sda < H) return GPIC_ESHAPE;
   if (!aligned16(z) || !aligned16(da) || (dz && !aligned16(dz)) || !aligned16(dzq) || !aligned16(ws))
@@ -1994,6 +2001,7 @@ int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_
 int gpic_fp8_swiglu_bwd_t(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H, int64_t sz, int64_t sda,
                           uint16_t *dz, uint8_t *dzq, uint8_t *dzqt, int64_t ldt, float *dequant, void *ws,
                           void *stream) {
+  status_scope();
   if (M < 0 || H < 0 || !dequant || !ws || (M > 0 && H > 0 && (!z || !da || !dzq)) || (H > 0 && ldt > 0 && !dzqt) ||
       (!dz && M > 0 && H > 0 && ldt == 0))
     return GPIC_EINVAL;

@@ -686,6 +686,7 @@ size_t gpic_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
                   const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, int fast_accum,
                   void *ws, size_t ws_bytes, void *stream) {
+  status_scope();
   (void)fast_accum;
   if (M < 0 || N < 0 || K < 0 || !sa || !sb || (M > 0 && N > 0 && !C)) return GPIC_EINVAL;
   if (K % 16 != 0 || N % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldc % 8 != 0) return GPIC_ESHAPE;
@@ -698,6 +699,7 @@ int gpic_fp8_gemm(const uint8_t *A, int64_t lda, const float *sa, const uint8_t 
 int gpic_fp8_gemm_mn(const uint8_t *A, int64_t lda, const float *sa, const uint8_t *B, int64_t ldb, const float *sb,
                      const uint16_t *bias, uint16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K, void *ws,
                      size_t ws_bytes, void *stream) {
+  status_scope();
   if (M < 0 || N < 0 || K < 0 || !sa || !sb || (M > 0 && N > 0 && !C)) return GPIC_EINVAL;
   if (M % 16 != 0 || N % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || ldc % 8 != 0) return GPIC_ESHAPE;
   // every load offset (K row x row stride) is a 32-bit buffer offset, and so is every C offset (ldc < 2^22)

@@ -22,6 +22,11 @@ constexpr size_t kCastWorkspaceBytes = 44 * 1024;     // partial maxima (4 KiB),
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The first statement of every entry point that launches kernels: clears the calling thread's last HIP error, so
+// that the hipGetLastError() the entry point returns after its launches reports those launches and not an earlier,
+// unrelated failure on the same thread.
+static inline void status_scope() { (void)hipGetLastError(); }
+
 // Device attributes the launches depend on, cached per device: each GPU of the process gets its own entry (the
 // library may run on several), and a cache slot is written whole by whichever thread computes it first (all compute
 // the same value). Devices past kMaxDevices are queried on every call.

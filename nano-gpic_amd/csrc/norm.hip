@@ -11,8 +11,10 @@
 // The arithmetic, row by row, in fp32; fma() is one fused multiply-add (one rounding, as Triton compiles the
 // reference's a * b + c on the GPU), every other operation rounds on its own (-ffp-contract=off):
 //   xb = bf16(fma(gate, a, x))                  (site 2; site 1: xb = x)
-//   ss: lane l of the row's wave accumulates ss = fma(xb, xb, ss) over its elements 4 (l + 64 j) + e in the order
-//       j, e, then the 64 lane sums are combined by the butterfly v += v[lane ^ o], o = 32, 16, 8, 4, 2, 1
+//   ss: lane l of the row's wave accumulates ss = fma(xb, xb, ss) over its elements 4 (l + 64 j) + e < C in the
+//       order j, e, then the 64 lane sums are combined by the butterfly v += v[lane ^ o], o = 32, 16, 8, 4, 2, 1
+// Rows are C % 4 == 0 elements wide: a lane's group j of 4 elements is either wholly in the row or wholly past its end
+// (the last group of a row whose C is not a multiple of 256 covers lanes 0 .. (C % 256) / 4 - 1 only).
 //   rstd = 1 / sqrt(ss / C + eps)               (IEEE division and square root)
 //   n = bf16(w * (xb * rstd));  h = bf16(fma(n, 1 + scale, shift))
 // The reference computes the same expression with Triton's reduction order and libdevice's rsqrt, whose last bits
@@ -48,6 +50,31 @@ struct NormArgs {
 };
 
 __device__ __forceinline__ u32x2 ld8(const uint16_t *p) { return *reinterpret_cast<const u32x2 *>(p); }
+
+// Rows whose width C is no multiple of 256 (kTail): a lane holds kJ = ceil(C / 256) groups and its last one may lie
+// past the row's end. Such a group loads the row's first group instead (in bounds, the address a per-lane offset from
+// the row's base like every other group's) and takes zeros in place of what it read: zeros add exactly nothing to a
+// row's sum of squares and give h = 0 (no effect on the maximum), so only the stores need the predicate. Without
+// kTail these are the plain loads.
+template <int kJ, bool kTail>
+__device__ __forceinline__ bool grp_on(int lane, int j, int C) {
+  return !kTail || j + 1 < kJ || 4 * (lane + 64 * j) < C;
+}
+template <int kJ, bool kTail>
+__device__ __forceinline__ uint32_t grp_off(int lane, int j, int C) {
+  const uint32_t c = 4u * (uint32_t)(lane + 64 * j);
+  return grp_on<kJ, kTail>(lane, j, C) ? c : 0u;
+}
+template <int kJ, bool kTail>
+__device__ __forceinline__ u32x2 ld8_grp(const uint16_t *p, int lane, int j, int C) {
+  const u32x2 v = ld8(p + grp_off<kJ, kTail>(lane, j, C));
+  return grp_on<kJ, kTail>(lane, j, C) ? v : u32x2{0u, 0u};
+}
+template <int kJ, bool kTail>
+__device__ __forceinline__ float4 ld16f_grp(const float *p, int lane, int j, int C) {
+  const float4 v = *reinterpret_cast<const float4 *>(p + grp_off<kJ, kTail>(lane, j, C));
+  return grp_on<kJ, kTail>(lane, j, C) ? v : float4{0.0f, 0.0f, 0.0f, 0.0f};
+}
 
 // No memory access and no instruction moves across this point, neither in the compiler's IR nor in its machine
 // scheduler: keeps loads in the phase they belong to (hoisted loads hold registers from the top of the kernel).
@@ -89,16 +116,18 @@ __device__ __forceinline__ float wave_sum_butterfly(float v) {
 
 // One row's h (this lane's groups j < J: elements 4 (lane + 64 j) .. + 3) as packed bf16 in H, and its amax bits
 // (NaN excluded). kStore: write x_new (site 2), rstd (lane 0) and h (when p.h) as well. The groups are handled with a
-// compile-time count when kJ > 0 (held in registers) or a run-time count C / 256 otherwise (then H is not kept).
+// compile-time count when kJ > 0 (held in registers) or a run-time count ceil(C / 256) otherwise (then H is not
+// kept); a group past the row's end is skipped.
 template <int kJ, bool kStore>
 __device__ __forceinline__ uint32_t norm_row(const NormArgs &p, int64_t row, u32x2 *H) {
   const int lane = threadIdx.x & 63;
-  const int J = kJ > 0 ? kJ : p.C / 256;
+  const int J = kJ > 0 ? kJ : (p.C + 255) / 256;
   const int64_t b = row / p.ntok;
   const uint16_t *xr = p.x + row * p.C;
   float ss = 0.0f;
   for (int j = 0; j < J; j++) {   // pass over the row: x_new and the sum of squares
     const int c = 4 * (lane + 64 * j);
+    if (c >= p.C) break;           // (this lane's groups past the row's end)
     float x[4];
     unpack4(ld8(xr + c), x);
     if (p.a) {
@@ -119,6 +148,7 @@ __device__ __forceinline__ uint32_t norm_row(const NormArgs &p, int64_t row, u32
   uint32_t m = 0;
   for (int j = 0; j < J; j++) {   // h, from x_new as rounded (re-read from the cache for site 2)
     const int c = 4 * (lane + 64 * j);
+    if (c >= p.C) break;
     float x[4], sh[4], sc[4];
     if (p.a) {
       float av[4], gv[4];
@@ -166,7 +196,7 @@ __device__ __forceinline__ uint32_t cast4_packed(u32x2 hw, float s) {
 // (same values, so the same maximum) and store nothing. kUni: every row of a wave lies in one batch (ntok % kR ==
 // 0), so gate, shift and scale are one vector per wave. row0 must be wave-uniform (a scalar: the rows' addresses are
 // then scalar bases plus one per-lane offset).
-template <int kJ, int kR, bool kUni, bool kRes>
+template <int kJ, int kR, bool kUni, bool kRes, bool kTail>
 __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int lane, u32x2 (&X)[kR][kJ]) {
   const int64_t C = p.C;
   auto rowi = [&](int r) { return min(row0 + r, p.rows - 1); };
@@ -174,7 +204,7 @@ __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int 
 #pragma unroll
   for (int r = 0; r < kR; r++)
 #pragma unroll
-    for (int j = 0; j < kJ; j++) X[r][j] = ld8(p.x + rowi(r) * C + 4 * (lane + 64 * j));
+    for (int j = 0; j < kJ; j++) X[r][j] = ld8_grp<kJ, kTail>(p.x + rowi(r) * C, lane, j, p.C);
   const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);   // rows of this wave that exist
   // site 2: a (and, per row unless kUni, gate) through a ring of kD rows: the loads of row r + kD - 1 are issued
   // before row r is used, and the fences keep the compiler from hoisting every row's loads to the top (x and a of
@@ -184,14 +214,14 @@ __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int 
   auto load_a = [&](int r) {
 #pragma unroll
     for (int j = 0; j < kJ; j++) {
-      A[r % kD][j] = ld8(p.a + rowi(r) * C + 4 * (lane + 64 * j));
-      if (!kUni) Gt[r % kD][j] = ld8(p.gate + bat(r) * p.sg + 4 * (lane + 64 * j));
+      A[r % kD][j] = ld8_grp<kJ, kTail>(p.a + rowi(r) * C, lane, j, p.C);
+      if (!kUni) Gt[r % kD][j] = ld8_grp<kJ, kTail>(p.gate + bat(r) * p.sg, lane, j, p.C);
     }
   };
   if (kRes) {
     if (kUni) {
 #pragma unroll
-      for (int j = 0; j < kJ; j++) G0[j] = ld8(p.gate + bat(0) * p.sg + 4 * (lane + 64 * j));
+      for (int j = 0; j < kJ; j++) G0[j] = ld8_grp<kJ, kTail>(p.gate + bat(0) * p.sg, lane, j, p.C);
     }
 #pragma unroll
     for (int r = 0; r < kD - 1 && r < kR; r++) load_a(r);
@@ -227,7 +257,8 @@ __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int 
     asm volatile("" : "+v"(S[r]));
     if (kRes && r < nr) {
 #pragma unroll
-      for (int j = 0; j < kJ; j++) *reinterpret_cast<u32x2 *>(p.xn + (row0 + r) * C + 4 * (lane + 64 * j)) = X[r][j];
+      for (int j = 0; j < kJ; j++)
+        if (grp_on<kJ, kTail>(lane, j, p.C)) *reinterpret_cast<u32x2 *>(p.xn + (row0 + r) * C + 4 * (lane + 64 * j)) = X[r][j];
     }
   }
   // phase 2: the kR butterflies interleaved, rstd
@@ -248,19 +279,18 @@ __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int 
   float mf = 0.0f;
 #pragma unroll
   for (int j = 0; j < kJ; j++) {
-    const int c = 4 * (lane + 64 * j);
-    const float4 wv = *reinterpret_cast<const float4 *>(p.w + c);
+    const float4 wv = ld16f_grp<kJ, kTail>(p.w, lane, j, p.C);
     const float w4[4] = {wv.x, wv.y, wv.z, wv.w};
     float sh[4], sc[4];
     if (kUni) {
-      unpack4(ld8(p.shift + bat(0) * p.ssh + c), sh);
-      unpack4(ld8(p.scale + bat(0) * p.ssc + c), sc);
+      unpack4(ld8_grp<kJ, kTail>(p.shift + bat(0) * p.ssh, lane, j, p.C), sh);
+      unpack4(ld8_grp<kJ, kTail>(p.scale + bat(0) * p.ssc, lane, j, p.C), sc);
     }
 #pragma unroll
     for (int r = 0; r < kR; r++) {
       if (!kUni) {
-        unpack4(ld8(p.shift + bat(r) * p.ssh + c), sh);
-        unpack4(ld8(p.scale + bat(r) * p.ssc + c), sc);
+        unpack4(ld8_grp<kJ, kTail>(p.shift + bat(r) * p.ssh, lane, j, p.C), sh);
+        unpack4(ld8_grp<kJ, kTail>(p.scale + bat(r) * p.ssc, lane, j, p.C), sc);
       }
       float x[4], hv[4];
       unpack4(X[r][j], x);
@@ -283,7 +313,7 @@ __device__ __forceinline__ float norm_rows(const NormArgs &p, int64_t row0, int 
 
 // Single pass: wave w of workgroup g takes rows (4 g + w) kR .. + kR - 1 through norm_rows, the workgroups fold their
 // maxima (gpic_once.h), and each casts its rows from its registers.
-template <int kJ, int kR, bool kUni, bool kRes>
+template <int kJ, int kR, bool kUni, bool kRes, bool kTail>
 __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *ws, uint32_t wait_ticks) {
   const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -291,7 +321,7 @@ __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *w
   const int64_t C = p.C;
   const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);   // rows of this wave that exist
   u32x2 X[kR][kJ];
-  const float mf = norm_rows<kJ, kR, kUni, kRes>(p, row0, lane, X);
+  const float mf = norm_rows<kJ, kR, kUni, kRes, kTail>(p, row0, lane, X);
   uint32_t tk;
   const uint32_t g = once_fold(block_max_u32(__float_as_uint(bf16_round(mf))), ws, ep, wait_ticks, tk, [&](int cb) {
     // workgroup cb's maximum from its rows (nothing stored): for a partial that did not appear in time
@@ -310,8 +340,9 @@ __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *w
     if (r < nr) {
 #pragma unroll
       for (int j = 0; j < kJ; j++)
-        __builtin_nontemporal_store(cast4_packed(X[r][j], scale),
-                                    reinterpret_cast<uint32_t *>(p.hq + (row0 + r) * C + 4 * (lane + 64 * j)));
+        if (grp_on<kJ, kTail>(lane, j, p.C))
+          __builtin_nontemporal_store(cast4_packed(X[r][j], scale),
+                                      reinterpret_cast<uint32_t *>(p.hq + (row0 + r) * C + 4 * (lane + 64 * j)));
     }
   once_done(ws, tk);
 }
@@ -320,7 +351,7 @@ __global__ __launch_bounds__(256, 4) void norm_q_once_kernel(NormArgs p, void *w
 // writes h when asked, and leaves the largest |h| of its rows in partial[g] (float bits of the bf16 value).
 // (Two workgroups per CU and 256 registers a lane: it loops over its groups, so it needs no more residency than that,
 // and the loop keeps more live than the single pass.) kH: write h.
-template <int kJ, int kR, bool kUni, bool kRes, bool kH>
+template <int kJ, int kR, bool kUni, bool kRes, bool kH, bool kTail>
 __global__ __launch_bounds__(256, 2) void norm_rows_kernel(NormArgs p, uint32_t *__restrict__ partial, int64_t groups) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t C = p.C;
@@ -329,14 +360,14 @@ __global__ __launch_bounds__(256, 2) void norm_rows_kernel(NormArgs p, uint32_t 
     const int64_t row0 = (g * 4 + wave) * kR;
     const int nr = (int)min<int64_t>(max<int64_t>(p.rows - row0, 0), kR);
     u32x2 X[kR][kJ];
-    mf = fmaxf(mf, norm_rows<kJ, kR, kUni, kRes>(p, row0, lane, X));
+    mf = fmaxf(mf, norm_rows<kJ, kR, kUni, kRes, kTail>(p, row0, lane, X));
     if (kH) {
 #pragma unroll
       for (int r = 0; r < kR; r++)
         if (r < nr) {
 #pragma unroll
           for (int j = 0; j < kJ; j++)
-            *reinterpret_cast<u32x2 *>(p.h + (row0 + r) * C + 4 * (lane + 64 * j)) = X[r][j];
+            if (grp_on<kJ, kTail>(lane, j, p.C)) *reinterpret_cast<u32x2 *>(p.h + (row0 + r) * C + 4 * (lane + 64 * j)) = X[r][j];
         }
     }
   }
@@ -368,8 +399,9 @@ __global__ __launch_bounds__(256) void norm_cast_kernel(NormArgs p, const uint32
   for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < p.rows; row += nw) {
     const int64_t b = row / p.ntok;
     const float rstd = p.rstd[row];
-    for (int j = 0; j < p.C / 256; j++) {
+    for (int j = 0; j < (p.C + 255) / 256; j++) {
       const int c = 4 * (lane + 64 * j);
+      if (c >= p.C) break;
       __builtin_nontemporal_store(cast4_packed(h_from_stats(p, row, b, rstd, c), scale),
                                   reinterpret_cast<uint32_t *>(p.hq + row * p.C + c));
     }
@@ -378,13 +410,14 @@ __global__ __launch_bounds__(256) void norm_cast_kernel(NormArgs p, const uint32
 
 // ------------------------------------------------------------------------------------------- host side
 
-static DeviceCache g_cap_norm[9][2][2];   // [kJ][kUni][kRes]
+static DeviceCache g_cap_norm[9][2][2][2];   // [kJ][kUni][kRes][kTail]
 struct NormCacheInit {
   NormCacheInit() {
     for (auto &cj : g_cap_norm)
       for (auto &cu : cj)
-        for (auto &c : cu)
-          for (int i = 0; i < kMaxDevices; i++) c[i] = -1;
+        for (auto &cr : cu)
+          for (auto &c : cr)
+            for (int i = 0; i < kMaxDevices; i++) c[i] = -1;
   }
 };
 static NormCacheInit g_norm_cache_init;
@@ -394,40 +427,49 @@ static NormCacheInit g_norm_cache_init;
 template <int kJ>
 constexpr int kRowsOnce = kJ >= 3 ? 32 / kJ : 10;
 
-template <int kJ, bool kUni, bool kRes>
+template <int kJ, bool kUni, bool kRes, bool kTail>
 static bool launch_norm_once_t(const NormArgs &p, void *ws, hipStream_t st) {
   constexpr int kR = kRowsOnce<kJ>;
-  const int cap = once_capacity(reinterpret_cast<const void *>(&norm_q_once_kernel<kJ, kR, kUni, kRes>),
-                                g_cap_norm[kJ][kUni][kRes], 256);
+  const int cap = once_capacity(reinterpret_cast<const void *>(&norm_q_once_kernel<kJ, kR, kUni, kRes, kTail>),
+                                g_cap_norm[kJ][kUni][kRes][kTail], 256);
   const int64_t wgs = (p.rows + 4 * kR - 1) / (4 * kR);
   if (cap <= 0 || wgs > cap) return false;
-  norm_q_once_kernel<kJ, kR, kUni, kRes><<<(int)wgs, 256, 0, st>>>(p, ws, once_wait_ticks());
+  norm_q_once_kernel<kJ, kR, kUni, kRes, kTail><<<(int)wgs, 256, 0, st>>>(p, ws, once_wait_ticks());
   return true;
 }
 
 // The first of the two passes for rows of at most 2048: one partial maximum per workgroup in `partial` (at most
 // kMaxParts workgroups, each taking every G-th group of 4 kR rows). Returns the number of partials.
-template <int kJ, bool kUni, bool kRes>
+template <int kJ, bool kUni, bool kRes, bool kTail>
 static int launch_norm_rows_t(const NormArgs &p, uint32_t *partial, hipStream_t st) {
   constexpr int kR = kRowsOnce<kJ>;
   const int64_t groups = (p.rows + 4 * kR - 1) / (4 * kR);
   const int g = (int)std::min<int64_t>(groups, kMaxParts);
-  if (p.h) norm_rows_kernel<kJ, kR, kUni, kRes, true><<<g, 256, 0, st>>>(p, partial, groups);
-  else norm_rows_kernel<kJ, kR, kUni, kRes, false><<<g, 256, 0, st>>>(p, partial, groups);
+  if (p.h) norm_rows_kernel<kJ, kR, kUni, kRes, true, kTail><<<g, 256, 0, st>>>(p, partial, groups);
+  else norm_rows_kernel<kJ, kR, kUni, kRes, false, kTail><<<g, 256, 0, st>>>(p, partial, groups);
   return g;
 }
 
+template <int kJ, bool kTail>
+static int launch_norm_rows_w(const NormArgs &p, uint32_t *partial, hipStream_t st) {
+  const bool uni = p.ntok % kRowsOnce<kJ> == 0;
+  if (p.a)
+    return uni ? launch_norm_rows_t<kJ, true, true, kTail>(p, partial, st)
+               : launch_norm_rows_t<kJ, false, true, kTail>(p, partial, st);
+  return uni ? launch_norm_rows_t<kJ, true, false, kTail>(p, partial, st)
+             : launch_norm_rows_t<kJ, false, false, kTail>(p, partial, st);
+}
+
+// kJ = ceil(C / 256) groups per lane; rows with C % 256 != 0 take the instances with the partial last group.
 template <int kJ>
 static int launch_norm_rows(const NormArgs &p, uint32_t *partial, hipStream_t st) {
-  const bool uni = p.ntok % kRowsOnce<kJ> == 0;
-  if (p.a) return uni ? launch_norm_rows_t<kJ, true, true>(p, partial, st) : launch_norm_rows_t<kJ, false, true>(p, partial, st);
-  return uni ? launch_norm_rows_t<kJ, true, false>(p, partial, st) : launch_norm_rows_t<kJ, false, false>(p, partial, st);
+  return p.C % 256 ? launch_norm_rows_w<kJ, true>(p, partial, st) : launch_norm_rows_w<kJ, false>(p, partial, st);
 }
 
 // Pass 1 of the two passes: the multi-row kernel for rows of at most 2048, else the row-at-a-time one. Returns the
 // number of partial maxima written to `partial`.
 static int norm_first_pass(const NormArgs &p, uint32_t *partial, hipStream_t st) {
-  switch (p.C / 256) {
+  switch ((p.C + 255) / 256) {
     case 1: return launch_norm_rows<1>(p, partial, st);
     case 2: return launch_norm_rows<2>(p, partial, st);
     case 3: return launch_norm_rows<3>(p, partial, st);
@@ -444,12 +486,18 @@ static int norm_first_pass(const NormArgs &p, uint32_t *partial, hipStream_t st)
   }
 }
 
+template <int kJ, bool kTail>
+static bool launch_norm_once_w(const NormArgs &p, void *ws, hipStream_t st) {
+  const bool uni = p.ntok % kRowsOnce<kJ> == 0;
+  if (p.a)
+    return uni ? launch_norm_once_t<kJ, true, true, kTail>(p, ws, st) : launch_norm_once_t<kJ, false, true, kTail>(p, ws, st);
+  return uni ? launch_norm_once_t<kJ, true, false, kTail>(p, ws, st) : launch_norm_once_t<kJ, false, false, kTail>(p, ws, st);
+}
+
 template <int kJ>
 static bool launch_norm_once(const NormArgs &p, void *ws, hipStream_t st) {
   if (!once_enabled() || p.h) return false;   // (bf16 h as well: the two passes)
-  const bool uni = p.ntok % kRowsOnce<kJ> == 0;
-  if (p.a) return uni ? launch_norm_once_t<kJ, true, true>(p, ws, st) : launch_norm_once_t<kJ, false, true>(p, ws, st);
-  return uni ? launch_norm_once_t<kJ, true, false>(p, ws, st) : launch_norm_once_t<kJ, false, false>(p, ws, st);
+  return p.C % 256 ? launch_norm_once_w<kJ, true>(p, ws, st) : launch_norm_once_w<kJ, false>(p, ws, st);
 }
 
 
@@ -476,7 +524,7 @@ struct NormBwdArgs {
   int C, tiles_b, P;
 };
 
-template <int kJ, bool kRes, bool kDxn>
+template <int kJ, bool kRes, bool kDxn, bool kTail>
 __global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pid = blockIdx.x;
@@ -488,11 +536,10 @@ __global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
   u32x2 SC[kJ], GT[kJ];
 #pragma unroll
   for (int j = 0; j < kJ; j++) {
-    const int c = 4 * (lane + 64 * j);
-    const float4 wv = *reinterpret_cast<const float4 *>(p.w + c);
+    const float4 wv = ld16f_grp<kJ, kTail>(p.w, lane, j, p.C);
     w4[j][0] = wv.x, w4[j][1] = wv.y, w4[j][2] = wv.z, w4[j][3] = wv.w;
-    SC[j] = ld8(p.scale + b * p.ssc + c);
-    if (kRes) GT[j] = ld8(p.gate + b * p.sg + c);
+    SC[j] = ld8_grp<kJ, kTail>(p.scale + b * p.ssc, lane, j, p.C);
+    if (kRes) GT[j] = ld8_grp<kJ, kTail>(p.gate + b * p.sg, lane, j, p.C);
   }
   float ash[kJ][4], asc[kJ][4], aw[kJ][4], ag[kJ][4];
 #pragma unroll
@@ -500,17 +547,18 @@ __global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
 #pragma unroll
     for (int e = 0; e < 4; e++) ash[j][e] = asc[j][e] = aw[j][e] = ag[j][e] = 0.0f;
   // A row's loads (packed bf16), issued one row ahead: the next row's are in flight while this one is computed.
+  // A group past the row's end (the last one, when C % 256 != 0) loads nothing and takes zeros: every sum and the
+  // row's mean then receive exactly zero from it (its dx and da are not stored).
   constexpr int kPre = kJ <= 4 ? 1 : 0;
   u32x2 DH[2][kJ], XS[2][kJ], AV[2][kJ], DX[2][kJ];
   auto load_row = [&](int buf, int64_t r) {
     const int64_t row = b * p.ntok + r;
 #pragma unroll
     for (int j = 0; j < kJ; j++) {
-      const int64_t o = row * C + 4 * (lane + 64 * j);
-      DH[buf][j] = ld8(p.dh + o);
-      XS[buf][j] = ld8(p.xs + o);
-      if (kRes) AV[buf][j] = ld8(p.a + o);
-      if (kDxn) DX[buf][j] = ld8(p.dxn + o);
+      DH[buf][j] = ld8_grp<kJ, kTail>(p.dh + row * C, lane, j, p.C);
+      XS[buf][j] = ld8_grp<kJ, kTail>(p.xs + row * C, lane, j, p.C);
+      if (kRes) AV[buf][j] = ld8_grp<kJ, kTail>(p.a + row * C, lane, j, p.C);
+      if (kDxn) DX[buf][j] = ld8_grp<kJ, kTail>(p.dxn + row * C, lane, j, p.C);
     }
   };
   auto do_row = [&](int buf, int64_t r) {
@@ -548,6 +596,7 @@ __global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
 #pragma unroll
     for (int j = 0; j < kJ; j++) {   // t and dt again from the packed row (fewer registers than keeping them)
       const int c = 4 * (lane + 64 * j);
+      const bool on = grp_on<kJ, kTail>(lane, j, p.C);
       float dh[4], x[4], sc[4], dx[4];
       unpack4(DH[buf][j], dh);
       unpack4(XS[buf][j], x);
@@ -570,10 +619,11 @@ __global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
         unpack4(GT[j], g);
 #pragma unroll
         for (int e = 0; e < 4; e++) ag[j][e] = __builtin_fmaf(dx[e], av[e], ag[j][e]);
-        *reinterpret_cast<u32x2 *>(p.da + row * C + c) =
-            u32x2{pack_bf16(dx[0] * g[0], dx[1] * g[1]), pack_bf16(dx[2] * g[2], dx[3] * g[3])};
+        if (on)
+          *reinterpret_cast<u32x2 *>(p.da + row * C + c) =
+              u32x2{pack_bf16(dx[0] * g[0], dx[1] * g[1]), pack_bf16(dx[2] * g[2], dx[3] * g[3])};
       }
-      *reinterpret_cast<u32x2 *>(p.dx + row * C + c) = u32x2{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3])};
+      if (on) *reinterpret_cast<u32x2 *>(p.dx + row * C + c) = u32x2{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3])};
     }
   };
   int64_t r = r0 + wave;
@@ -598,6 +648,7 @@ __global__ __launch_bounds__(256, 2) void norm_bwd_kernel(NormBwdArgs p) {
 #pragma unroll
   for (int j = 0; j < kJ; j++) {
     const int c = 4 * (lane + 64 * j);
+    if (!grp_on<kJ, kTail>(lane, j, p.C)) continue;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       red[(wave * kNS + 0) * C + c + e] = ash[j][e];
@@ -669,12 +720,18 @@ __global__ __launch_bounds__(256) void norm_bwd_reduce_kernel(const float *__res
   }
 }
 
+template <int kJ, bool kTail>
+static void launch_norm_bwd_w(const NormBwdArgs &p, bool res, hipStream_t st) {
+  const size_t lds = (size_t)4 * (res ? 4 : 3) * p.C * sizeof(float);
+  if (!res) norm_bwd_kernel<kJ, false, false, kTail><<<p.P, 256, lds, st>>>(p);
+  else if (p.dxn) norm_bwd_kernel<kJ, true, true, kTail><<<p.P, 256, lds, st>>>(p);
+  else norm_bwd_kernel<kJ, true, false, kTail><<<p.P, 256, lds, st>>>(p);
+}
+
 template <int kJ>
 static void launch_norm_bwd(const NormBwdArgs &p, bool res, hipStream_t st) {
-  const size_t lds = (size_t)4 * (res ? 4 : 3) * p.C * sizeof(float);
-  if (!res) norm_bwd_kernel<kJ, false, false><<<p.P, 256, lds, st>>>(p);
-  else if (p.dxn) norm_bwd_kernel<kJ, true, true><<<p.P, 256, lds, st>>>(p);
-  else norm_bwd_kernel<kJ, true, false><<<p.P, 256, lds, st>>>(p);
+  if (p.C % 256) launch_norm_bwd_w<kJ, true>(p, res, st);
+  else launch_norm_bwd_w<kJ, false>(p, res, st);
 }
 
 static int64_t norm_bwd_parts(int64_t rows, int64_t ntok) {
@@ -690,10 +747,11 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
                              const uint16_t *shift, int64_t ssh, const uint16_t *scale, int64_t ssc, int64_t rows,
                              int64_t ntok, int64_t C, float eps, uint16_t *xn, uint16_t *h, float *rstd, uint8_t *hq,
                              float *dequant, void *ws, void *stream) {
+  status_scope();
   const bool cast = dequant != nullptr;   // else the norm alone
   if (rows < 0 || C <= 0 || ntok <= 0 || !ws || !w || !shift || !scale) return GPIC_EINVAL;
   if (rows > 0 && (!x || !rstd || (cast ? !hq : !h) || (a && (!gate || !xn)))) return GPIC_EINVAL;
-  if (C % 256 != 0 || rows % ntok != 0 || ssh % 4 != 0 || ssc % 4 != 0 || (a && sg % 4 != 0) || ssh < C || ssc < C ||
+  if (C % 4 != 0 || rows % ntok != 0 || ssh % 4 != 0 || ssc % 4 != 0 || (a && sg % 4 != 0) || ssh < C || ssc < C ||
       (a && sg < C) || C > (1 << 20))
     return GPIC_ESHAPE;
   if (!aligned16(x) || (a && !aligned16(a)) || ((uintptr_t)gate & 7u) || !aligned16(w) || ((uintptr_t)shift & 7u) ||
@@ -711,7 +769,7 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
     return (int)hipGetLastError();
   }
   bool done = false;
-  switch (C / 256) {
+  switch ((C + 255) / 256) {
     case 1: done = launch_norm_once<1>(p, ws, st); break;
     case 2: done = launch_norm_once<2>(p, ws, st); break;
     case 3: done = launch_norm_once<3>(p, ws, st); break;
@@ -741,12 +799,13 @@ int gpic_fp8_res_mod_rmsnorm_bwd(const uint16_t *dh, const uint16_t *dxn, const 
                                  const float *rstd, int64_t rows, int64_t ntok, int64_t C, uint16_t *dx, uint16_t *da,
                                  float *dshift, float *dscale, float *dgate, float *dw, void *ws, size_t ws_bytes,
                                  void *stream) {
+  status_scope();
   const bool res = a != nullptr;
   if (rows < 0 || C <= 0 || ntok <= 0 || !w || !scale || !dshift || !dscale || !dw || (res && (!gate || !dgate)))
     return GPIC_EINVAL;
   if (rows > 0 && (!dh || !xs || !rstd || !dx || (res && !da) || !ws)) return GPIC_EINVAL;
   if (!res && (dxn || dgate)) return GPIC_EINVAL;
-  if (C % 256 != 0 || C > 2048 || rows % ntok != 0 || ssc % 4 != 0 || ssc < C || (res && (sg % 4 != 0 || sg < C)))
+  if (C % 4 != 0 || C > 2048 || rows % ntok != 0 || ssc % 4 != 0 || ssc < C || (res && (sg % 4 != 0 || sg < C)))
     return GPIC_ESHAPE;
   if (!aligned16(dh) || (dxn && !aligned16(dxn)) || !aligned16(xs) || (a && !aligned16(a)) || !aligned16(w) ||
       ((uintptr_t)scale & 7u) || ((uintptr_t)gate & 7u) || !aligned16(dx) || (da && !aligned16(da)) ||
@@ -764,7 +823,7 @@ int gpic_fp8_res_mod_rmsnorm_bwd(const uint16_t *dh, const uint16_t *dxn, const 
   if (P >= (int64_t(1) << 31) / 4 || B * C >= (int64_t(1) << 31)) return GPIC_ESHAPE;
   NormBwdArgs p{dh, dxn, xs, a, gate, w, scale, rstd, dx, da, static_cast<float *>(ws), rows, ntok, sg, ssc, (int)C,
                 (int)((ntok + kBwdRows - 1) / kBwdRows), (int)P};
-  switch (C / 256) {
+  switch ((C + 255) / 256) {
     case 1: launch_norm_bwd<1>(p, res, st); break;
     case 2: launch_norm_bwd<2>(p, res, st); break;
     case 3: launch_norm_bwd<3>(p, res, st); break;

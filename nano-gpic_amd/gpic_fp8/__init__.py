@@ -8,8 +8,8 @@ from .fp8_native import (E4, FMAX, TINY, Fp8Linear, Fp8LinearF8, convert_native,
                          swiglu_bwd_q, swiglu_bwd_t, swiglu_tcast, swiglu_tcast_t, tcast, tcast_t, tcast_t_group,
                          weight_casts, _mm)
 from .fp8 import KEEP, convert_fp8, fp8_filter
-from .norm import (fp8_mod_rmsnorm_linear, fp8_res_mod_rmsnorm_mlp, mod_rmsnorm, res_mod_rmsnorm,
-                   res_mod_rmsnorm_q)
+from .norm import (Fp8NormLinearF8, convert_fused_norm, fp8_mod_rmsnorm_linear, fp8_res_mod_rmsnorm_mlp,
+                   mod_rmsnorm, res_mod_rmsnorm, res_mod_rmsnorm_q)
 from .norm import reference as norm_reference
 
 __all__ = ["E4", "FMAX", "TINY", "Fp8Linear", "Fp8LinearF8", "convert_native", "convert_fp8", "fp8_filter", "KEEP",
@@ -17,4 +17,4 @@ __all__ = ["E4", "FMAX", "TINY", "Fp8Linear", "Fp8LinearF8", "convert_native", "
            "swiglu_bwd", "swiglu_bwd_q", "swiglu_bwd_t", "swiglu_tcast", "swiglu_tcast_t", "tcast", "tcast_t", "tcast_t_group",
            "weight_casts", "_mm",
            "mod_rmsnorm", "res_mod_rmsnorm", "res_mod_rmsnorm_q", "norm_reference", "fp8_mod_rmsnorm_linear",
-           "fp8_res_mod_rmsnorm_mlp"]
+           "fp8_res_mod_rmsnorm_mlp", "Fp8NormLinearF8", "convert_fused_norm"]

@@ -22,14 +22,30 @@ FLAGS = [
 
 
 def build(verbose=False):
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    """Each source compiled to an object in its own hipcc process (in parallel), then linked into the library."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    procs = []
+    for name in SOURCES:
+        obj = os.path.join(objdir, name.replace(".hip", ".o"))
+        cmd = [HIPCC, *compile_flags, "-c", "-I", INCLUDE, "-o", obj, os.path.join(CSRC, name)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((name, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    objs = []
+    for name, obj, pr in procs:
+        _, err = pr.communicate()
+        if pr.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {name} ({pr.returncode}):\n{err[-6000:]}")
+        objs.append(obj)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-I", INCLUDE, "-o", tmp, *srcs]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-6000:]}")
+        raise RuntimeError(f"hipcc link failed ({r.returncode}):\n{r.stderr[-6000:]}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -1,15 +1,17 @@
 """Recipe dispatcher of the FP8 path (baselines/PixelGen/src/utils/fp8.py:13-56): "native" / "native2" convert the
 image blocks with convert_native (phase 1 / 2), "native3" with every GEMM in FP8 (phase 3), "native3+text" also the
-image blocks' kv_y and the text-refine blocks' linears (phase 3, convert_native(text=True)). Every other recipe name
-selects a torchao Float8Linear recipe in the reference; this build implements the native recipes only and refuses the
-others with a ValueError.
+image blocks' kv_y and the text-refine blocks' linears (phase 3, convert_native(text=True)); "native3+norm" and
+"native3+text+norm" also route the image blocks' norm sites through the producer-fused kernels
+(convert_native(fused_norm=True)). Every other recipe name selects a torchao Float8Linear recipe in the reference;
+this build implements the native recipes only and refuses the others with a ValueError.
 """
 import torch
 
 from .fp8_native import convert_native
 
 KEEP = ("adaLN_modulation",)
-NATIVE = {"native": (1, False), "native2": (2, False), "native3": (3, False), "native3+text": (3, True)}
+NATIVE = {"native": (1, False, False), "native2": (2, False, False), "native3": (3, False, False),
+          "native3+text": (3, True, False), "native3+norm": (3, False, True), "native3+text+norm": (3, True, True)}
 
 
 def fp8_filter(mod, fqn):
@@ -33,8 +35,8 @@ def convert_fp8(net, recipe):
         raise ValueError(f"FP8 recipe {recipe!r} is not available: this build implements the MI355X-native recipes "
                          f"{sorted(NATIVE)} only (the reference's other recipes are torchao's Float8Linear)")
     keys = set(net.state_dict())
-    phase, text = NATIVE[recipe]
-    n = convert_native(net, phase=phase, text=text)
+    phase, text, fused_norm = NATIVE[recipe]
+    n = convert_native(net, phase=phase, text=text, fused_norm=fused_norm)
     if set(net.state_dict()) != keys:
         raise RuntimeError("FP8 conversion changed the state-dict keys")
     where = "image and text blocks" if text else "image blocks"

@@ -632,7 +632,7 @@ def _convert_block(blk, phase, attn_names):
     return n
 
 
-def convert_native(net, phase=1, text=False):
+def convert_native(net, phase=1, text=False, fused_norm=False):
     """Phase 1: the image blocks' qkv_x, proj, w12 to Fp8Linear and their SwiGLU's w3 GEMM to the fused path. Phase 2:
     qkv_x and proj as in phase 1, the MLP as one fused FP8 function with FP8 dgrads. Phase 3: qkv_x and proj to
     Fp8LinearF8, the MLP as one function with every GEMM in FP8. Returns the count of GEMMs converted
@@ -640,13 +640,21 @@ def convert_native(net, phase=1, text=False):
     text=True (an extension: the reference's native recipes convert the image blocks only, fp8_native.py:294, while its
     torchao filter also takes the text-refine blocks, fp8.py:31) converts, in the same phase, the image blocks' kv_y
     (over the text tokens) and the text-refine blocks' attention qkv, proj and SwiGLU MLP (JiT_T2I.py:131,227,231,274):
-    linears of M = batch x text tokens, which the same kernels serve."""
+    linears of M = batch x text tokens, which the same kernels serve.
+    fused_norm=True (phase 3 only; an extension: the reference's lever K, JiT_T2I.py:201-207, and its FP8 linears stay
+    separate) also rewires each image block's forward so its two norm sites write h's e4m3 bytes for qkv_x and the
+    MLP directly (gpic_fp8.norm.convert_fused_norm); the GEMM count is unchanged."""
+    if fused_norm and phase != 3:
+        raise ValueError("fused_norm needs phase 3 (the fused norm consumers run every GEMM in FP8)")
     n = 0
     for blk in getattr(net, "blocks", []):
         n += _convert_block(blk, phase, ("qkv_x", "proj", "kv_y") if text else ("qkv_x", "proj"))
     if text:
         for blk in getattr(net, "text_refine_blocks", []):
             n += _convert_block(blk, phase, ("qkv", "proj"))
+    if fused_norm:
+        from .norm import convert_fused_norm
+        convert_fused_norm(net)
     return n
 
 

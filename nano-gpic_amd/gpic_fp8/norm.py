@@ -12,7 +12,9 @@ e4m3 bytes and scale directly, and h itself only when asked. Functions:
 - mod_rmsnorm / res_mod_rmsnorm / reference: the reference's API (fused_norm.py:293-313) with bf16 h, on the kernel;
 - fp8_mod_rmsnorm_linear(x, w_norm, shift, scale, eps, weight, bias): site 1 feeding a phase-3 FP8 linear (qkv_x);
 - fp8_res_mod_rmsnorm_mlp(x, a, gate, w_norm, shift, scale, eps, w12, w3): site 2 feeding the phase-3 FP8 SwiGLU MLP,
-  returning (x_new, mlp output).
+  returning (x_new, mlp output);
+- convert_fused_norm(net) (convert_native(..., fused_norm=True), recipes "native3+norm", "native3+text+norm"): the
+  image blocks' forward routed through the two fused consumers, so a converted model takes the fused path.
 
 The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel (res_mod_rmsnorm_bwd);
 the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
@@ -22,7 +24,20 @@ from typing import Optional
 import torch
 
 from . import _lib as L
-from .fp8_native import E4, fp8_gemm, fp8_gemm_mn, swiglu_bwd_q, swiglu_tcast, tcast, tcast_t
+from .fp8_native import (E4, Fp8LinearF8, fp8_gemm, fp8_gemm_mn, fp8_linear_f8, swiglu_bwd_q, swiglu_tcast, tcast,
+                         tcast_t)
+
+
+# The widest rows the backward kernel takes (its per-column sums live in registers); the forward takes any width.
+BWD_MAX_C = 2048
+
+
+def _check_bwd_width(C, ctx):
+    """Raises in an autograd Function's forward, before its work, when a gradient will be asked of a norm wider than
+    the backward takes (ctx.needs_input_grad: which inputs the graph wants gradients of)."""
+    if C > BWD_MAX_C and any(ctx.needs_input_grad):
+        raise ValueError(f"the norm's backward kernel takes rows of at most {BWD_MAX_C} elements, got C = {C}; "
+                         "run the forward under torch.no_grad() or with inputs that need no gradient")
 
 
 def _vec(t, B, C):
@@ -40,15 +55,15 @@ def _vec(t, B, C):
 def res_mod_rmsnorm_q(x: torch.Tensor, a: torch.Tensor, gate: torch.Tensor, w: torch.Tensor, shift: torch.Tensor,
                       scale: torch.Tensor, eps: float, has_res: bool, want_h: bool, want_q: bool = True
                       ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """x [B, N, C] bf16 (C % 256 == 0), a [B, N, C] bf16 (has_res), gate / shift / scale [B, 1, C], w [C] ->
+    """x [B, N, C] bf16 (C % 4 == 0), a [B, N, C] bf16 (has_res), gate / shift / scale [B, 1, C], w [C] ->
     (x_new [B, N, C] bf16 or an empty tensor, h [B, N, C] bf16 or an empty tensor (want_h), h's e4m3 bytes [B, N, C]
     and their dequantization scale [1] fp32 (empty tensors unless want_q), rstd [B * N] fp32). want_q=False is the
     norm alone (the reference's op)."""
     L.require_gpu(x, a, gate, w, shift, scale)
     if not (want_h or want_q):
         raise ValueError("res_mod_rmsnorm_q needs want_h or want_q")
-    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.shape[2] % 256:
-        raise ValueError(f"the norm kernel takes bf16 x [B, N, C] with C % 256 == 0, got {x.dtype} {tuple(x.shape)}")
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.shape[2] % 4 or x.shape[2] == 0:
+        raise ValueError(f"the norm kernel takes bf16 x [B, N, C] with C % 4 == 0, got {x.dtype} {tuple(x.shape)}")
     B, N, C = x.shape
     xc = L.aligned(x.contiguous())
     ac = L.aligned(a.to(torch.bfloat16).contiguous()) if has_res else None
@@ -147,6 +162,7 @@ class _ResModRMSNorm(torch.autograd.Function):
     """The reference's res_mod_rmsnorm_fwd with bf16 h (fused_norm.py:150-175, 245-287) on the HIP kernel."""
     @staticmethod
     def forward(ctx, x, a, gate, w, shift, scale, eps, has_res):
+        _check_bwd_width(x.shape[-1], ctx)
         xn, h, _, _, rstd = res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, has_res, True, False)
         ctx.has_res = has_res
         ctx.save_for_backward(xn if has_res else x, a if has_res else None, gate if has_res else None, w, shift, scale,
@@ -189,6 +205,7 @@ class _Fp8ModRMSNormLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w_norm, shift, scale, eps, weight, bias):
         B, N, C = x.shape
+        _check_bwd_width(C, ctx)
         _, _, hq, sh, rstd = res_mod_rmsnorm_q(x, x, x, w_norm, shift, scale, eps, False, False)
         hq2 = hq.view(B * N, C)
         wq, wqt, sw = tcast_t(weight)
@@ -218,6 +235,7 @@ class _Fp8ResModRMSNormMLP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, a, gate, w_norm, shift, scale, eps, w12, w3):
         B, N, C = x.shape
+        _check_bwd_width(C, ctx)
         xn, _, hq, sh, rstd = res_mod_rmsnorm_q(x, a, gate, w_norm, shift, scale, eps, True, False)
         hq2 = hq.view(B * N, C)
         w12q, w12qt, s12 = tcast_t(w12)
@@ -257,3 +275,75 @@ def fp8_res_mod_rmsnorm_mlp(x, a, gate, w_norm, shift, scale, eps, w12, w3):
     with torch.autocast("cuda", enabled=False):
         return _Fp8ResModRMSNormMLP.apply(x.to(torch.bfloat16), a.to(torch.bfloat16), gate, w_norm, shift, scale, eps,
                                           w12, w3)
+
+
+# ------------------------------------------------------------------------------------------------ converter
+
+class Fp8NormLinearF8(Fp8LinearF8):
+    """The qkv_x of an image block converted with fused_norm: an Fp8LinearF8 (the same parameters and state-dict keys)
+    that, when its block's forward has handed it the pending site-1 norm, takes the norm's e4m3 output directly
+    (fp8_mod_rmsnorm_linear: h is never written in bf16) instead of a bf16 h. The block passes the attention a
+    placeholder on the meta device in place of h; the attention reads only its shape and hands it to qkv_x
+    (JiT_T2I.py:138-185), so any other use of it fails loudly. Called without a pending norm it is an Fp8LinearF8."""
+    def forward(self, x):
+        pend = self.__dict__.pop("_gpic_norm", None)
+        if pend is None:
+            return fp8_linear_f8(x, self.weight, self.bias)
+        marker, xs, w_norm, shift, scale, eps = pend
+        if x is not marker:
+            raise RuntimeError("qkv_x was handed a pending norm but called on another tensor")
+        return fp8_mod_rmsnorm_linear(xs, w_norm, shift, scale, eps, self.weight, self.bias)
+
+
+def _norm_eps(norm):
+    return getattr(norm, "variance_epsilon", getattr(norm, "eps", 1e-6))
+
+
+def fused_norm_ok(blk):
+    """An image block with the structure of FlattenDiTBlock (JiT_T2I.py:189-210) whose norm sites the fused path can
+    take: norm1 / norm2 RMSNorms of width C (C % 4 == 0, C <= BWD_MAX_C), adaLN_modulation, attn.qkv_x and the SwiGLU
+    MLP's w12 / w3 (no biases) already converted to phase 3."""
+    n1, n2 = getattr(blk, "norm1", None), getattr(blk, "norm2", None)
+    attn, mlp = getattr(blk, "attn", None), getattr(blk, "mlp", None)
+    if n1 is None or n2 is None or attn is None or mlp is None or not hasattr(blk, "adaLN_modulation"):
+        return False
+    qkv = getattr(attn, "qkv_x", None)
+    C = n1.weight.numel() if isinstance(getattr(n1, "weight", None), torch.Tensor) else 0
+    return (isinstance(qkv, Fp8LinearF8) and getattr(mlp, "_fp8", False) and mlp.w12.bias is None and
+            mlp.w3.bias is None and isinstance(getattr(n2, "weight", None), torch.Tensor) and
+            n2.weight.numel() == C and C > 0 and C % 4 == 0 and C <= BWD_MAX_C and qkv.in_features == C)
+
+
+def _fused_block_forward(blk):
+    """FlattenDiTBlock.forward's lever-K branch (JiT_T2I.py:201-207) with each norm site's output cast in the norm:
+    site 1 hands qkv_x h's e4m3 bytes (through Fp8NormLinearF8), site 2 and the MLP run as fp8_res_mod_rmsnorm_mlp.
+    The same operations, in the same order, as that branch over mod_rmsnorm / res_mod_rmsnorm and the phase-3
+    linears, so the outputs and gradients are the same bits; h is never written in bf16."""
+    def forward(x, y, c, pos, mask=None):
+        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = blk.adaLN_modulation(c).chunk(6, dim=-1)
+        qkv = blk.attn.qkv_x
+        marker = torch.empty(x.shape, dtype=torch.bfloat16, device="meta")
+        qkv._gpic_norm = (marker, x, blk.norm1.weight, shift_msa, scale_msa, _norm_eps(blk.norm1))
+        try:
+            a = blk.attn(marker, y, pos, mask)
+        finally:
+            qkv.__dict__.pop("_gpic_norm", None)
+        x, out = fp8_res_mod_rmsnorm_mlp(x, a, gate_msa, blk.norm2.weight, shift_mlp, scale_mlp, _norm_eps(blk.norm2),
+                                         blk.mlp.w12.weight, blk.mlp.w3.weight)
+        return x + gate_mlp * out
+    return forward
+
+
+def convert_fused_norm(net):
+    """Route each phase-3 image block's norm sites through the producer-fused kernels (after convert_native(phase=3)):
+    the block's forward becomes its lever-K branch with h's cast folded into the norm, and its qkv_x an
+    Fp8NormLinearF8. Parameters and state-dict keys are unchanged. Returns the number of blocks rewired."""
+    n = 0
+    for blk in getattr(net, "blocks", []):
+        if not fused_norm_ok(blk) or getattr(blk, "_gpic_fused_norm", False):
+            continue
+        blk.attn.qkv_x.__class__ = Fp8NormLinearF8
+        blk.forward = _fused_block_forward(blk)
+        blk._gpic_fused_norm = True
+        n += 1
+    return n

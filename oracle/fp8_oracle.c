@@ -239,8 +239,8 @@ void gpo_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_t H,
  *   xb = bf16(fmaf(gate, a, x)) (a != NULL; else xb = x);  rstd = 1 / sqrt(ss / C + eps)  (IEEE);
  *   n = bf16(w * (xb * rstd));  h = bf16(fmaf(n, 1 + scale, shift))
  * with ss accumulated in the device's order: lane l (0..63) takes ss = fmaf(xb, xb, ss) over elements
- * 4 (l + 64 j) + e in the order j, e; then the 64 lane sums are combined by the butterfly v_l += v_{l ^ o},
- * o = 32, 16, ..., 1 (C % 256 == 0).
+ * 4 (l + 64 j) + e < C in the order j, e; then the 64 lane sums are combined by the butterfly v_l += v_{l ^ o},
+ * o = 32, 16, ..., 1 (C % 4 == 0: a lane's group of 4 is wholly inside the row or wholly past its end).
  * The reference sums in Triton's order and takes libdevice's rsqrt; its own eager formula (fused_norm.py:305-313)
  * rounds gate * a to bf16 before the add. gate, shift, scale are [B, C] rows (strides sg, ssh, ssc), row r in batch
  * r / ntok. Writes xn (a != NULL), h and rstd. */
@@ -255,13 +255,14 @@ void gpo_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_t *gate,
                      int64_t C, float eps, uint16_t *xn, uint16_t *h, float *rstd) {
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++) {
-        const int64_t b = r / ntok, J = C / 256;
+        const int64_t b = r / ntok, J = (C + 255) / 256;
         float part[64], nxt[64];
         for (int l = 0; l < 64; l++) {
             float s = 0.0f;
             for (int64_t j = 0; j < J; j++)
                 for (int e = 0; e < 4; e++) {
                     const int64_t c = 4 * (l + 64 * j) + e;
+                    if (c >= C) break;
                     const float v = norm_xb(x, a, gate, r * C + c, b * sg + c);
                     s = fmaf(v, v, s);
                 }

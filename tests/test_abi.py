@@ -85,9 +85,9 @@ def test_validation_codes():
     assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, wsp, 0, wsp, wsp, None) == -1
     assert b(wsp, wsp, 4, 16, 32, 16, None, wsp, None, 16, wsp, wsp, None) == -1
     assert b(wsp, wsp, 4, 16, 32, 16, wsp + 8, wsp, wsp, 16, wsp, wsp, None) == -4
-    # the norm sites' producer: C % 256, rows % ntok, strides, nothing to write, misaligned weight
+    # the norm sites' producer: C % 4, rows % ntok, strides, nothing to write, misaligned weight
     nm = lib.gpic_fp8_res_mod_rmsnorm
-    assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 4, 2, 128, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
+    assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 4, 2, 130, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
     assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 5, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
     assert nm(wsp, None, None, 0, wsp, wsp, 255, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp, None) == -3
     assert nm(wsp, None, None, 0, wsp, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, None, None, wsp, None) == -1
@@ -95,11 +95,11 @@ def test_validation_codes():
     assert nm(wsp, None, None, 0, wsp + 8, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, None, None, wsp, wsp, wsp, wsp,
               None) == -4
     assert nm(wsp, wsp, None, 256, wsp, wsp, 256, wsp, 256, 4, 2, 256, 1e-6, wsp, None, wsp, wsp, wsp, wsp, None) == -1
-    # the norm's backward: C % 256 and <= 2048, rows % ntok, site-1 arguments, workspace size, alignment
+    # the norm's backward: C % 4 and <= 2048, rows % ntok, site-1 arguments, workspace size, alignment
     nb = lib.gpic_fp8_res_mod_rmsnorm_bwd
     nbw = lib.gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes
     assert nbw(4, 2, 256) == 4 * 2 * 256 * 4 and nbw(4, 3, 256) == 0 and nbw(0, 1, 256) == 0
-    assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 256, wsp, 4, 2, 128, wsp, None, wsp, wsp, None, wsp, wsp, 1 << 20,
+    assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 256, wsp, 4, 2, 130, wsp, None, wsp, wsp, None, wsp, wsp, 1 << 20,
               None) == -3
     assert nb(wsp, None, wsp, None, None, 0, wsp, wsp, 4096, wsp, 4, 2, 4096, wsp, None, wsp, wsp, None, wsp, wsp,
               1 << 20, None) == -3

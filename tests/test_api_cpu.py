@@ -162,3 +162,106 @@ def test_reference_helper_matches_golden():
         y = torch.from_numpy(g["lin_y"].view(np.int16)).view(torch.bfloat16)
     r = G.reference(x, w, b).float()
     assert torch.linalg.norm(r - y.float()) / torch.linalg.norm(y.float()) < 1e-2
+
+
+class RMSNorm(nn.Module):
+    """baselines/PixelGen/src/models/layers/rmsnorm.py: weight and variance_epsilon"""
+    def __init__(self, d, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.variance_epsilon = eps
+
+
+class NormBlock(Block):
+    """FlattenDiTBlock's modules (JiT_T2I.py:189-198): norm1, attn, norm2, mlp, adaLN_modulation"""
+    def __init__(self, d):
+        super().__init__(d)
+        self.norm1, self.norm2 = RMSNorm(d), RMSNorm(d)
+
+
+class NormNet(nn.Module):
+    def __init__(self, d=32, n=3):
+        super().__init__()
+        self.blocks = nn.ModuleList(NormBlock(d) for _ in range(n))
+        self.text_refine_blocks = nn.ModuleList(TextBlock(d) for _ in range(1))
+
+
+def test_convert_fused_norm():
+    """native3+norm: the same GEMMs as native3, state-dict keys unchanged, each image block's qkv_x an
+    Fp8NormLinearF8 and its forward rewired (idempotent); blocks without norm sites, and the text blocks, keep
+    phase 3's plain linears; fused_norm outside phase 3 is refused."""
+    net = NormNet()
+    net.blocks.append(Block(32))                      # no norm1 / norm2: converted to phase 3, not rewired
+    keys = set(net.state_dict())
+    assert G.convert_fp8(net, "native3+norm") == 4 * 4
+    assert set(net.state_dict()) == keys
+    for b in net.blocks[:3]:
+        assert type(b.attn.qkv_x) is G.Fp8NormLinearF8 and b._gpic_fused_norm and "forward" in b.__dict__
+        assert type(b.attn.proj) is G.Fp8LinearF8 and b.mlp._fp8
+    last = net.blocks[3]
+    assert type(last.attn.qkv_x) is G.Fp8LinearF8 and "forward" not in last.__dict__
+    assert G.convert_fused_norm(net) == 0
+    assert G.convert_fp8(NormNet(), "native3+text+norm") == 3 * 5 + 4
+    with pytest.raises(ValueError, match="phase 3"):
+        G.convert_native(NormNet(), phase=2, fused_norm=True)
+    wide = NormNet(d=4096, n=1)                         # wider than the norm's backward takes: not rewired
+    G.convert_native(wide, phase=3, fused_norm=True)
+    assert type(wide.blocks[0].attn.qkv_x) is G.Fp8LinearF8
+
+
+def test_fp8_norm_linear_without_pending_norm_is_a_linear():
+    """Fp8NormLinearF8 called without a pending norm is Fp8LinearF8 (here: refuses CPU tensors the same way), and
+    a pending norm handed to another tensor raises."""
+    lin = nn.Linear(32, 96, bias=False)
+    lin.__class__ = G.Fp8NormLinearF8
+    x = torch.randn(2, 8, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        lin(x)
+    marker = torch.empty(2, 8, 32, device="meta")
+    lin._gpic_norm = (marker, x, torch.ones(32), x, x, 1e-6)
+    with pytest.raises(RuntimeError, match="another tensor"):
+        lin(x)
+    assert "_gpic_norm" not in lin.__dict__
+
+
+@pytest.mark.parametrize("res", [False, True])
+def test_norm_reference_helper_close_to_oracle(res):
+    """gpic_fp8.norm.reference (the model's eager ops, fused_norm.py:305-313, on CPU) agrees with the oracle's norm
+    within the bf16 roundings the eager ops take separately (x + gate * a and n * (1 + scale) + shift rounded per
+    operation instead of fused)."""
+    from oracle import oracle as O
+    B, N, C, eps = 2, 24, 896, 1e-6
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
+    a = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
+    gate = (torch.randn(B, 1, C, generator=g) * 0.5).to(torch.bfloat16)
+    sh = (torch.randn(B, 1, C, generator=g) * 0.1).to(torch.bfloat16)
+    sc = (torch.randn(B, 1, C, generator=g) * 0.1).to(torch.bfloat16)
+    w = 1 + 0.1 * torch.randn(C, generator=g)
+    xs, h = G.norm_reference(x, a, gate, w, sh, sc, eps, res)
+    u = lambda t, r: t.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(r, C)
+    oxn, oh, _ = O.mod_rmsnorm(u(x, B * N), w.numpy(), u(sh, B), u(sc, B), N, eps, u(a, B * N) if res else None,
+                               u(gate, B) if res else None)
+    hf = torch.from_numpy(O.bf16_to_f32(oh)).view(B, N, C)
+    assert (h.float() - hf).abs().max() <= 2 ** -6 * hf.abs().max()
+    assert torch.linalg.norm(h.float() - hf) / torch.linalg.norm(hf) < 1e-2
+    if res:
+        xf = torch.from_numpy(O.bf16_to_f32(oxn)).view(B, N, C)
+        assert torch.linalg.norm(xs.float() - xf) / torch.linalg.norm(xf) < 1e-2
+
+
+def test_norm_width_checks_before_any_work():
+    """A norm wider than the backward kernel takes (C > 2048) refuses gradients in the forward, before any kernel; with
+    no gradient wanted it goes on to the (GPU-only) forward; widths that are no multiple of 4 are refused."""
+    B, N, C = 1, 4, 2560
+    x = torch.randn(B, N, C, dtype=torch.bfloat16)
+    m = torch.zeros(B, 1, C, dtype=torch.bfloat16)
+    w = torch.ones(C)
+    with pytest.raises(ValueError, match="at most 2048"):
+        G.mod_rmsnorm(x.clone().requires_grad_(), w, m, m, 1e-6)
+    with pytest.raises(ValueError, match="at most 2048"):
+        G.fp8_mod_rmsnorm_linear(x, w.clone().requires_grad_(), m, m, 1e-6, torch.zeros(16, C, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        G.mod_rmsnorm(x, w, m, m, 1e-6)
+    with pytest.raises(RuntimeError, match="GPU only"):   # (the device is checked first)
+        G.res_mod_rmsnorm_q(x[..., :6], x[..., :6], m[..., :6], w[:6], m[..., :6], m[..., :6], 1e-6, True, True)

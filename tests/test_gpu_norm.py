@@ -71,6 +71,10 @@ def knob():
     (2, 100, 768),       # single pass, a partly filled last workgroup
     (3, 64, 2560),       # wider than the single pass takes (C / 256 = 10) -> two passes
     (8, 512, 256),       # narrow rows (10 per wave)
+    (128, 256, 896),     # d11 (the ladder's width 896): the last group of each row half full
+    (128, 256, 1152),    # d13 (1152)
+    (3, 40, 100),        # one partial group per row (lanes 0-24)
+    (2, 33, 2340),       # wider than 2048 and no multiple of 256: the row-at-a-time kernel with a partial group
 ])
 def test_norm_against_oracle(dev, B, N, C, res):
     x, a, gate, w, shift, scale = inputs(B, N, C, B + N + C + res, dev, res, outliers=0.01)
@@ -236,7 +240,8 @@ def _close_f32(got, want, name, rel=1e-5):
 
 
 @pytest.mark.parametrize("res,dxn", [(False, False), (True, True), (True, False)])
-@pytest.mark.parametrize("B,N,C", [(128, 256, 1024), (4, 100, 768), (2, 64, 1792), (3, 50, 2048)])
+@pytest.mark.parametrize("B,N,C", [(128, 256, 1024), (4, 100, 768), (2, 64, 1792), (3, 50, 2048), (64, 128, 896),
+                                   (8, 100, 1152), (3, 30, 100)])
 def test_backward_kernel(dev, B, N, C, res, dxn):
     """The HIP backward (gpic_fp8_res_mod_rmsnorm_bwd) against the reference's formula in torch fp32, and twice in a
     row bit for bit (fixed summation order)."""
@@ -273,3 +278,130 @@ def test_backward_kernel_empty(dev):
                                                       torch.empty(0, device=dev, dtype=torch.float32))
     assert dx.numel() == 0 and da.numel() == 0 and torch.equal(dw, torch.zeros_like(dw))
     assert not dg.any() and not dsh.any() and not dsc.any() and dg.shape == (2, 256)
+
+
+def test_wide_rows_refuse_gradients_before_the_forward(dev):
+    """Rows wider than the backward kernel takes (C > 2048): the forward runs without gradients, and asking for them
+    raises before any work (not in the backward)."""
+    x, a, gate, w, shift, scale = inputs(2, 8, 2560, 43, dev, True)
+    with torch.no_grad():
+        G.res_mod_rmsnorm(x, a, gate, w, shift, scale, 1e-6)
+    with pytest.raises(ValueError, match="at most 2048"):
+        G.res_mod_rmsnorm(x.requires_grad_(), a, gate, w, shift, scale, 1e-6)
+
+
+# ---- a converted model takes the fused path: FlattenDiTBlock's lever-K branch (JiT_T2I.py:189-207)
+
+import copy  # noqa: E402
+
+import torch.nn as nn  # noqa: E402
+
+
+class _RMSNorm(nn.Module):
+    """rmsnorm.py's module: weight, variance_epsilon"""
+    def __init__(self, d):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.variance_epsilon = 1e-6
+
+
+class _Attn(nn.Module):
+    """Attention's linears (qkv_x without bias, proj with, JiT_T2I.py:130,136); x is used for its shape and qkv_x only,
+    as in the reference. The attention itself in fp32."""
+    def __init__(self, d, heads):
+        super().__init__()
+        self.heads = heads
+        self.qkv_x = nn.Linear(d, 3 * d, bias=False)
+        self.proj = nn.Linear(d, d)
+
+    def forward(self, x, y, pos, mask=None):
+        B, N, C = x.shape
+        q, k, v = self.qkv_x(x).float().view(B, N, 3, self.heads, C // self.heads).permute(2, 0, 3, 1, 4)
+        a = torch.softmax(q @ k.transpose(-1, -2).contiguous() / (C // self.heads) ** 0.5, -1)
+        return self.proj((a @ v).transpose(1, 2).reshape(B, N, C).to(torch.bfloat16))
+
+
+class _MLP(nn.Module):
+    def __init__(self, d, h):
+        super().__init__()
+        self.w12 = nn.Linear(d, 2 * h, bias=False)
+        self.w3 = nn.Linear(h, d, bias=False)
+
+    def forward(self, x):
+        x1, x2 = self.w12(x).chunk(2, dim=-1)
+        return self.w3(torch.nn.functional.silu(x1) * x2)
+
+
+class _LeverKBlock(nn.Module):
+    """FlattenDiTBlock's modules; forward = its lever-K branch (JiT_T2I.py:201-207) over the drop-in norm API."""
+    def __init__(self, d, heads):
+        super().__init__()
+        self.norm1 = _RMSNorm(d)
+        self.attn = _Attn(d, heads)
+        self.norm2 = _RMSNorm(d)
+        self.mlp = _MLP(d, 4 * d)
+        self.adaLN_modulation = nn.Sequential(nn.Linear(d, 6 * d, bias=True))
+
+    def forward(self, x, y, c, pos, mask=None):
+        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = self.adaLN_modulation(c).chunk(6, dim=-1)
+        h = G.mod_rmsnorm(x, self.norm1.weight, shift_msa, scale_msa, self.norm1.variance_epsilon)
+        x, h = G.res_mod_rmsnorm(x, self.attn(h, y, pos, mask), gate_msa, self.norm2.weight, shift_mlp, scale_mlp,
+                                 self.norm2.variance_epsilon)
+        return x + gate_mlp * self.mlp(h)
+
+
+class _LeverKNet(nn.Module):
+    def __init__(self, d, heads, n):
+        super().__init__()
+        self.blocks = nn.ModuleList(_LeverKBlock(d, heads) for _ in range(n))
+
+    def forward(self, x, c):
+        for b in self.blocks:
+            x = b(x, None, c, None)
+        return x
+
+
+@pytest.mark.parametrize("C", [896, 1024])
+def test_converted_block_takes_the_fused_path(dev, C, monkeypatch):
+    """convert_fp8(net, "native3+norm") against "native3" on the same weights (the blocks' lever-K branch over
+    mod_rmsnorm / res_mod_rmsnorm and the phase-3 linears): the output and every gradient bit for bit, while the
+    converted model never writes a bf16 h (every call of the norm op casts in the producer). C = 896 is the d11
+    width (rows of 3.5 groups of 256)."""
+    from gpic_fp8 import norm as NM
+    torch.manual_seed(5)
+    B, N = 4, 256
+    net_u = _LeverKNet(C, 8, 2).to(dev).to(torch.bfloat16)
+    for b in net_u.blocks:   # non-trivial norm weights and modulation
+        with torch.no_grad():
+            b.norm1.weight.add_(0.1 * torch.randn_like(b.norm1.weight))
+            b.norm2.weight.add_(0.1 * torch.randn_like(b.norm2.weight))
+            b.adaLN_modulation[0].weight.mul_(5.0)
+    net_f = copy.deepcopy(net_u)
+    assert G.convert_fp8(net_u, "native3") == 8 and G.convert_fp8(net_f, "native3+norm") == 8
+    assert all(type(b.attn.qkv_x) is G.Fp8NormLinearF8 for b in net_f.blocks)
+    x = torch.randn(B, N, C, device=dev).to(torch.bfloat16)
+    c = torch.randn(B, 1, C, device=dev).to(torch.bfloat16)
+    dy = (torch.randn(B, N, C, device=dev) * 0.1).to(torch.bfloat16)
+    calls = []
+    real = NM.res_mod_rmsnorm_q
+
+    def spy(*args, **kw):
+        calls.append(args[8] if len(args) > 8 else kw.get("want_h"))
+        return real(*args, **kw)
+    outs = []
+    for net in (net_f, net_u):
+        monkeypatch.setattr(NM, "res_mod_rmsnorm_q", spy)
+        calls.clear()
+        xl, cl = x.clone().requires_grad_(), c.clone().requires_grad_()
+        y = net(xl, cl)
+        y.backward(dy)
+        outs.append([y, xl.grad, cl.grad] + [p.grad for p in net.parameters()])
+        if net is net_f:
+            assert calls == [False] * 4, calls       # two sites x two blocks, all casting in the norm
+        else:
+            assert calls == [True] * 4, calls        # the reference's ops: bf16 h, then the linears cast it
+        monkeypatch.undo()
+    for got, want in zip(*outs):
+        assert got is not None and want is not None
+        assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got,
+                           want.view(torch.int16) if want.dtype == torch.bfloat16 else want)

@@ -330,7 +330,7 @@ def _oracle_norm(x, a, gate, w, sh, sc, eps):
 
 
 @pytest.mark.parametrize("res", [False, True])
-@pytest.mark.parametrize("C", [256, 768, 1024, 1792])
+@pytest.mark.parametrize("C", [100, 256, 768, 896, 1024, 1152, 1792])
 def test_norm_against_torch(res, C):
     """x_new equals torch's x + gate * a in fp32 rounded once to bf16 (the reference kernel's, fused_norm.py:82); rstd
     is within 2 fp32 ulp of torch.rsqrt(mean(x_new^2) + eps); h equals torch's n = bf16(w * (x_new * rstd)),
@@ -369,10 +369,12 @@ def test_norm_multiply_add_is_fused():
     assert (h != _u16(unfused).reshape(-1, C)).sum() > 50
 
 
-def test_norm_power_of_two_invariance():
+@pytest.mark.parametrize("C", [1024, 1152])
+def test_norm_power_of_two_invariance(C):
     """With eps = 0, scaling x by 2^k leaves h unchanged bit for bit (the sum of squares, the square root and the
-    division scale exactly): a check of the sum's structure that does not restate it."""
-    x, _, _, w, sh, sc = _norm_inputs(2, 33, 1024, 5, False)
+    division scale exactly): a check of the sum's structure that does not restate it (C = 1152: rows whose last
+    group of 256 columns is half full)."""
+    x, _, _, w, sh, sc = _norm_inputs(2, 33, C, 5, False)
     _, h0, r0 = _oracle_norm(x, None, None, w, sh, sc, 0.0)
     for k in (-3, 2, 7):
         _, h1, r1 = _oracle_norm((x.float() * 2.0 ** k).to(torch.bfloat16), None, None, w, sh, sc, 0.0)
