@@ -363,14 +363,28 @@ def cpu_threads():
 
 
 def cpu_model():
+    """The host CPU's model string as lscpu reports it (its "Model name", and "BIOS Model name" when that says more),
+    else /proc/cpuinfo's."""
+    import subprocess
+    names = []
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "BIOS Model name") and v.strip() and v.strip() not in names:
+                names.append(v.strip())
+    except (OSError, subprocess.SubprocessError):
         pass
-    return None
+    if not names:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        names.append(line.split(":", 1)[1].strip())
+                        break
+        except OSError:
+            pass
+    return " / ".join(names) or None
 
 
 def median_s(fn, runs):
@@ -384,11 +398,12 @@ def median_s(fn, runs):
     return sorted(times)[len(times) // 2]
 
 
-def cpu_baseline(runs=5, sample_tokens=8192):
+def cpu_baseline(runs=3, sample_tokens=None):
     """The reference path on the host's cores in torch CPU ops (the oracle's torch restatement: reference()'s fp32
     product of dequantized e4m3 operands, the casts with IEEE scales, the eager SwiGLU expressions): config 1 at full
-    size, and the d12 block step of this benchmark (every GEMM in FP8, as on the GPU) on `sample_tokens` of the 32768
-    tokens; median of `runs` timed runs after a warm-up, with all the threads this process is granted."""
+    size, and the d12 block step of this benchmark (every GEMM in FP8, as on the GPU) at the GPU's size, all 32768
+    tokens (`sample_tokens` to run fewer); median of `runs` timed runs after a warm-up, with all the threads this
+    process is granted."""
     import torch
     from oracle import oracle as O
     threads = cpu_threads()
@@ -404,7 +419,7 @@ def cpu_baseline(runs=5, sample_tokens=8192):
         return O.torch_mm(xq, sx, wq, sw)
     c1 = median_s(config1, max(runs, 7))
 
-    Ms = sample_tokens
+    Ms = sample_tokens or M_TOK
     g = torch.Generator().manual_seed(0)
 
     def bf(*shape, std=1.0):
@@ -441,9 +456,10 @@ def cpu_baseline(runs=5, sample_tokens=8192):
     fl = flops(gemm_shapes(M=Ms))
     return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"d12 block fwd+bwd FP8 linear path (the step of this benchmark, every GEMM FP8) on {Ms} of the "
-                      f"{M_TOK} tokens in torch CPU ops (reference()'s fp32 product of dequantized e4m3 operands, "
-                      f"IEEE-scaled casts, eager SwiGLU); median of {runs} runs after a warm-up",
-            "ms_per_sample_step": round(sec * 1e3, 1), "gemm_tflop_per_sample_step": round(fl / 1e12, 4),
+                      f"{M_TOK} tokens (the GPU's configuration{'' if Ms == M_TOK else ', sampled'}) in torch CPU ops "
+                      f"(reference()'s fp32 product of dequantized e4m3 operands, IEEE-scaled casts, eager SwiGLU); "
+                      f"median of {runs} runs after a warm-up",
+            "tokens": Ms, "ms_per_step": round(sec * 1e3, 1), "gemm_tflop_per_step": round(fl / 1e12, 4),
             "config1_ms": round(c1 * 1e3, 2),
             "config1_workload": "X [4096 x 768] . W [768 x 768] seed 0: two casts + fp32 product -> bf16 (4.83 GFLOP)",
             "config1_gflops": round(2.0 * 4096 * 768 * 768 / c1 / 1e9, 1),

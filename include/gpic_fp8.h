@@ -134,8 +134,12 @@ int gpic_fp8_swiglu_bwd(const uint16_t *z, const uint16_t *da, int64_t M, int64_
 /*
  * gpic_fp8_swiglu_tcast plus the transposed bytes qt [H, ldt] (H % 16 == 0, ldt % 16 == 0, ldt >= M; columns
  * M..ldt-1 zero): the K-major operand of w3's FP8 wgrad. Same bytes and scale as gpic_fp8_swiglu_tcast.
- *   a  [M, H] bf16, contiguous, or NULL: when given, the SwiGLU product is written there by the amax pass and the
- *      cast reads it instead of recomputing it (the same bytes; faster: the product is computed once)
+ *   a  [M, H] bf16, contiguous, or NULL. With qt given, or in the two-pass casts: the SwiGLU product is written there
+ *      by the amax pass and the cast reads it instead of recomputing it (the same bytes; faster: the product is
+ *      computed once), so `a` holds the whole product afterwards. In the q-only single pass (qt == NULL, sq == H,
+ *      below) `a` is scratch: the pass writes only the rows of the product that do not fit on chip (none when the
+ *      whole product fits), and the contents of `a` afterwards are unspecified. A caller that needs the bf16 product
+ *      itself must pass qt, or disable the single pass (gpic_fp8_set_single_pass).
  *   qt may be NULL (then ldt == 0, and H % 8 == 0 suffices): q only. With sq == H the single pass: one launch that
  *      holds up to 96 MiB of the product on chip (on 256 CUs) and, given `a`, streams the rest through a -- up to 8x
  *      that (d12's [32768, 8192]: 190 us against 246 for the amax pass writing a and a flat cast of it, flushed

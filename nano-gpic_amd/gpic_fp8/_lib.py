@@ -108,10 +108,15 @@ def _new_workspace(index, nbytes):
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
     out = {}
+    caller = torch.cuda.current_stream(dev)
 
     def alloc():
+        # on the caller's stream: the caching allocator hands out a block only once the work queued on its stream
+        # before its last free has run, so the block is free to be zeroed and used on that stream at once (on the
+        # helper thread's default stream instead, kernels still running there could write over the fresh words)
         try:
-            out["ws"] = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+            with torch.cuda.stream(caller):
+                out["ws"] = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
         except BaseException as e:   # re-raised on the caller's thread
             out["err"] = e
 

@@ -149,10 +149,22 @@ def _(xs):
     return out
 
 
+class WeightCast(tuple):
+    """A weight's (q, qt, dequant) from weight_casts, which also records the weight it was cast from (its storage
+    pointer and version counter, which every in-place update such as an optimizer step advances), so that a cast
+    kept past an update of the weight is refused instead of feeding the GEMMs stale bytes."""
+    src = None
+
+
 def weight_casts(*ws):
-    """The (q, qt, dequant) triples of tcast_t_group(ws), one per weight, in order."""
+    """The (q, qt, dequant) triples of tcast_t_group(ws), one per weight, in order (WeightCast tuples)."""
     o = tcast_t_group(list(ws))
-    return [tuple(o[3 * i:3 * i + 3]) for i in range(len(ws))]
+    out = []
+    for i, w in enumerate(ws):
+        c = WeightCast(o[3 * i:3 * i + 3])
+        c.src = (w.data_ptr(), w._version)
+        out.append(c)
+    return out
 
 
 def _swiglu_prep(z):
@@ -567,13 +579,19 @@ def fp8_swiglu_w3(z, w3):
 def _check_cast(name, w, c):
     if c is not None and (len(c) != 3 or c[0].shape != w.shape or c[1].shape[0] != w.shape[1]):
         raise ValueError(f"{name}: a (q, qt, dequant) triple of tcast_t(weight) [{tuple(w.shape)}] expected")
+    src = getattr(c, "src", None)
+    if src is not None and src != (w.data_ptr(), w._version):
+        raise ValueError(f"{name} was cast from another weight, or before the weight's last update: cast it again "
+                         "(weight_casts) after every in-place change of the weight")
     return c
 
 
 def fp8_linear_f8(x, w, b=None, wcast=None):
     """Phase 3 fp8_linear: FP8 dgrad and wgrad as well. wcast: w's (q, qt, dequant) from weight_casts (the same bytes
     tcast_t(w) would give, cast beforehand with the block's other weights), else w is cast here. A wcast must come
-    from w's current values: cast again after every update of w (an optimizer step); only its shapes are checked."""
+    from w's current values: cast again after every update of w (an optimizer step). A WeightCast (weight_casts)
+    that was cast from another tensor or before w's last in-place update is refused; of a plain tuple only the
+    shapes are checked."""
     with torch.autocast("cuda", enabled=False):
         return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b, _check_cast("wcast", w, wcast))
 

@@ -113,6 +113,29 @@ def test_weight_cast_shape_checked(dev):
         G.fp8_linear_f8(x, w, wcast=c)
 
 
+def test_stale_weight_cast_refused(dev):
+    """A WeightCast taken before an in-place update of its weight (an optimizer step), or taken from another tensor of
+    the same shape, is refused; cast again, it is accepted and gives tcast_t's result; a plain (q, qt, dequant) tuple is
+    checked by shape only."""
+    g = torch.Generator(device=dev).manual_seed(3)
+    w = (torch.randn(64, 32, generator=g, device=dev) / 32 ** 0.5).to(torch.bfloat16)
+    x = torch.randn(16, 32, generator=g, device=dev).to(torch.bfloat16)
+    (c,) = G.weight_casts(w)
+    y0 = G.fp8_linear_f8(x, w, wcast=c)
+    with torch.no_grad():
+        w.mul_(2.0)                                   # the update
+    with pytest.raises(ValueError, match="last update"):
+        G.fp8_linear_f8(x, w, wcast=c)
+    with pytest.raises(ValueError, match="another weight"):
+        G.fp8_linear_f8(x, w.clone(), wcast=G.weight_casts(w)[0])
+    (c2,) = G.weight_casts(w)
+    y1 = G.fp8_linear_f8(x, w, wcast=c2)
+    assert torch.equal(y1.view(torch.int16), G.fp8_linear_f8(x, w).view(torch.int16))
+    # w x 2: the same bytes with twice the scale, so exactly twice the output (power-of-two scaling rounds exactly)
+    assert torch.equal(y1.view(torch.int16), (y0.float() * 2).to(torch.bfloat16).view(torch.int16))
+    assert torch.equal(G.fp8_linear_f8(x, w, wcast=tuple(c)).view(torch.int16), y0.view(torch.int16))
+
+
 @pytest.mark.parametrize("wait", [-1, 0])
 def test_group_replayed(dev, knob, wait):
     """The grouped cast captured in a graph on a stream that has already cast, replayed 4 times with new values

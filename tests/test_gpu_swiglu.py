@@ -410,3 +410,31 @@ def test_bwd_matches_eager_torch_within_one_ulp(dev):
     ref = torch.cat([dz1, dz2], -1)
     diff = (dz.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
     assert diff.max().item() <= 1 and (diff == 0).float().mean().item() > 0.99
+
+
+def test_q_only_product_buffer_contract(dev):
+    """The contract of `a` in gpic_fp8_swiglu_tcast_t with qt = NULL and sq == H (include/gpic_fp8.h): the single
+    pass uses `a` as scratch for the rows that do not fit on chip, so a product that fits leaves `a` as it was; with
+    the single pass disabled the amax pass writes the whole product there. The bytes and scale are the same and equal
+    the oracle's either way."""
+    from gpic_fp8 import _lib as L
+    M, H = 512, 256
+    z = rand_bf16((M, 2 * H), 3.0, seed=77).to(dev)
+    oq, od, _ = O.swiglu_tcast(bits(z.cpu()))
+    try:
+        for single in (True, False):
+            L.set_single_pass(single, -1)
+            a = torch.full((M, H), 7.0, dtype=torch.bfloat16, device=dev)
+            q = torch.empty(M, H, dtype=torch.uint8, device=dev)
+            s = torch.empty(1, dtype=torch.float32, device=dev)
+            rc = L.lib().gpic_fp8_swiglu_tcast_t(z.data_ptr(), M, H, z.stride(0), a.data_ptr(), q.data_ptr(), H, None,
+                                                 0, s.data_ptr(), L.cast_workspace(dev).data_ptr(), L.stream_ptr(dev))
+            assert rc == 0
+            torch.cuda.synchronize()
+            assert s.item() == od and np.array_equal(qb(q), oq)
+            if single:
+                assert bool((a == 7.0).all()), "the single pass wrote a product that fits on chip"
+            else:
+                assert np.array_equal(bits(a), O.swiglu_product(bits(z.cpu())))
+    finally:
+        L.set_single_pass(True, -1)
