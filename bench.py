@@ -328,6 +328,56 @@ def mfma_ceiling(G, dev):
     return out
 
 
+def hbm_floor(dev, read_bytes, write_bytes, runs=15):
+    """How long one launch takes just to read `read_bytes` from HBM, just to write `write_bytes`, and to do both with a
+    cast's traffic pattern (each workgroup writing as soon as its own reads are in), with L2 / MALL flushed before each
+    launch as for the cast (tests/hip/hbm_floor.hip; the best of its launch shapes, median of `runs` event-timed
+    launches). A single-pass cast moves the same bytes and must also agree on the maximum across the chip before its
+    first write, so the read-and-write launch is a floor under it. None if the measurement library has not been
+    built."""
+    import ctypes
+    import torch
+    path = os.path.join(ROOT, "tests", "hip", "libhbm_floor.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.gpic_probe_hbm.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    lib.gpic_probe_hbm_groups.argtypes = [ctypes.c_int, ctypes.c_uint64]
+    lib.gpic_probe_hbm_rw.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    src = torch.ones(read_bytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty(write_bytes // 4, dtype=torch.float32, device=dev)
+    out = torch.empty(max(lib.gpic_probe_hbm_groups(2, read_bytes), 1), dtype=torch.int32, device=dev)
+    flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    shapes = {0: "1024 threads x 16 words", 1: "512 x 16", 2: "256 x 8", 3: "512 x 32"}
+    best = {}
+    calls = {"read": lambda cfg: lib.gpic_probe_hbm(1, cfg, src.data_ptr(), read_bytes, out.data_ptr(), st),
+             "write": lambda cfg: lib.gpic_probe_hbm(0, cfg, dst.data_ptr(), write_bytes, None, st),
+             "read_write": lambda cfg: lib.gpic_probe_hbm_rw(cfg, src.data_ptr(), read_bytes, dst.data_ptr(), st)}
+    for key, call in calls.items():
+        for cfg in shapes:
+            times = []
+            for _ in range(runs):
+                flush.fill_(1)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                if call(cfg) != 0:
+                    return None
+                e1.record()
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3)
+            us = sorted(times)[len(times) // 2]
+            if key not in best or us < best[key][0]:
+                best[key] = (us, shapes[cfg])
+    del flush, src, dst
+    r, w, rw = best["read"], best["write"], best["read_write"]
+    return {"read_us": round(r[0], 2), "read_shape": r[1], "read_GBs": round(read_bytes / r[0] / 1e3, 1),
+            "write_us": round(w[0], 2), "write_shape": w[1], "write_GBs": round(write_bytes / w[0] / 1e3, 1),
+            "read_write_us": round(rw[0], 2), "read_write_shape": rw[1],
+            "read_write_GBs": round((read_bytes + write_bytes) / rw[0] / 1e3, 1)}
+
+
 def gemm_source_sha():
     """Hash of gemm.hip's code: each line with its // comment and trailing blanks removed, blank lines dropped, so
     that comment edits do not make the measured traffic look stale."""
@@ -548,6 +598,8 @@ def main():
         cold.append(e0.elapsed_time(e1))
     cast_cold_ms = sorted(cold)[len(cold) // 2]
     del flush
+    # the floor under any single-pass cast of config 2: one launch reading its 64 MiB, one writing its 32 MiB
+    floor = hbm_floor(dev, xc.numel() * 2, xc.numel())
 
     # ---- the other casts: an fp32 weight-shaped tensor (DDP keeps fp32 weights) and the d12 SwiGLU casts of the step,
     # as device time (short kernels: Python's issue time would show in a back-to-back loop)
@@ -681,7 +733,11 @@ def main():
                  "us": round(cast_cold_ms * 1e3, 2), "achieved_GBs": round(cast_bytes / cast_cold_ms / 1e6, 1),
                  "peak_GBs": PEAK_HBM_GBS, "frac": round(cast_bytes / cast_cold_ms / 1e6 / PEAK_HBM_GBS, 4),
                  "algorithmic_bytes": cast_bytes, "us_warm": round(cast_ms * 1e3, 2),
-                 "frac_warm": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4)},
+                 "frac_warm": round(cast_bytes / cast_ms / 1e6 / PEAK_HBM_GBS, 4),
+                 # launches that only read the 64 MiB, only write the 32 MiB, or do both without the cast's
+                 # cross-chip maximum, flushed the same way: the last is a floor under any single pass
+                 "hbm_floor": floor,
+                 "frac_of_floor": round(floor["read_write_us"] / (cast_cold_ms * 1e3), 4) if floor else None},
         "cast_fp32_weight": {"workload": "fp32 [3072 x 1024] -> e4m3 + amax + scale (a DDP weight)",
                              "us": round(w32_ms * 1e3, 2) if w32_ms else None, "algorithmic_bytes": w32_bytes,
                              "achieved_GBs": round(w32_bytes / w32_ms / 1e6, 1) if w32_ms else None},

@@ -50,12 +50,13 @@ def build(verbose=False):
     return LIB
 
 
-TEST_LIBS = {"bf16_selfcheck.hip": "libbf16_selfcheck.so", "mfma_ceiling.hip": "libmfma_ceiling.so"}
+TEST_LIBS = {"bf16_selfcheck.hip": "libbf16_selfcheck.so", "mfma_ceiling.hip": "libmfma_ceiling.so",
+             "hbm_floor.hip": "libhbm_floor.so"}
 
 
 def build_test_libs(verbose=False):
-    """The test-side libraries under tests/hip (the bf16 rounding self-check, the MFMA ceiling measurement), with the
-    same compiler flags as the product."""
+    """The test-side libraries under tests/hip (the bf16 rounding self-check, the MFMA ceiling and HBM floor
+    measurements), with the same compiler flags as the product."""
     root = os.path.dirname(os.path.dirname(HERE))
     outs = []
     for src_name, lib_name in TEST_LIBS.items():

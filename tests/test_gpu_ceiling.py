@@ -47,3 +47,36 @@ def test_mfma_ceiling(shape, data):
 
     with pytest.raises(AssertionError):      # a form the probe does not know is refused
         probe(24, False, None, 2)
+
+
+@pytest.mark.gpu
+def test_hbm_floor_probe(dev):
+    """tests/hip/hbm_floor.hip: one read launch and one write launch over 64 / 32 MiB, in every launch shape; bench.py
+    reports the config-2 cast against their times. The read returns each workgroup's maximum word (all ones here: the
+    bits of 1.0f), so the probe is seen to read what it claims."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "hip", "libhbm_floor.so")
+    lib = ctypes.CDLL(path)
+    lib.gpic_probe_hbm.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    lib.gpic_probe_hbm_groups.argtypes = [ctypes.c_int, ctypes.c_uint64]
+    nb = 64 * 1024 * 1024
+    src = torch.ones(nb // 4, dtype=torch.float32, device=dev)
+    dst = torch.zeros(nb // 8, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    for cfg in range(4):
+        g = lib.gpic_probe_hbm_groups(cfg, nb)
+        out = torch.zeros(g, dtype=torch.int32, device=dev)
+        assert lib.gpic_probe_hbm(1, cfg, src.data_ptr(), nb, out.data_ptr(), st) == 0
+        assert lib.gpic_probe_hbm(0, cfg, dst.data_ptr(), nb // 2, None, st) == 0
+        torch.cuda.synchronize()
+        assert bool((out == 0x3F800000).all()), cfg
+        assert bool((dst.view(torch.int32) == 0x38383838).all()), cfg
+    lib.gpic_probe_hbm_rw.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    for cfg in range(4):   # the read-and-write launch: 8 bytes per 16-byte word (here 1.0f x 4: zeros)
+        dst.fill_(7.0)
+        assert lib.gpic_probe_hbm_rw(cfg, src.data_ptr(), nb, dst.data_ptr(), st) == 0
+        torch.cuda.synchronize()
+        assert bool((dst == 0).all()), cfg
+    assert lib.gpic_probe_hbm(1, 9, src.data_ptr(), nb, out.data_ptr(), st) == -1
+    assert lib.gpic_probe_hbm(1, 0, src.data_ptr(), 17, out.data_ptr(), st) == -1
