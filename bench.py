@@ -254,6 +254,34 @@ def norm_sites(G, dev, B=128, N=256, eps=1e-6):
     return out
 
 
+def heads_site(G, dev, B=128, N=256):
+    """The attention output feeding proj in a d12 block over one GPU's 32768 tokens (16 heads of 64), as the flash
+    backend of scaled_dot_product_attention writes it ([B, H, N, D] in memory): fused (tcast_heads reads o in its own
+    layout and writes proj's e4m3 input) against unfused (the head-merging copy o.transpose(1, 2).reshape(B, N, C),
+    then tcast), device time, with the bytes each moves (fused: o read, e4m3 written; unfused: o read and written by
+    the copy, read again and cast)."""
+    import torch
+    H = 16
+    D = C // H
+    g = torch.Generator(device=dev).manual_seed(13)
+    o = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
+    t = {"fused": time_device(lambda: G.tcast_heads(o), 20, 3),
+         "unfused": time_device(lambda: G.tcast(o.transpose(1, 2).reshape(B, N, C)), 20, 3)}
+    n = B * N * C
+    by = {"fused": n * 3, "unfused": n * 7}
+    out = {"workload": f"d12 attention output [{B} x {H} x {N} x {D}] bf16 ([B, H, N, D] in memory) -> proj's e4m3 "
+                       "input [32768 x 1024] + scale: tcast_heads (fused) against the head-merging copy then tcast "
+                       "(device time)"}
+    for k, ms in t.items():
+        out[k + "_us"] = round(ms * 1e3, 2) if ms else None
+        out[k + "_bytes"] = by[k]
+        out[k + "_GBs"] = round(by[k] / ms / 1e6, 1) if ms else None
+    if t["fused"] and t["unfused"]:
+        out["speedup"] = round(t["unfused"] / t["fused"], 3)
+        out["fused_frac_hbm"] = round(by["fused"] / t["fused"] / 1e6 / PEAK_HBM_GBS, 4)
+    return out
+
+
 def norm_block(G, dev, B=128, N=256, eps=1e-6, steps=20):
     """The d12 block's two norm sites with the FP8 linears they feed, fwd + bwd over 32768 tokens (site 1 -> qkv_x,
     site 2 -> the SwiGLU MLP; every GEMM FP8): fused (the norm kernel writes h's e4m3 bytes, h never exists in bf16:
@@ -628,6 +656,8 @@ def main():
     # writing bf16 h and tcast(h) reading it back (unfused), device time
     norm = norm_sites(G, dev)
     nblock = norm_block(G, dev)
+    # ---- the attention output's producer: proj's e4m3 input read from o [B, H, N, D] in its own layout
+    heads = heads_site(G, dev)
 
     # ---- config 5: the d18 block (C = 1792, H = 7168) with 1% outlier activation channels, fwd + bwd
     C18, H18 = 1792, 7168
@@ -753,6 +783,7 @@ def main():
                    "bwd_frac_min": round(swb_min / swb_ms / 1e6 / PEAK_HBM_GBS, 4) if swb_ms else None},
         "norm_sites": norm,
         "norm_block": nblock,
+        "heads_site": heads,
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
                       "tflops": round(fl18 / ms18 / 1e9, 1)},

@@ -106,6 +106,24 @@ int gpic_fp8_tcast_t_group(int count, const void *const *x, int dtype, const int
                            void *stream);
 
 /*
+ * The attention output's cast with its head merge folded in: the cast of proj's input, read from the attention's own
+ * output. Replaces, at the attention output feeding proj (baselines/PixelGen/src/models/transformer/JiT_T2I.py:183-185:
+ * x = attention(q, k, v); x.transpose(1, 2).reshape(B, N, C); self.proj(x)), the head-merging copy plus the FP8
+ * linear's tcast of its result (fp8_native.py:114-122, 187) with one producer of proj's e4m3 input (an extension:
+ * the reference keeps them apart, fp8_native.py:3-6):
+ *   o        [B, H, N, D] bf16, element (b, h, n, d) at o + b sb + h sh + n sn + d (strides in elements, multiples of
+ *            8, >= 0; D % 16 == 0; 16-byte aligned) -- e.g. scaled_dot_product_attention's output in either of the
+ *            layouts its backends write ([B, H, N, D] or [B, N, H, D] in memory)
+ *   q        [B N, H D] e4m3, row b N + n, column h D + d: the bytes gpic_fp8_tcast gives for the contiguous
+ *            o.transpose(1, 2).reshape(B N, H D), with the same amax, scale and dequant
+ * The source's word indices (16 bytes) and the output's words must stay below 2^31 (else GPIC_ESHAPE). When the
+ * strides already describe [B, N, H, D] contiguous, the call is gpic_fp8_tcast of o. Same single-pass / two-pass
+ * choice, workspace and empty-tensor rule as gpic_fp8_tcast.
+ */
+int gpic_fp8_tcast_heads(const uint16_t *o, int64_t B, int64_t H, int64_t N, int64_t D, int64_t sb, int64_t sh,
+                         int64_t sn, uint8_t *q, float *dequant, void *ws, void *stream);
+
+/*
  * SwiGLU product cast. Replaces gpic::fp8_swiglu_tcast (fp8_native.py:130-144; _swiglu_tile :53-58,
  * _swiglu_amax_kernel :61-66, _swiglu_cast_kernel :69-78).
  *   z        [M, 2H] bf16, row stride sz (H % 8 == 0, sz % 8 == 0)
@@ -169,7 +187,7 @@ int gpic_fp8_swiglu_bwd_t(const uint16_t *z, const uint16_t *da, int64_t M, int6
  *   rstd = 1 / sqrt(sum(x_new^2) / C + eps) -> rstd [rows];  n = bf16(w * (x_new * rstd))
  *   h = bf16(fma(n, 1 + scale, shift)) -> h (when h != NULL), and its tensorwise e4m3 bytes -> hq, dequant (the
  *   tcast rule: amax over the non-NaN values, IEEE scales, saturating round-to-nearest-even)
- *   x, a, xn, h: [rows, C] bf16 (C % 256 == 0, 16-byte aligned); hq [rows, C] e4m3; w [C] fp32 (16-byte aligned)
+ *   x, a, xn, h: [rows, C] bf16 (C % 4 == 0, 16-byte aligned); hq [rows, C] e4m3; w [C] fp32 (16-byte aligned)
  *   gate, shift, scale: [B, C] bf16 rows with strides sg, ssh, ssc (multiples of 4, >= C; 8-byte aligned); row r of
  *   x uses row r / ntok of them (rows % ntok == 0)
  * dequant == NULL (then h != NULL, hq unused): the norm alone, as the reference's op (one pass writing h).
@@ -192,7 +210,7 @@ int gpic_fp8_res_mod_rmsnorm(const uint16_t *x, const uint16_t *a, const uint16_
  *   d_w = sum dn t (over all rows)  [C] fp32
  *   dh, dxn, xs (x_new at site 2, x at site 1), a, dx, da: [rows, C] bf16 (16-byte aligned); dxn may be NULL at site 2
  *   and must be NULL at site 1 (as gate, d_gate); gate, scale: [B, C] bf16 rows (strides sg, ssc); w [C] fp32;
- *   rstd [rows] fp32 (the forward's); C % 256 == 0, C <= 2048, rows % ntok == 0.
+ *   rstd [rows] fp32 (the forward's); C % 4 == 0, C <= 2048, rows % ntok == 0.
  *   ws: gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes(rows, ntok, C) bytes (the partial column sums).
  * Deterministic: every sum is taken in a fixed order.
  */

@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "gpic_device.h"
 #include "gpic_launch.h"
@@ -27,6 +28,45 @@
 namespace gpic {
 
 constexpr int kUnroll = 4;    // 16-element units per thread in flight in the streaming passes
+
+// ------------------------------------------------------------------------------------------- source maps
+//
+// The flat casts read output word i (8 bf16 or 4 fp32 elements) from source word map(i). FlatMap: the source is the
+// output's shape, contiguous. HeadMap: the attention output o [B, H, N, D] with any strides, cast into the rows of
+// [B N, H D] (o.transpose(1, 2).reshape(B N, H D)) -- the head-merging layout change folded into the cast.
+struct FlatMap {
+  __device__ __forceinline__ int64_t operator()(int64_t i) const { return i; }
+  __device__ __forceinline__ uint32_t operator()(uint32_t i) const { return i; }
+};
+
+// Division by a divisor d fixed for a launch, for dividends below 2^31: q = (n m) >> (31 + s), s = ceil(log2 d),
+// m = ceil(2^(31 + s) / d) < 2^32. Exact: with m d = 2^(31 + s) + e, 0 <= e < d <= 2^s, the error n e / (d 2^(31 + s))
+// stays below 1 / d for n < 2^31, so it never carries past the next multiple of d.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+static inline FastDiv fast_div(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) s++;
+  return FastDiv{d, (uint32_t)(((1ull << (31 + s)) + d - 1) / d), s};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+  return (uint32_t)(((uint64_t)n * f.m) >> (31 + f.s));
+}
+
+// Output word i = ((b N + n) H + h) D/8 + dw lies at source word b sb + h sh + n sn + dw (strides in 16-byte words;
+// the host checks every source word index and the output's word count below 2^31).
+struct HeadMap {
+  FastDiv dw8, heads, tokens;   // D / 8, H, N
+  uint32_t sb, sh, sn;
+  __device__ __forceinline__ uint32_t operator()(uint32_t i) const {
+    const uint32_t g = fdiv(i, dw8), dw = i - g * dw8.d;   // head row g = (b N + n) H + h
+    const uint32_t r = fdiv(g, heads), h = g - r * heads.d;
+    const uint32_t b = fdiv(r, tokens), n = r - b * tokens.d;
+    return b * sb + h * sh + n * sn + dw;
+  }
+  __device__ __forceinline__ int64_t operator()(int64_t i) const { return (*this)((uint32_t)i); }
+};
 
 // ------------------------------------------------------------------------------------------- pass 1: amax
 
@@ -52,9 +92,11 @@ __device__ __forceinline__ uint32_t word_max(uint32_t m, u32x4 w) {
 // Writes max |x| over the non-NaN elements of this workgroup's share to partial[blockIdx.x].
 // kKeep: ordinary loads, which leave x in the MALL for the cast pass (used when x fits it, kMallBytes); otherwise
 // non-temporal loads (measured: for x of 192 MiB and more, ordinary loads slow both passes).
-template <typename T, bool kKeep>
+// Map: the source of each 16-byte word (a 16-element unit's words are consecutive in the source); the n % 16 tail is
+// read flat (HeadMap sources have none).
+template <typename T, bool kKeep, class Map = FlatMap>
 __global__ __launch_bounds__(kCastThreads) void amax_kernel(const T *__restrict__ x, int64_t n,
-                                                             uint32_t *__restrict__ partial) {
+                                                             uint32_t *__restrict__ partial, const Map map = Map()) {
   constexpr int kWords = sizeof(T);   // 16-byte words per 16-element unit: 2 (bf16) or 4 (fp32)
   const int64_t units = n / 16;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -67,7 +109,7 @@ __global__ __launch_bounds__(kCastThreads) void amax_kernel(const T *__restrict_
     for (int k = 0; k < kUnroll; k++)
 #pragma unroll
       for (int i = 0; i < kWords; i++) {
-        const u32x4 *p = xv + (u + k * stride) * kWords + i;
+        const u32x4 *p = xv + map((u + k * stride) * kWords) + i;
         w[k][i] = kKeep ? *p : __builtin_nontemporal_load(p);
       }
 #pragma unroll
@@ -77,7 +119,7 @@ __global__ __launch_bounds__(kCastThreads) void amax_kernel(const T *__restrict_
   }
   for (; u < units; u += stride)
 #pragma unroll
-    for (int i = 0; i < kWords; i++) m = word_max<T>(m, __builtin_nontemporal_load(xv + u * kWords + i));
+    for (int i = 0; i < kWords; i++) m = word_max<T>(m, __builtin_nontemporal_load(xv + map(u * kWords) + i));
   bool nan;
   if constexpr (sizeof(T) == 2) {
     m = max(m & 0xffffu, m >> 16);
@@ -90,8 +132,9 @@ __global__ __launch_bounds__(kCastThreads) void amax_kernel(const T *__restrict_
     m = 0;
     for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < units; v += stride)
       for (int i = 0; i < 16; i++) {
-        const uint32_t a = sizeof(T) == 2 ? absbits_bf16(reinterpret_cast<const uint16_t *>(x)[v * 16 + i])
-                                          : absbits_f32(reinterpret_cast<const float *>(x)[v * 16 + i]);
+        const u32x4 *p = xv + map(v * kWords);
+        const uint32_t a = sizeof(T) == 2 ? absbits_bf16(reinterpret_cast<const uint16_t *>(p)[i])
+                                          : absbits_f32(reinterpret_cast<const float *>(p)[i]);
         if (a <= 0x7f800000u) m = max(m, a);
       }
   }
@@ -124,10 +167,11 @@ __device__ __forceinline__ u32x4 cast_unit(const u32x4 (&w)[sizeof(T)], float sc
   }
 }
 
-template <typename T>
+template <typename T, class Map = FlatMap>
 __global__ __launch_bounds__(kCastThreads) void cast_kernel(const T *__restrict__ x, int64_t n,
                                                              const uint32_t *__restrict__ partial, int nparts,
-                                                             uint8_t *__restrict__ q, float *__restrict__ dequant) {
+                                                             uint8_t *__restrict__ q, float *__restrict__ dequant,
+                                                             const Map map = Map()) {
   constexpr int kWords = sizeof(T);
   float scale, deq;
   scales_from_amax(fold_partials(partial, nparts), scale, deq);
@@ -142,14 +186,14 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(const T *__restrict_
 #pragma unroll
     for (int k = 0; k < kUnroll; k++)
 #pragma unroll
-      for (int i = 0; i < kWords; i++) w[k][i] = __builtin_nontemporal_load(xv + (u + k * stride) * kWords + i);
+      for (int i = 0; i < kWords; i++) w[k][i] = __builtin_nontemporal_load(xv + map((u + k * stride) * kWords) + i);
 #pragma unroll
     for (int k = 0; k < kUnroll; k++) __builtin_nontemporal_store(cast_unit<T>(w[k], scale), qv + u + k * stride);
   }
   for (; u < units; u += stride) {
     u32x4 w[kWords];
 #pragma unroll
-    for (int i = 0; i < kWords; i++) w[i] = __builtin_nontemporal_load(xv + u * kWords + i);
+    for (int i = 0; i < kWords; i++) w[i] = __builtin_nontemporal_load(xv + map(u * kWords) + i);
     __builtin_nontemporal_store(cast_unit<T>(w, scale), qv + u);
   }
   if (blockIdx.x == 0 && threadIdx.x < (n & 15)) {
@@ -649,19 +693,20 @@ static inline int grid_for(int64_t units, int cap) {
 
 constexpr int64_t kMallBytes = 128ll << 20;   // x at most this large stays in the 256 MiB MALL between the passes
 
-template <typename T>
-static void launch_amax(const T *x, int64_t n, int grid, uint32_t *partial, hipStream_t st) {
-  if (n * (int64_t)sizeof(T) <= kMallBytes) amax_kernel<T, true><<<grid, kCastThreads, 0, st>>>(x, n, partial);
-  else amax_kernel<T, false><<<grid, kCastThreads, 0, st>>>(x, n, partial);
+template <typename T, class Map = FlatMap>
+static void launch_amax(const T *x, int64_t n, int grid, uint32_t *partial, hipStream_t st, const Map map = Map()) {
+  if (n * (int64_t)sizeof(T) <= kMallBytes) amax_kernel<T, true, Map><<<grid, kCastThreads, 0, st>>>(x, n, partial, map);
+  else amax_kernel<T, false, Map><<<grid, kCastThreads, 0, st>>>(x, n, partial, map);
 }
 
-template <typename T>
-static int launch_tcast(const T *x, int64_t n, uint8_t *q, float *dequant, uint32_t *partial, hipStream_t st) {
+template <typename T, class Map = FlatMap>
+static int launch_tcast(const T *x, int64_t n, uint8_t *q, float *dequant, uint32_t *partial, hipStream_t st,
+                        const Map map = Map()) {
   const int64_t units = n / 16;
   const int ga = grid_for((units + kUnroll - 1) / kUnroll, kAmaxBlocks);
-  launch_amax(x, n, ga, partial, st);
+  launch_amax(x, n, ga, partial, st, map);
   const int gc = grid_for((units + kUnroll - 1) / kUnroll, kMaxCastBlocks);
-  cast_kernel<T><<<gc, kCastThreads, 0, st>>>(x, n, partial, ga, q, dequant);
+  cast_kernel<T, Map><<<gc, kCastThreads, 0, st>>>(x, n, partial, ga, q, dequant, map);
   return (int)hipGetLastError();
 }
 
@@ -922,12 +967,13 @@ __device__ __forceinline__ uint32_t words_amax(const u32x4 (&w)[W]) {
 // workgroup b holds words [b P, (b + 1) P), P = 256 wpt, thread t words b P + 256 j + t, j < wpt <= kOnceWords<T>.
 // Hybrid (sgroups > 0, x larger than the grid holds): the 256-word groups past the held words, G P + 256 s + t, are
 // streamed by workgroup s % G twice -- for the maximum, then (last first, for MALL hits) for the cast -- so only
-// what does not fit is read twice.
-template <typename T>
+// what does not fit is read twice. Map: the source word of each output word (the tail is read flat: HeadMap sources
+// have none).
+template <typename T, class Map = FlatMap>
 __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__ x, int64_t n, int wpt,
                                                            int64_t sgroups, uint8_t *__restrict__ q,
                                                            float *__restrict__ dequant, void *ws,
-                                                           uint32_t wait_ticks) {
+                                                           uint32_t wait_ticks, const Map map = Map()) {
   const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   constexpr int kE = 16 / sizeof(T);   // elements per word
   const int64_t nw = n / kE;
@@ -946,7 +992,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
 #pragma unroll
       for (int k = 0; k < kStream; k++) {
         const int64_t sk = s + k * G, i = sword(sk);
-        S[k] = sk < sgroups && i < nw ? __builtin_nontemporal_load(xv + i) : u32x4{0u, 0u, 0u, 0u};
+        S[k] = sk < sgroups && i < nw ? __builtin_nontemporal_load(xv + map(i)) : u32x4{0u, 0u, 0u, 0u};
       }
       a = max(a, words_amax<T, kStream>(S));
     }
@@ -957,7 +1003,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
 #pragma unroll
   for (int j = 0; j < kW; j++) {
     const int64_t i = word(blockIdx.x, j);
-    w[j] = j < wpt && i < nw ? __builtin_nontemporal_load(xv + i) : u32x4{0u, 0u, 0u, 0u};
+    w[j] = j < wpt && i < nw ? __builtin_nontemporal_load(xv + map(i)) : u32x4{0u, 0u, 0u, 0u};
   }
   // every workgroup folds the tail elements into its partial, so a partial computed from x includes them as well
   auto tail_amax = [&]() {
@@ -978,7 +1024,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
     uint32_t a = tail_amax();
     for (int j = 0; j < wpt; j++) {
       const int64_t i = word(c, j);
-      if (i < nw) a = max(a, word_amax_exact<T>(__builtin_nontemporal_load(xv + i)));
+      if (i < nw) a = max(a, word_amax_exact<T>(__builtin_nontemporal_load(xv + map(i))));
     }
     if (sgroups > 0) a = max(a, stream_amax(c));
     return block_max_u32(a);
@@ -1009,7 +1055,7 @@ __global__ __launch_bounds__(256, 4) void cast_once_kernel(const T *__restrict__
 #pragma unroll
       for (int k = 0; k < kStream; k++) {
         const int64_t i = sword(blockIdx.x + (k0 - k) * G);
-        S[k] = k0 - k >= 0 && i < nw ? __builtin_nontemporal_load(xv + i) : u32x4{0u, 0u, 0u, 0u};
+        S[k] = k0 - k >= 0 && i < nw ? __builtin_nontemporal_load(xv + map(i)) : u32x4{0u, 0u, 0u, 0u};
       }
 #pragma unroll
       for (int k = 0; k < kStream; k++) {
@@ -1491,15 +1537,17 @@ __global__ __launch_bounds__(kSwThreads) void swiglu_bwd_once_kernel(const uint1
 // CU, each thread holding kWideR words in registers and kWideL in LDS -- 400 KiB per CU, 100 MiB over 256 CUs. Words
 // go in groups of 1024, one per thread, workgroup b taking groups j G + b (j < wpt held); a larger x is a hybrid as in
 // cast_once_kernel: the sgroups groups past wpt G, workgroup s % G taking group s, are read for the maximum and read
-// again, last first, for the cast. The n % 8 tail elements: folded into every workgroup's partial, cast by workgroup 0.
+// again, last first, for the cast. The n % 8 tail elements: folded into every workgroup's partial, cast by workgroup 0
+// (read flat). Map: the source word of each output word.
 constexpr int kWideR = 16;   // words a thread holds in registers (64 VGPRs)
 constexpr int kWideL = 9;    // words a thread holds in LDS (144 KiB per workgroup)
 constexpr int kWide = kWideR + kWideL;
 
+template <class Map = FlatMap>
 __global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *__restrict__ x, int64_t n, int wpt,
                                                                 uint32_t sgroups, uint8_t *__restrict__ q,
                                                                 float *__restrict__ dequant, void *ws,
-                                                                uint32_t wait_ticks) {
+                                                                uint32_t wait_ticks, const Map map = Map()) {
   const uint32_t ep = once_epoch(ws);   // (before the first loads: its latency passes behind them)
   __shared__ u32x4 held[kWideL * kSwThreads];
   const uint32_t nw = (uint32_t)(n / 8), t = threadIdx.x, G = gridDim.x;
@@ -1509,9 +1557,9 @@ __global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *_
   const u32x4 zero{0u, 0u, 0u, 0u};
   auto hword = [&](uint32_t b, int j) { return ((uint32_t)j * G + b) * kSwThreads + t; };
   auto sword = [&](uint32_t s) { return base_s + kSwThreads * s + t; };
-  // branch-free: a word past x reads word 0 and is zeroed
+  // branch-free: a word past x reads source word 0 and is zeroed
   auto ld = [&](bool ok, uint32_t i) {
-    const u32x4 v = __builtin_nontemporal_load(xv + (ok ? i : 0u));
+    const u32x4 v = __builtin_nontemporal_load(xv + (ok ? map(i) : 0u));
     return ok ? v : zero;
   };
   auto tail_amax = [&]() {
@@ -1548,11 +1596,11 @@ __global__ __launch_bounds__(kSwThreads) void cast_wide_kernel(const uint16_t *_
     uint32_t a = tail_amax();
     for (int j = 0; j < wpt; j++) {
       const uint32_t i = hword((uint32_t)cb, j);
-      if (i < nw) a = max(a, word_amax_exact<uint16_t>(__builtin_nontemporal_load(xv + i)));
+      if (i < nw) a = max(a, word_amax_exact<uint16_t>(__builtin_nontemporal_load(xv + map(i))));
     }
     for (uint32_t s = cb; s < sgroups; s += G) {
       const uint32_t i = sword(s);
-      if (i < nw) a = max(a, word_amax_exact<uint16_t>(__builtin_nontemporal_load(xv + i)));
+      if (i < nw) a = max(a, word_amax_exact<uint16_t>(__builtin_nontemporal_load(xv + map(i))));
     }
     return block_max_u32(a);
   });
@@ -1621,20 +1669,25 @@ uint32_t once_wait_ticks() { return (uint32_t)std::max(0, g_once_wait_us.load(st
 
 bool once_enabled() { return g_once_enabled.load(std::memory_order_relaxed) != 0; }
 
-static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw, g_cap_wide, g_cap_tg;
+static DeviceCache g_cap_flat_bf16, g_cap_flat_f32, g_cap_t, g_cap_sw, g_cap_bw, g_cap_wide, g_cap_tg, g_cap_heads,
+    g_cap_heads_wide;
 struct DeviceCacheInit {   // every slot starts at -1 (not yet computed)
   DeviceCacheInit() {
     for (int i = 0; i < kMaxDevices; i++)
-      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = g_cap_wide[i] = g_cap_tg[i] = -1;
+      g_cap_flat_bf16[i] = g_cap_flat_f32[i] = g_cap_t[i] = g_cap_sw[i] = g_cap_bw[i] = g_cap_wide[i] = g_cap_tg[i] =
+          g_cap_heads[i] = g_cap_heads_wide[i] = -1;
   }
 };
 static DeviceCacheInit g_device_cache_init;
 
 // The single-pass flat cast when x fits, as a hybrid up to kHybridFlat times that (false, nothing launched, above).
-template <typename T>
-static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant, void *ws, hipStream_t st) {
-  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T>),
-                                sizeof(T) == 2 ? g_cap_flat_bf16 : g_cap_flat_f32, 256);
+// Map: where each output word's source lies (FlatMap: x itself; HeadMap: bf16 attention heads).
+template <typename T, class Map = FlatMap>
+static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant, void *ws, hipStream_t st,
+                              const Map map = Map()) {
+  constexpr bool kFlat = std::is_same<Map, FlatMap>::value;
+  const int cap = once_capacity(reinterpret_cast<const void *>(&cast_once_kernel<T, Map>),
+                                !kFlat ? g_cap_heads : sizeof(T) == 2 ? g_cap_flat_bf16 : g_cap_flat_f32, 256);
   constexpr int kE = 16 / sizeof(T);
   const int64_t nw = n / kE;
   const int64_t held = (int64_t)kOnceWords<T> * 256 * cap;   // words the grid holds in registers
@@ -1643,7 +1696,8 @@ static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant,
                                      // kHybridFlat x its hold (flushed caches: 64 MiB 23.8 us against 24.8, 32 MiB
                                      // 18.3 against 16.4, 192 MiB 74 against 88 as this kernel's hybrid)
     if (4 * nw > 3 * held) {
-      const int capw = once_capacity(reinterpret_cast<const void *>(&cast_wide_kernel), g_cap_wide, kSwThreads);
+      const int capw = once_capacity(reinterpret_cast<const void *>(&cast_wide_kernel<Map>),
+                                     kFlat ? g_cap_wide : g_cap_heads_wide, kSwThreads);
       const int64_t heldw = (int64_t)kWide * kSwThreads * capw;
       if (capw <= 0 || nw > kHybridFlat * heldw) return false;
       int grid = capw, wpt = kWide;
@@ -1655,21 +1709,22 @@ static bool launch_tcast_once(const T *x, int64_t n, uint8_t *q, float *dequant,
         grid = (int)std::min<int64_t>(groups, capw);
         wpt = (int)((groups + grid - 1) / grid);
       }
-      cast_wide_kernel<<<grid, kSwThreads, 0, st>>>(reinterpret_cast<const uint16_t *>(x), n, wpt, (uint32_t)sgroups,
-                                                    q, dequant, ws, once_wait_ticks());
+      cast_wide_kernel<Map><<<grid, kSwThreads, 0, st>>>(reinterpret_cast<const uint16_t *>(x), n, wpt,
+                                                         (uint32_t)sgroups, q, dequant, ws, once_wait_ticks(), map);
       return true;
     }
   }
   if (nw > kHybridFlat * held) return false;
   if (nw > held) {   // hybrid: every workgroup holds its full share, the rest is streamed
     const int64_t sgroups = (nw - held + 255) / 256;
-    cast_once_kernel<T><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_wait_ticks());
+    cast_once_kernel<T, Map><<<cap, 256, 0, st>>>(x, n, kOnceWords<T>, sgroups, q, dequant, ws, once_wait_ticks(),
+                                                  map);
     return true;
   }
   const int64_t groups = std::max<int64_t>(1, (nw + 255) / 256);   // 256-word groups
   const int grid = (int)std::min<int64_t>(groups, cap);
   const int wpt = (int)((groups + grid - 1) / grid);
-  cast_once_kernel<T><<<grid, 256, 0, st>>>(x, n, wpt, 0, q, dequant, ws, once_wait_ticks());
+  cast_once_kernel<T, Map><<<grid, 256, 0, st>>>(x, n, wpt, 0, q, dequant, ws, once_wait_ticks(), map);
   return true;
 }
 
@@ -1836,6 +1891,33 @@ int gpic_fp8_tcast(const void *x, int dtype, int64_t n, uint8_t *q, float *dequa
   const float *xf = static_cast<const float *>(x);
   if (launch_tcast_once(xf, n, q, dequant, ws, st)) return (int)hipGetLastError();
   return launch_tcast(xf, n, q, dequant, partial, st);
+}
+
+int gpic_fp8_tcast_heads(const uint16_t *o, int64_t B, int64_t H, int64_t N, int64_t D, int64_t sb, int64_t sh,
+                         int64_t sn, uint8_t *q, float *dequant, void *ws, void *stream) {
+  status_scope();
+  if (B < 0 || H < 0 || N < 0 || D < 0 || sb < 0 || sh < 0 || sn < 0 || !dequant || !ws) return GPIC_EINVAL;
+  const int64_t big = 1ll << 31;   // every extent and stride below 2^31, so the products below stay exact
+  if (D % 16 != 0 || B >= big || H >= big || N >= big || D >= big || sb >= big || sh >= big || sn >= big)
+    return GPIC_ESHAPE;
+  if (sb % 8 != 0 || sh % 8 != 0 || sn % 8 != 0) return GPIC_EALIGN;
+  int64_t n = 0;
+  if (__builtin_mul_overflow(B, H, &n) || __builtin_mul_overflow(n, N, &n) || __builtin_mul_overflow(n, D, &n))
+    return GPIC_ESHAPE;
+  if (n == 0) return gpic_fp8_tcast(o, GPIC_DTYPE_BF16, 0, q, dequant, ws, stream);
+  if (!o || !q) return GPIC_EINVAL;
+  if (!aligned16(o) || !aligned16(q) || !aligned16(ws)) return GPIC_EALIGN;
+  // one past the last source word (each product below 2^62: the sum fits 64 unsigned bits)
+  const uint64_t last = ((uint64_t)(B - 1) * sb + (uint64_t)(H - 1) * sh + (uint64_t)(N - 1) * sn + D) / 8;
+  if (n / 8 >= big || last >= (uint64_t)big) return GPIC_ESHAPE;
+  // [B, N, H, D] contiguous (a stride of a dimension of extent 1 does not matter): the flat cast of o
+  if ((H == 1 || sh == D) && (N == 1 || sn == H * D) && (B == 1 || sb == N * H * D))
+    return gpic_fp8_tcast(o, GPIC_DTYPE_BF16, n, q, dequant, ws, stream);
+  const HeadMap map{fast_div((uint32_t)(D / 8)), fast_div((uint32_t)H), fast_div((uint32_t)N),
+                    (uint32_t)(sb / 8), (uint32_t)(sh / 8), (uint32_t)(sn / 8)};
+  hipStream_t st = (hipStream_t)stream;
+  if (launch_tcast_once<uint16_t, HeadMap>(o, n, q, dequant, ws, st, map)) return (int)hipGetLastError();
+  return launch_tcast<uint16_t, HeadMap>(o, n, q, dequant, static_cast<uint32_t *>(ws), st, map);
 }
 
 int gpic_fp8_tcast_noalloc(const void *x, int dtype, int64_t n, uint8_t *q, float *dequant, void *stream) {

@@ -28,6 +28,7 @@ SIGNATURES = {
     "gpic_fp8_tcast_noalloc": (_int, [_vp, _int, _i64, _vp, _vp, _vp]),
     "gpic_fp8_tcast_t": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_tcast_t_group": (_int, [_int, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gpic_fp8_tcast_heads": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "gpic_fp8_swiglu_tcast": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_swiglu_tcast_t": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     "gpic_fp8_swiglu_bwd": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),

@@ -1,8 +1,9 @@
 """Recipe dispatcher of the FP8 path (baselines/PixelGen/src/utils/fp8.py:13-56): "native" / "native2" convert the
 image blocks with convert_native (phase 1 / 2), "native3" with every GEMM in FP8 (phase 3), "native3+text" also the
-image blocks' kv_y and the text-refine blocks' linears (phase 3, convert_native(text=True)); "native3+norm" and
-"native3+text+norm" also route the image blocks' norm sites through the producer-fused kernels
-(convert_native(fused_norm=True)). Every other recipe name selects a torchao Float8Linear recipe in the reference;
+image blocks' kv_y and the text-refine blocks' linears (phase 3, convert_native(text=True)); "+norm" also routes the
+image blocks' norm sites through the producer-fused kernels (convert_native(fused_norm=True)), "+heads" the attention
+output feeding each converted proj (convert_native(fused_heads=True)), "+fused" both. Every other recipe name selects
+a torchao Float8Linear recipe in the reference;
 this build implements the native recipes only and refuses the others with a ValueError.
 """
 import torch
@@ -10,8 +11,12 @@ import torch
 from .fp8_native import convert_native
 
 KEEP = ("adaLN_modulation",)
-NATIVE = {"native": (1, False, False), "native2": (2, False, False), "native3": (3, False, False),
-          "native3+text": (3, True, False), "native3+norm": (3, False, True), "native3+text+norm": (3, True, True)}
+# recipe -> (phase, text, fused_norm, fused_heads)
+NATIVE = {"native": (1, False, False, False), "native2": (2, False, False, False), "native3": (3, False, False, False),
+          "native3+text": (3, True, False, False), "native3+norm": (3, False, True, False),
+          "native3+text+norm": (3, True, True, False), "native3+heads": (3, False, False, True),
+          "native3+text+heads": (3, True, False, True), "native3+fused": (3, False, True, True),
+          "native3+text+fused": (3, True, True, True)}
 
 
 def fp8_filter(mod, fqn):
@@ -35,8 +40,8 @@ def convert_fp8(net, recipe):
         raise ValueError(f"FP8 recipe {recipe!r} is not available: this build implements the MI355X-native recipes "
                          f"{sorted(NATIVE)} only (the reference's other recipes are torchao's Float8Linear)")
     keys = set(net.state_dict())
-    phase, text, fused_norm = NATIVE[recipe]
-    n = convert_native(net, phase=phase, text=text, fused_norm=fused_norm)
+    phase, text, fused_norm, fused_heads = NATIVE[recipe]
+    n = convert_native(net, phase=phase, text=text, fused_norm=fused_norm, fused_heads=fused_heads)
     if set(net.state_dict()) != keys:
         raise RuntimeError("FP8 conversion changed the state-dict keys")
     where = "image and text blocks" if text else "image blocks"

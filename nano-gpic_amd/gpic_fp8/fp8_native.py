@@ -101,6 +101,41 @@ def _(x, want_q=True):
             x.new_empty(1, dtype=torch.float32))
 
 
+@torch.library.custom_op("gpic::fp8_tcast_heads", mutates_args=())
+def tcast_heads(o: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The attention output o [B, H, N, D] (D % 16 == 0) -> (q [B, N, H D] e4m3, dequant [1] fp32): the bytes and scale
+    tcast(o.transpose(1, 2).reshape(B, N, H D)) gives -- proj's input at JiT_T2I.py:183-185 -- read from o in its own
+    layout (either of those scaled_dot_product_attention's backends write: [B, H, N, D] or [B, N, H, D] in memory), so
+    the head-merging copy is never made. An extension of the reference, which casts the copy (fp8_native.py:3-6,
+    114-122). A bf16 o whose rows are not 16-byte aligned is made contiguous first; another dtype takes that copy and
+    tcast."""
+    L.require_gpu(o)
+    if o.dim() != 4 or o.shape[3] % 16:
+        raise ValueError(f"tcast_heads needs o [B, H, N, D] with D % 16 == 0, got {tuple(o.shape)}")
+    B, H, N, D = o.shape
+    if o.dtype != torch.bfloat16:
+        return tcast(o.transpose(1, 2).reshape(B, N, H * D))
+    # a dimension of extent 1 takes stride 0 (its stride never multiplies a nonzero index)
+    st = [0 if e == 1 else s for e, s in zip(o.shape, o.stride())]
+    if (o.numel() and (st[3] not in (0, 1) or any(s % 8 or s < 0 for s in st[:3]) or o.data_ptr() % 16)):
+        o = L.aligned(o.contiguous())
+        st = [0 if e == 1 else s for e, s in zip(o.shape, o.stride())]
+    q = torch.empty(B, N, H * D, dtype=E4, device=o.device)
+    s = torch.empty(1, dtype=torch.float32, device=o.device)
+    with torch.cuda.device(o.device):
+        ws = L.cast_workspace(o.device)
+        L.check(L.lib().gpic_fp8_tcast_heads(o.data_ptr() if o.numel() else None, B, H, N, D, st[0], st[1], st[2],
+                                             q.data_ptr() if o.numel() else None, s.data_ptr(), ws.data_ptr(),
+                                             L.stream_ptr(o.device)), "gpic_fp8_tcast_heads")
+    return q, s
+
+
+@tcast_heads.register_fake
+def _(o):
+    B, H, N, D = o.shape
+    return o.new_empty(B, N, H * D, dtype=E4), o.new_empty(1, dtype=torch.float32)
+
+
 @torch.library.custom_op("gpic::fp8_tcast_t_group", mutates_args=())
 def tcast_t_group(xs: list[torch.Tensor]) -> list[torch.Tensor]:
     """tcast_t of each 2-D tensor in xs, in one call: [q0, qt0, s0, q1, qt1, s1, ...], the same bytes and scales as
@@ -469,6 +504,35 @@ class _Fp8LinearF8(torch.autograd.Function):
         return dx, dw, db, None
 
 
+class _Fp8HeadsLinearF8(torch.autograd.Function):
+    """_Fp8LinearF8 on x = o.transpose(1, 2).reshape(B, N, H D) for the attention output o [B, H, N, D] (proj,
+    JiT_T2I.py:183-185): x's e4m3 bytes come from tcast_heads(o), so x itself is never written; the same GEMMs and
+    saved bytes as _Fp8LinearF8, and the gradient of o is dx viewed back as [B, H, N, D] (what the transpose and
+    reshape give in autograd), so every output and gradient is the same bits as fp8_linear_f8 on the copy."""
+    @staticmethod
+    def forward(ctx, o, w, b, wcast=None):
+        B, H, N, D = o.shape
+        xq, sx = tcast_heads(o)
+        xq = xq.view(B * N, H * D)
+        wq, wqt, sw = tcast_t(w) if wcast is None else wcast
+        y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
+        ctx.save_for_backward(xq, sx, wqt, sw)
+        ctx.has_b, ctx.shape, ctx.wdt = b is not None, (B, H, N, D), w.dtype
+        return y.view(B, N, w.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        xq, sx, wqt, sw = ctx.saved_tensors
+        B, H, N, D = ctx.shape
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
+        dyq, sdy = tcast(dy2)
+        dx = fp8_gemm(dyq, sdy, wqt, sw, None, False)                      # [M, N] . [K, N]^T
+        do = dx.view(B, N, H, D).transpose(1, 2)
+        dw = fp8_gemm_mn(dyq, sdy, xq, sx).to(ctx.wdt)                     # [M, N]^T . [M, K]
+        db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
+        return do, dw, db, None
+
+
 class _SwiGLUw3(torch.autograd.Function):
     """y = w3(silu(z1) * z2), the product written as FP8 rows for the GEMM (fp8_native.py:207-232)."""
     @staticmethod
@@ -596,6 +660,18 @@ def fp8_linear_f8(x, w, b=None, wcast=None):
         return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b, _check_cast("wcast", w, wcast))
 
 
+def fp8_heads_linear_f8(o, w, b=None, wcast=None):
+    """Phase 3 fp8_linear_f8 applied to the attention output o [B, H, N, D] as proj takes it: the same result and
+    gradients as fp8_linear_f8(o.transpose(1, 2).reshape(B, N, H D), w, b) without that copy (its e4m3 bytes come from
+    tcast_heads(o)). wcast: as fp8_linear_f8's."""
+    if o.dim() != 4:
+        raise ValueError(f"fp8_heads_linear_f8 needs o [B, H, N, D], got {tuple(o.shape)}")
+    if o.shape[1] * o.shape[3] != w.shape[1]:
+        raise ValueError(f"o {tuple(o.shape)} merges to {o.shape[1] * o.shape[3]} features, w has {w.shape[1]}")
+    with torch.autocast("cuda", enabled=False):
+        return _Fp8HeadsLinearF8.apply(o.to(torch.bfloat16), w, b, _check_cast("wcast", w, wcast))
+
+
 def fp8_mlp_f8(x, w12, w3, w12cast=None, w3cast=None):
     """Phase 3 fp8_mlp: every GEMM of the SwiGLU MLP in FP8. w12cast / w3cast: as fp8_linear_f8's wcast."""
     with torch.autocast("cuda", enabled=False):
@@ -650,7 +726,7 @@ def _convert_block(blk, phase, attn_names):
     return n
 
 
-def convert_native(net, phase=1, text=False, fused_norm=False):
+def convert_native(net, phase=1, text=False, fused_norm=False, fused_heads=False):
     """Phase 1: the image blocks' qkv_x, proj, w12 to Fp8Linear and their SwiGLU's w3 GEMM to the fused path. Phase 2:
     qkv_x and proj as in phase 1, the MLP as one fused FP8 function with FP8 dgrads. Phase 3: qkv_x and proj to
     Fp8LinearF8, the MLP as one function with every GEMM in FP8. Returns the count of GEMMs converted
@@ -661,9 +737,14 @@ def convert_native(net, phase=1, text=False, fused_norm=False):
     linears of M = batch x text tokens, which the same kernels serve.
     fused_norm=True (phase 3 only; an extension: the reference's lever K, JiT_T2I.py:201-207, and its FP8 linears stay
     separate) also rewires each image block's forward so its two norm sites write h's e4m3 bytes for qkv_x and the
-    MLP directly (gpic_fp8.norm.convert_fused_norm); the GEMM count is unchanged."""
+    MLP directly (gpic_fp8.norm.convert_fused_norm); the GEMM count is unchanged.
+    fused_heads=True (phase 3 only; an extension: the reference casts the head-merged copy of the attention output,
+    JiT_T2I.py:183-185) also makes each converted attention's proj cast the attention output in its own layout
+    (gpic_fp8.heads.convert_fused_heads): the head-merging copy is never made; the GEMM count is unchanged."""
     if fused_norm and phase != 3:
         raise ValueError("fused_norm needs phase 3 (the fused norm consumers run every GEMM in FP8)")
+    if fused_heads and phase != 3:
+        raise ValueError("fused_heads needs phase 3 (the attention output's fused cast feeds the phase-3 proj)")
     n = 0
     for blk in getattr(net, "blocks", []):
         n += _convert_block(blk, phase, ("qkv_x", "proj", "kv_y") if text else ("qkv_x", "proj"))
@@ -673,6 +754,9 @@ def convert_native(net, phase=1, text=False, fused_norm=False):
     if fused_norm:
         from .norm import convert_fused_norm
         convert_fused_norm(net)
+    if fused_heads:
+        from .heads import convert_fused_heads
+        convert_fused_heads(net)
     return n
 
 

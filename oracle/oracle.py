@@ -16,6 +16,8 @@ How each function is pinned (tests/test_oracle.py):
                 power-of-two scale invariant.
   swiglu        the eager torch expression of fp8_native.py:226-231 with torch.sigmoid, within 1 bf16 ulp (and
                 equal for >99.9% of values); the exp against math.exp to <= 2 fp32 ulp on every bf16 input.
+  tcast_heads   the cast of o in its own order, permuted: the scale is the same for any order of the elements and
+                the bytes are elementwise, so byte (b N + n, h D + d) is byte (b, h, n, d) of tcast(o).
   mm            exact small-integer operands with power-of-two scales (bf16-exact sums), identity / one-hot B,
                 and torch's fp32 matmul of the same dequantized operands.
 """
@@ -161,6 +163,14 @@ def tcast(x):
 
 
 # ---------------------------------------------------------------- SwiGLU (fp8_native.py:52-98, 130-172)
+
+def tcast_heads(o):
+    """The attention output's cast as proj reads it (JiT_T2I.py:183-185: x = attention(q, k, v);
+    x.transpose(1, 2).reshape(B, N, C); tcast(x) in proj, fp8_native.py:114-122,187): o [B, H, N, D] bf16 bits ->
+    (e4m3 bytes [B N, H D], dequant, amax bits)."""
+    B, H, N, D = o.shape
+    return tcast(np.ascontiguousarray(o.transpose(0, 2, 1, 3)).reshape(B * N, H * D))
+
 
 def sigmoid(x):
     L = lib()

@@ -71,6 +71,19 @@ def test_validation_codes():
     assert tg(2, good[0], 0, I(4, 20), I(16, 16), good[4], good[5], I(16, 16), *good[7:]) == -3   # ldt < rows
     assert tg(2, P(wsp, wsp + 2), 0, *good[2:]) == -4                           # misaligned second source
     assert lib.gpic_fp8_tcast_t(wsp, 0, 40, 32, wsp, wsp, 32, wsp, wsp, None) == -3
+    # the attention output's head-merging cast: extents and strides >= 0, D % 16, strides % 8, 16-byte pointers,
+    # word indices below 2^31
+    th = lib.gpic_fp8_tcast_heads
+    assert th(wsp, -1, 2, 4, 16, 128, 64, 16, wsp, wsp, wsp, None) == -1
+    assert th(wsp, 1, 2, 4, 16, 128, -64, 16, wsp, wsp, wsp, None) == -1
+    assert th(wsp, 1, 2, 4, 16, 128, 64, 16, wsp, None, wsp, None) == -1
+    assert th(None, 1, 2, 4, 16, 128, 64, 16, wsp, wsp, wsp, None) == -1
+    assert th(wsp, 1, 2, 4, 24, 192, 96, 24, wsp, wsp, wsp, None) == -3
+    assert th(wsp, 1, 2, 4, 16, 128, 68, 16, wsp, wsp, wsp, None) == -4
+    assert th(wsp + 8, 1, 2, 4, 16, 128, 64, 16, wsp, wsp, wsp, None) == -4
+    assert th(wsp, 1, 2, 4, 16, 128, 64, 16, wsp + 8, wsp, wsp, None) == -4
+    assert th(wsp, 2, 2, 4, 16, 1 << 34, 64, 16, wsp, wsp, wsp, None) == -3
+    assert th(wsp, 1 << 20, 16, 1024, 64, 1 << 20, 64, 1024, wsp, wsp, wsp, None) == -3
     # SwiGLU: H % 8, strides
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 12, 24, wsp, 12, wsp, wsp, None) == -3
     assert lib.gpic_fp8_swiglu_tcast(wsp, 4, 16, 16, wsp, 16, wsp, wsp, None) == -3

@@ -265,3 +265,90 @@ def test_norm_width_checks_before_any_work():
         G.mod_rmsnorm(x, w, m, m, 1e-6)
     with pytest.raises(RuntimeError, match="GPU only"):   # (the device is checked first)
         G.res_mod_rmsnorm_q(x[..., :6], x[..., :6], m[..., :6], w[:6], m[..., :6], m[..., :6], 1e-6, True, True)
+
+
+# ------------------------------------------------------------------------------------------------ attention output
+
+def test_pending_heads_keeps_only_the_merge_pending():
+    """The attention output handed back by a converted attention: transpose(1, 2) then reshape to [B, N, H D] stay
+    pending; any other use gives exactly the eager tensor (attributes, methods, operators, torch functions)."""
+    from gpic_fp8.heads import _PendingHeads
+    o = torch.randn(2, 3, 5, 16)
+    eager = o.transpose(1, 2).reshape(2, 5, 48)
+    p = _PendingHeads(o, 0)
+    t = p.transpose(1, 2)
+    assert isinstance(t, _PendingHeads) and t.stage == 1
+    assert isinstance(p.transpose(-3, -2), _PendingHeads)
+    for shape in ((2, 5, 48), ((2, 5, 48),), (2, 5, -1), (torch.Size([2, 5, 48]),)):
+        m = t.reshape(*shape)
+        assert isinstance(m, _PendingHeads) and m.stage == 2 and torch.equal(m.materialize(), eager)
+    assert torch.equal(t.reshape(10, 48), eager.reshape(10, 48))                 # another reshape: eager result
+    assert torch.equal(p.transpose(2, 3), o.transpose(2, 3))                     # another transpose: eager result
+    m = t.reshape(2, 5, 48)
+    assert m.shape == eager.shape and m.dtype == o.dtype
+    assert torch.equal(torch.add(m, 1), eager + 1) and torch.equal(m * 2, eager * 2) and torch.equal(2 * m, eager * 2)
+    assert torch.equal(m[0], eager[0]) and torch.equal(-m, -eager)
+    assert torch.equal(p + 0, o) and torch.equal(t.contiguous(), o.transpose(1, 2).contiguous())
+
+
+def _sdpa_net(d=32, heads=2, n=2):
+    import attn_blocks as AB
+
+    class _B(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = AB.SdpaAttn(d, heads)
+            self.mlp = SwiGLU(d, 4 * d)
+
+    class _N(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = nn.ModuleList(_B() for _ in range(n))
+            self.text_refine_blocks = nn.ModuleList(TextBlock(d) for _ in range(1))
+    return _N()
+
+
+def test_convert_fused_heads(monkeypatch):
+    """native3+heads: the same GEMMs and state-dict keys as native3; each attention whose forward calls
+    scaled_dot_product_attention as `attention` gets an Fp8HeadsLinearF8 proj and a rebound forward (idempotent);
+    attentions without such a forward keep phase 3's proj; outside phase 3 the option is refused. The rebound
+    forward hands proj the attention output itself (fp8_heads_linear_f8 on o [B, H, N, D]) and reads every other
+    global name from its module at call time. GEMMs stand in as plain linears (no GPU here)."""
+    import attn_blocks as AB
+    from gpic_fp8 import heads as HD
+    net = _sdpa_net()
+    ref = _sdpa_net()
+    ref.load_state_dict(net.state_dict())
+    keys = set(net.state_dict())
+    assert G.convert_fp8(net, "native3+heads") == 2 * 4
+    assert set(net.state_dict()) == keys
+    for b in net.blocks:
+        assert type(b.attn.proj) is G.Fp8HeadsLinearF8 and type(b.attn.qkv_x) is G.Fp8LinearF8
+        assert b.attn._gpic_fused_heads and "forward" in b.attn.__dict__
+    assert type(net.text_refine_blocks[0].attn.proj) is nn.Linear                 # image blocks only without text
+    assert G.convert_fused_heads(net) == 0
+    with pytest.raises(ValueError, match="phase 3"):
+        G.convert_native(_sdpa_net(), phase=2, fused_heads=True)
+    plain = Net(n=1)                                                             # stand-in attention with no forward
+    G.convert_native(plain, phase=3, fused_heads=True)
+    assert type(plain.blocks[0].attn.proj) is G.Fp8LinearF8
+    assert G.convert_fp8(_sdpa_net(), "native3+text+heads") == 2 * 4 + 4
+
+    seen = []
+    lin = lambda x, w, b=None, wcast=None: torch.nn.functional.linear(x, w, b)
+
+    def heads_lin(o, w, b=None):
+        seen.append(tuple(o.shape))
+        B, H, N, D = o.shape
+        return torch.nn.functional.linear(o.transpose(1, 2).reshape(B, N, H * D), w, b)
+    monkeypatch.setattr(F, "fp8_linear_f8", lin)
+    monkeypatch.setattr(HD, "fp8_linear_f8", lin)
+    monkeypatch.setattr(HD, "fp8_heads_linear_f8", heads_lin)
+    x = torch.randn(3, 7, 32)
+    for b, r in zip(net.blocks, ref.blocks):
+        assert torch.allclose(b.attn(x, None, None), r.attn(x, None, None), rtol=1e-6, atol=1e-6)
+    assert seen == [(3, 2, 7, 16)] * 2 and [b.attn.proj.heads_calls for b in net.blocks] == [1, 1]
+    g = net.blocks[0].attn.forward.__func__.__globals__
+    assert g["nn"] is AB.nn and g["attention"] is not AB.attention
+    monkeypatch.setattr(AB, "_gpic_probe", 5, raising=False)
+    assert g["_gpic_probe"] == 5                                                 # module globals read live

@@ -134,6 +134,22 @@ def test_transpose_invariant():
     assert np.array_equal(qt, q.T) and d == dt
 
 
+def test_tcast_heads_is_the_permuted_cast():
+    """tcast_heads: byte (b N + n, h D + d) is byte (b, h, n, d) of the cast of o in its own order, with its scale
+    (one amax for any order; bytes elementwise). A mutant that merges without the transpose fails."""
+    rng = np.random.default_rng(6)
+    B, H, N, D = 2, 3, 5, 16
+    o = O.f32_to_bf16(rng.standard_normal((B, H, N, D)).astype(np.float32))
+    q, d, am = O.tcast_heads(o)
+    q0, d0, am0 = O.tcast(o)
+    assert d == d0 and am == am0 and q.shape == (B * N, H * D)
+    for b in range(B):
+        for h in range(H):
+            for n in range(N):
+                assert np.array_equal(q[b * N + n, h * D:(h + 1) * D], q0[b, h, n])
+    assert not np.array_equal(O.tcast(o.reshape(B * N, H * D))[0], q)
+
+
 def test_pow2_scale_invariant():
     rng = np.random.default_rng(5)
     x = rng.standard_normal(5000).astype(np.float32)
