@@ -19,6 +19,7 @@ e4m3 bytes and scale directly, and h itself only when asked. Functions:
 The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel (res_mod_rmsnorm_bwd);
 the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
 """
+import types
 from typing import Optional
 
 import torch
@@ -314,24 +315,23 @@ def fused_norm_ok(blk):
             n2.weight.numel() == C and C > 0 and C % 4 == 0 and C <= BWD_MAX_C and qkv.in_features == C)
 
 
-def _fused_block_forward(blk):
+def _fused_block_forward(blk, x, y, c, pos, mask=None):
     """FlattenDiTBlock.forward's lever-K branch (JiT_T2I.py:201-207) with each norm site's output cast in the norm:
     site 1 hands qkv_x h's e4m3 bytes (through Fp8NormLinearF8), site 2 and the MLP run as fp8_res_mod_rmsnorm_mlp.
     The same operations, in the same order, as that branch over mod_rmsnorm / res_mod_rmsnorm and the phase-3
-    linears, so the outputs and gradients are the same bits; h is never written in bf16."""
-    def forward(x, y, c, pos, mask=None):
-        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = blk.adaLN_modulation(c).chunk(6, dim=-1)
-        qkv = blk.attn.qkv_x
-        marker = torch.empty(x.shape, dtype=torch.bfloat16, device="meta")
-        qkv._gpic_norm = (marker, x, blk.norm1.weight, shift_msa, scale_msa, _norm_eps(blk.norm1))
-        try:
-            a = blk.attn(marker, y, pos, mask)
-        finally:
-            qkv.__dict__.pop("_gpic_norm", None)
-        x, out = fp8_res_mod_rmsnorm_mlp(x, a, gate_msa, blk.norm2.weight, shift_mlp, scale_mlp, _norm_eps(blk.norm2),
-                                         blk.mlp.w12.weight, blk.mlp.w3.weight)
-        return x + gate_mlp * out
-    return forward
+    linears, so the outputs and gradients are the same bits; h is never written in bf16. Bound to the block as its
+    forward (a method, so that a deep copy of the model, e.g. an EMA copy, runs its own modules)."""
+    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = blk.adaLN_modulation(c).chunk(6, dim=-1)
+    qkv = blk.attn.qkv_x
+    marker = torch.empty(x.shape, dtype=torch.bfloat16, device="meta")
+    qkv._gpic_norm = (marker, x, blk.norm1.weight, shift_msa, scale_msa, _norm_eps(blk.norm1))
+    try:
+        a = blk.attn(marker, y, pos, mask)
+    finally:
+        qkv.__dict__.pop("_gpic_norm", None)
+    x, out = fp8_res_mod_rmsnorm_mlp(x, a, gate_msa, blk.norm2.weight, shift_mlp, scale_mlp, _norm_eps(blk.norm2),
+                                     blk.mlp.w12.weight, blk.mlp.w3.weight)
+    return x + gate_mlp * out
 
 
 def convert_fused_norm(net):
@@ -343,7 +343,7 @@ def convert_fused_norm(net):
         if not fused_norm_ok(blk) or getattr(blk, "_gpic_fused_norm", False):
             continue
         blk.attn.qkv_x.__class__ = Fp8NormLinearF8
-        blk.forward = _fused_block_forward(blk)
+        blk.forward = types.MethodType(_fused_block_forward, blk)
         blk._gpic_fused_norm = True
         n += 1
     return n

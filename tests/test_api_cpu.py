@@ -1,5 +1,6 @@
 """Host-side logic of the drop-in API: the converters (GEMM counts, state-dict keys, phases), the torchao recipe
 guard, the op registrations and fake kernels, the refusal of CPU tensors, and the reference() helper."""
+import copy
 import os
 
 import numpy as np
@@ -201,6 +202,9 @@ def test_convert_fused_norm():
     last = net.blocks[3]
     assert type(last.attn.qkv_x) is G.Fp8LinearF8 and "forward" not in last.__dict__
     assert G.convert_fused_norm(net) == 0
+    twin = copy.deepcopy(net)                          # e.g. an EMA copy: its forwards run its own modules
+    for b, t in zip(net.blocks[:3], twin.blocks[:3]):
+        assert t.forward.__self__ is t and b.forward.__self__ is b
     assert G.convert_fp8(NormNet(), "native3+text+norm") == 3 * 5 + 4
     with pytest.raises(ValueError, match="phase 3"):
         G.convert_native(NormNet(), phase=2, fused_norm=True)
@@ -327,6 +331,9 @@ def test_convert_fused_heads(monkeypatch):
         assert b.attn._gpic_fused_heads and "forward" in b.attn.__dict__
     assert type(net.text_refine_blocks[0].attn.proj) is nn.Linear                 # image blocks only without text
     assert G.convert_fused_heads(net) == 0
+    twin = copy.deepcopy(net)                          # e.g. an EMA copy: its forwards run its own modules
+    for b, t in zip(net.blocks, twin.blocks):
+        assert t.attn.forward.__self__ is t.attn and b.attn.forward.__self__ is b.attn
     with pytest.raises(ValueError, match="phase 3"):
         G.convert_native(_sdpa_net(), phase=2, fused_heads=True)
     plain = Net(n=1)                                                             # stand-in attention with no forward

@@ -152,13 +152,14 @@ def _run(net, x, c, mask):
     return [y, x.grad] + [p.grad for p in net.parameters()]
 
 
-@pytest.mark.parametrize("recipe", ["native3+heads", "native3+fused"])
+@pytest.mark.parametrize("recipe,C,heads", [("native3+heads", 1024, 16), ("native3+fused", 1024, 16),
+                                             ("native3+fused", 896, 14)])
 @pytest.mark.parametrize("masked", [False, True])
-def test_converted_model_takes_the_heads_path(dev, recipe, masked):
+def test_converted_model_takes_the_heads_path(dev, recipe, C, heads, masked):
     """convert_fp8(net, recipe) against "native3" on the same weights: the output and every gradient bit for bit,
     with and without a key mask (scaled_dot_product_attention then writes o as [B, N, H, D] or [B, H, N, D]), while
-    every proj takes the attention output directly."""
-    C, heads, B, N = 1024, 16, 8, 256
+    every proj takes the attention output directly. C = 896 is the d11 width (14 heads of 64)."""
+    B, N = 8, 256
     net_u, net_f = _nets(C, heads, 2, dev)
     assert G.convert_fp8(net_u, "native3") == 8 and G.convert_fp8(net_f, recipe) == 8
     x = torch.randn(B, N, C, device=dev).to(torch.bfloat16)
@@ -174,3 +175,23 @@ def test_converted_model_takes_the_heads_path(dev, recipe, masked):
     assert all(type(b.attn.proj) is G.Fp8HeadsLinearF8 and b.attn.proj.heads_calls == 1 for b in net_f.blocks)
     if recipe == "native3+fused":
         assert all(type(b.attn.qkv_x) is G.Fp8NormLinearF8 for b in net_f.blocks)
+
+
+def test_deep_copy_of_a_converted_model_runs_its_own_modules(dev):
+    """A deep copy of a native3+fused model (as an EMA copy is made) gives the original's bits on the same weights,
+    and after its own weights change only the copy's output changes: its rebound forwards use the copy's modules."""
+    C, heads, B, N = 512, 8, 2, 64
+    net, _ = _nets(C, heads, 2, dev)
+    G.convert_fp8(net, "native3+fused")
+    twin = copy.deepcopy(net)
+    x = torch.randn(B, N, C, device=dev).to(torch.bfloat16)
+    c = torch.randn(B, 1, C, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y0, y1 = net(x, c), twin(x, c)
+        assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+        for b in twin.blocks:
+            b.attn.proj.weight.mul_(0.5)
+            b.mlp.w3.weight.mul_(0.5)
+        y2, y3 = net(x, c), twin(x, c)
+    assert torch.equal(y2.view(torch.int16), y0.view(torch.int16)) and not torch.equal(y3, y0)
+    assert all(b.attn.proj.heads_calls == 2 for b in twin.blocks)
