@@ -117,8 +117,9 @@ def cast_traffic(G, dev):
     """Each cast once, for counter collection (one row per dispatch, in this order): config 2 (a warm-up call, then a
     warm one, then one after a 512 MB write that flushes L2 / MALL), an fp32 weight [3072 x 1024] (DDP weights are
     fp32), the dY of qkv [32768 x 3072] (the step's largest flat cast), the d12 SwiGLU casts of the step: the
-    product cast of z [32768 x 8192] and the backward's dz cast, and the step's four bf16 weights in one grouped
-    transposing cast."""
+    product cast of z [32768 x 8192] and the backward's dz cast, the step's four bf16 weights in one grouped
+    transposing cast, and the attention output's cast with its head merge folded in (tcast_heads of o
+    [128 x 16 x 256 x 64] as the flash backend writes it, [B, H, N, D] in memory)."""
     import torch
     xc = config2_input(dev)
     flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
@@ -129,6 +130,7 @@ def cast_traffic(G, dev):
     dqkv = (torch.randn(M_TOK, 3 * C, generator=g, device=dev) * 0.01).to(torch.bfloat16)
     wts = [(torch.randn(r, c, generator=g, device=dev) * c ** -0.5).to(torch.bfloat16)
            for r, c in ((3 * C, C), (C, C), (2 * H, C), (C, H))]
+    o = torch.randn(M_TOK // 256, 16, 256, C // 16, generator=g, device=dev).to(torch.bfloat16)
     order = []
     for name, fn in (("config2 warm-up", lambda: G.tcast(xc)), ("config2 warm", lambda: G.tcast(xc)),
                      ("flush", lambda: flush.fill_(1)), ("config2 flushed", lambda: G.tcast(xc)),
@@ -136,7 +138,8 @@ def cast_traffic(G, dev):
                      ("qkv dY [32768 x 3072]", lambda: G.tcast(dqkv)),
                      ("swiglu product cast z [32768 x 8192]", lambda: G.swiglu_tcast(z)),
                      ("swiglu backward dz cast", lambda: G.swiglu_bwd_q(z, da)),
-                     ("d12 weights, grouped transposing cast", lambda: G.tcast_t_group(wts))):
+                     ("d12 weights, grouped transposing cast", lambda: G.tcast_t_group(wts)),
+                     ("attention output [128 x 16 x 256 x 64] (tcast_heads)", lambda: G.tcast_heads(o))):
         fn()
         torch.cuda.synchronize()
         order.append(name)
