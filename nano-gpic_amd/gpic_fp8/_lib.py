@@ -70,6 +70,27 @@ def check(status, what):
         raise RuntimeError(f"{what} failed: {msg} (status {status})")
 
 
+_IMPL = {}   # custom op -> the function it was made from
+
+
+def custom_op(name):
+    """torch.library.custom_op(name, mutates_args=()) that also keeps the function it wraps, for call()."""
+    def deco(fn):
+        op = torch.library.custom_op(name, mutates_args=())(fn)
+        _IMPL[op] = fn
+        return op
+    return deco
+
+
+def call(op, *args):
+    """op(*args) for the path's own calls (the autograd Functions, one op inside another): outside torch.compile
+    tracing the op's function runs directly, skipping the dispatcher (~10 us of host time per call, which bounds
+    blocks of short kernels); under tracing the op itself, so a compiled graph holds the opaque custom op. Any other
+    callable (a stand-in put in an op's place) is called as it is."""
+    fn = None if torch.compiler.is_compiling() else _IMPL.get(op)
+    return fn(*args) if fn is not None else op(*args)
+
+
 def require_gpu(*tensors):
     for t in tensors:
         if t is not None and t.device.type != "cuda":

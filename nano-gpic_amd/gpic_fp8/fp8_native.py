@@ -53,7 +53,7 @@ def _prep_rows(t, min_cols):
 
 # ------------------------------------------------------------------------------------------------ casts
 
-@torch.library.custom_op("gpic::fp8_tcast", mutates_args=())
+@L.custom_op("gpic::fp8_tcast")
 def tcast(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """x (any float dtype) -> e4m3 (contiguous, x's shape) and its tensorwise dequantization scale amax / 448 [1] fp32.
     (fp8_native.py:114-122)"""
@@ -73,7 +73,7 @@ def _(x):
     return x.new_empty(x.shape, dtype=E4), x.new_empty(1, dtype=torch.float32)
 
 
-@torch.library.custom_op("gpic::fp8_tcast_t", mutates_args=())
+@L.custom_op("gpic::fp8_tcast_t")
 def tcast_t(x: torch.Tensor, want_q: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """x [R, C] (any float dtype, C % 16 == 0) -> (q [R, C] e4m3, or an empty tensor when want_q is False;
     qt [C, R16] e4m3 = q transposed, R16 = R rounded up to 16, zero bytes in columns R..R16-1; dequant [1] fp32).
@@ -101,7 +101,7 @@ def _(x, want_q=True):
             x.new_empty(1, dtype=torch.float32))
 
 
-@torch.library.custom_op("gpic::fp8_tcast_heads", mutates_args=())
+@L.custom_op("gpic::fp8_tcast_heads")
 def tcast_heads(o: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """The attention output o [B, H, N, D] (D % 16 == 0) -> (q [B, N, H D] e4m3, dequant [1] fp32): the bytes and scale
     tcast(o.transpose(1, 2).reshape(B, N, H D)) gives -- proj's input at JiT_T2I.py:183-185 -- read from o in its own
@@ -114,7 +114,7 @@ def tcast_heads(o: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         raise ValueError(f"tcast_heads needs o [B, H, N, D] with D % 16 == 0, got {tuple(o.shape)}")
     B, H, N, D = o.shape
     if o.dtype != torch.bfloat16:
-        return tcast(o.transpose(1, 2).reshape(B, N, H * D))
+        return L.call(tcast, o.transpose(1, 2).reshape(B, N, H * D))
     # a dimension of extent 1 takes stride 0 (its stride never multiplies a nonzero index)
     st = [0 if e == 1 else s for e, s in zip(o.shape, o.stride())]
     if (o.numel() and (st[3] not in (0, 1) or any(s % 8 or s < 0 for s in st[:3]) or o.data_ptr() % 16)):
@@ -136,7 +136,7 @@ def _(o):
     return o.new_empty(B, N, H * D, dtype=E4), o.new_empty(1, dtype=torch.float32)
 
 
-@torch.library.custom_op("gpic::fp8_tcast_t_group", mutates_args=())
+@L.custom_op("gpic::fp8_tcast_t_group")
 def tcast_t_group(xs: list[torch.Tensor]) -> list[torch.Tensor]:
     """tcast_t of each 2-D tensor in xs, in one call: [q0, qt0, s0, q1, qt1, s1, ...], the same bytes and scales as
     tcast_t(x) for each x. bf16 tensors that fit the device together (a d12 block's four weights) are cast in one
@@ -193,7 +193,7 @@ class WeightCast(tuple):
 
 def weight_casts(*ws):
     """The (q, qt, dequant) triples of tcast_t_group(ws), one per weight, in order (WeightCast tuples)."""
-    o = tcast_t_group(list(ws))
+    o = L.call(tcast_t_group, list(ws))
     out = []
     for i, w in enumerate(ws):
         c = WeightCast(o[3 * i:3 * i + 3])
@@ -211,7 +211,7 @@ def _swiglu_prep(z):
     return _prep_rows(z, z.shape[1])
 
 
-@torch.library.custom_op("gpic::fp8_swiglu_tcast", mutates_args=())
+@L.custom_op("gpic::fp8_swiglu_tcast")
 def swiglu_tcast(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """z [M, 2H] bf16 (w12's output) -> silu(z1) * z2 as e4m3 [M, H] and its tensorwise scale [1] fp32.
     (fp8_native.py:130-144). gpic_fp8_swiglu_tcast_t with qt = NULL: the single pass, which holds up to 96 MiB of the
@@ -237,7 +237,7 @@ def _(z):
     return z.new_empty(M, H2 // 2, dtype=E4), z.new_empty(1, dtype=torch.float32)
 
 
-@torch.library.custom_op("gpic::fp8_swiglu_tcast_t", mutates_args=())
+@L.custom_op("gpic::fp8_swiglu_tcast_t")
 def swiglu_tcast_t(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """swiglu_tcast plus the transposed bytes qt [H, M16] (zero past M): the K-major operand of w3's FP8 wgrad."""
     zc = _swiglu_prep(z)
@@ -288,7 +288,7 @@ def _swiglu_bwd(z, da, want_dz):
     return dz, dq, s
 
 
-@torch.library.custom_op("gpic::fp8_swiglu_bwd", mutates_args=())
+@L.custom_op("gpic::fp8_swiglu_bwd")
 def swiglu_bwd(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """z [M, 2H] bf16, da [M, H] bf16 -> dz [M, 2H] bf16, dz as e4m3 [M, 2H] and its tensorwise scale [1] fp32.
     (fp8_native.py:153-166)"""
@@ -301,7 +301,7 @@ def _(z, da):
     return z.new_empty(M, H2), z.new_empty(M, H2, dtype=E4), z.new_empty(1, dtype=torch.float32)
 
 
-@torch.library.custom_op("gpic::fp8_swiglu_bwd_q", mutates_args=())
+@L.custom_op("gpic::fp8_swiglu_bwd_q")
 def swiglu_bwd_q(z: torch.Tensor, da: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """swiglu_bwd without dz in memory: (dzq [M, 2H] e4m3, scale [1] fp32), the same bytes -- for phase 3, whose w12
     wgrad takes dzq instead of dz (an extension of the reference). One single-pass launch holds up to 80 MiB of dz on
@@ -317,7 +317,7 @@ def _(z, da):
     return z.new_empty(M, H2, dtype=E4), z.new_empty(1, dtype=torch.float32)
 
 
-@torch.library.custom_op("gpic::fp8_swiglu_bwd_t", mutates_args=())
+@L.custom_op("gpic::fp8_swiglu_bwd_t")
 def swiglu_bwd_t(z: torch.Tensor, da: torch.Tensor,
                  want_dz: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """swiglu_bwd plus the transposed bytes dzqt [2H, M16] (zero past M): the K-major operand of w12's FP8 wgrad.
@@ -355,7 +355,7 @@ def _gemm_operand(t, name):
     return t
 
 
-@torch.library.custom_op("gpic::fp8_gemm", mutates_args=())
+@L.custom_op("gpic::fp8_gemm")
 def fp8_gemm(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
              bias: Optional[torch.Tensor] = None, fast: bool = True) -> torch.Tensor:
     """a [M, K] e4m3, b [N, K] e4m3 (both K-contiguous), sa / sb [1] fp32 dequantization scales ->
@@ -401,7 +401,7 @@ def _gemm_operand_mn(t, name):
     return t
 
 
-@torch.library.custom_op("gpic::fp8_gemm_mn", mutates_args=())
+@L.custom_op("gpic::fp8_gemm_mn")
 def fp8_gemm_mn(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tensor,
                 bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """a [K, M] e4m3, b [K, N] e4m3 (both with K as the row index), sa / sb [1] fp32 ->
@@ -426,7 +426,7 @@ def fp8_gemm_mn(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Te
             u = torch.zeros(t.shape[1], k16, dtype=torch.uint8, device=t.device)
             u[:, :K] = t.view(torch.uint8).t()
             return u.view(E4)
-        return fp8_gemm(kmajor(a), sa, kmajor(b), sb, bias, False)
+        return L.call(fp8_gemm, kmajor(a), sa, kmajor(b), sb, bias, False)
     sa = sa.to(torch.float32).reshape(1)
     sb = sb.to(torch.float32).reshape(1)
     if bias is not None:
@@ -451,7 +451,7 @@ def _(a, sa, b, sb, bias=None):
 
 def _mm(xq, sx, wq, sw, fast=True):
     """[M, K] e4m3 x [N, K] e4m3 (each with its tensorwise scale) -> [M, N] bf16 (fp8_native.py:175-178)."""
-    return fp8_gemm(xq, sx, wq, sw, None, fast)
+    return L.call(fp8_gemm, xq, sx, wq, sw, None, fast)
 
 
 # ------------------------------------------------------------------------------------------------ autograd
@@ -462,9 +462,9 @@ class _Fp8Linear(torch.autograd.Function):
     def forward(ctx, x, w, b):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        xq, sx = tcast(x2)
-        wq, sw = tcast(w)
-        y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
+        xq, sx = L.call(tcast, x2)
+        wq, sw = L.call(tcast, w)
+        y = L.call(fp8_gemm, xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
         ctx.save_for_backward(x2, w)
         ctx.has_b, ctx.shape, ctx.wdt = b is not None, shape, w.dtype
         return y.view(*shape[:-1], w.shape[0])
@@ -486,9 +486,9 @@ class _Fp8LinearF8(torch.autograd.Function):
     def forward(ctx, x, w, b, wcast=None):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        xq, sx = tcast(x2)
-        wq, wqt, sw = tcast_t(w) if wcast is None else wcast
-        y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
+        xq, sx = L.call(tcast, x2)
+        wq, wqt, sw = L.call(tcast_t, w) if wcast is None else wcast
+        y = L.call(fp8_gemm, xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
         ctx.save_for_backward(xq, sx, wqt, sw)
         ctx.has_b, ctx.shape, ctx.wdt = b is not None, shape, w.dtype
         return y.view(*shape[:-1], w.shape[0])
@@ -497,9 +497,9 @@ class _Fp8LinearF8(torch.autograd.Function):
     def backward(ctx, dy):
         xq, sx, wqt, sw = ctx.saved_tensors
         dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
-        dyq, sdy = tcast(dy2)
-        dx = fp8_gemm(dyq, sdy, wqt, sw, None, False).view(ctx.shape)     # [M, N] . [K, N]^T
-        dw = fp8_gemm_mn(dyq, sdy, xq, sx).to(ctx.wdt)                   # [M, N]^T . [M, K]
+        dyq, sdy = L.call(tcast, dy2)
+        dx = L.call(fp8_gemm, dyq, sdy, wqt, sw, None, False).view(ctx.shape)     # [M, N] . [K, N]^T
+        dw = L.call(fp8_gemm_mn, dyq, sdy, xq, sx).to(ctx.wdt)                   # [M, N]^T . [M, K]
         db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
         return dx, dw, db, None
 
@@ -512,10 +512,10 @@ class _Fp8HeadsLinearF8(torch.autograd.Function):
     @staticmethod
     def forward(ctx, o, w, b, wcast=None):
         B, H, N, D = o.shape
-        xq, sx = tcast_heads(o)
+        xq, sx = L.call(tcast_heads, o)
         xq = xq.view(B * N, H * D)
-        wq, wqt, sw = tcast_t(w) if wcast is None else wcast
-        y = fp8_gemm(xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
+        wq, wqt, sw = L.call(tcast_t, w) if wcast is None else wcast
+        y = L.call(fp8_gemm, xq, sx, wq, sw, None if b is None else b.to(torch.bfloat16))
         ctx.save_for_backward(xq, sx, wqt, sw)
         ctx.has_b, ctx.shape, ctx.wdt = b is not None, (B, H, N, D), w.dtype
         return y.view(B, N, w.shape[0])
@@ -525,10 +525,10 @@ class _Fp8HeadsLinearF8(torch.autograd.Function):
         xq, sx, wqt, sw = ctx.saved_tensors
         B, H, N, D = ctx.shape
         dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
-        dyq, sdy = tcast(dy2)
-        dx = fp8_gemm(dyq, sdy, wqt, sw, None, False)                      # [M, N] . [K, N]^T
+        dyq, sdy = L.call(tcast, dy2)
+        dx = L.call(fp8_gemm, dyq, sdy, wqt, sw, None, False)                      # [M, N] . [K, N]^T
         do = dx.view(B, N, H, D).transpose(1, 2)
-        dw = fp8_gemm_mn(dyq, sdy, xq, sx).to(ctx.wdt)                     # [M, N]^T . [M, K]
+        dw = L.call(fp8_gemm_mn, dyq, sdy, xq, sx).to(ctx.wdt)                     # [M, N]^T . [M, K]
         db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
         return do, dw, db, None
 
@@ -539,8 +539,8 @@ class _SwiGLUw3(torch.autograd.Function):
     def forward(ctx, z, w3):
         shape = z.shape
         z2d = z.reshape(-1, shape[-1])
-        aq, sa = swiglu_tcast(z2d)
-        wq, sw = tcast(w3)
+        aq, sa = L.call(swiglu_tcast, z2d)
+        wq, sw = L.call(tcast, w3)
         y = _mm(aq, sa, wq, sw)
         ctx.save_for_backward(z2d, aq, sa, w3)
         ctx.shape, ctx.wdt = shape, w3.dtype
@@ -569,11 +569,11 @@ class _Fp8MLP(torch.autograd.Function):
     def forward(ctx, x, w12, w3):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        xq, sx = tcast(x2)
-        w12q, s12 = tcast(w12)
+        xq, sx = L.call(tcast, x2)
+        w12q, s12 = L.call(tcast, w12)
         z = _mm(xq, sx, w12q, s12)
-        aq, sa = swiglu_tcast(z)
-        w3q, s3 = tcast(w3)
+        aq, sa = L.call(swiglu_tcast, z)
+        w3q, s3 = L.call(tcast, w3)
         y = _mm(aq, sa, w3q, s3)
         ctx.save_for_backward(x2, z, aq, sa, w12, w3)
         ctx.shape, ctx.dt = shape, (w12.dtype, w3.dtype)
@@ -583,11 +583,11 @@ class _Fp8MLP(torch.autograd.Function):
     def backward(ctx, dy):
         x2, z, aq, sa, w12, w3 = ctx.saved_tensors
         dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
-        dyq, sdy = tcast(dy2)
-        _, w3tq, s3t = tcast_t(w3, False)                  # [H, C]: the dgrad's B operand
+        dyq, sdy = L.call(tcast, dy2)
+        _, w3tq, s3t = L.call(tcast_t, w3, False)                  # [H, C]: the dgrad's B operand
         da = _mm(dyq, sdy, w3tq, s3t, fast=False)          # [M, H]
-        dz, dzq, sdz = swiglu_bwd(z, da)
-        _, w12tq, s12t = tcast_t(w12, False)               # [C, 2H]
+        dz, dzq, sdz = L.call(swiglu_bwd, z, da)
+        _, w12tq, s12t = L.call(tcast_t, w12, False)               # [C, 2H]
         dx = _mm(dzq, sdz, w12tq, s12t, fast=False)        # [M, C]
         dw12 = (dz.t() @ x2).to(ctx.dt[0])
         dw3 = (dy2.t() @ (aq.to(torch.float32) * sa).to(torch.bfloat16)).to(ctx.dt[1])
@@ -602,12 +602,12 @@ class _Fp8MLPF8(torch.autograd.Function):
     def forward(ctx, x, w12, w3, w12cast=None, w3cast=None):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        xq, sx = tcast(x2)
-        w12q, w12qt, s12 = tcast_t(w12) if w12cast is None else w12cast
-        z = fp8_gemm(xq, sx, w12q, s12)
-        aq, sa = swiglu_tcast(z)
-        w3q, w3qt, s3 = tcast_t(w3) if w3cast is None else w3cast
-        y = fp8_gemm(aq, sa, w3q, s3)
+        xq, sx = L.call(tcast, x2)
+        w12q, w12qt, s12 = L.call(tcast_t, w12) if w12cast is None else w12cast
+        z = L.call(fp8_gemm, xq, sx, w12q, s12)
+        aq, sa = L.call(swiglu_tcast, z)
+        w3q, w3qt, s3 = L.call(tcast_t, w3) if w3cast is None else w3cast
+        y = L.call(fp8_gemm, aq, sa, w3q, s3)
         ctx.save_for_backward(xq, sx, z, aq, sa, w12qt, s12, w3qt, s3)
         ctx.shape, ctx.dt = shape, (w12.dtype, w3.dtype)
         return y.view(*shape[:-1], w3.shape[0])
@@ -616,12 +616,12 @@ class _Fp8MLPF8(torch.autograd.Function):
     def backward(ctx, dy):
         xq, sx, z, aq, sa, w12qt, s12, w3qt, s3 = ctx.saved_tensors
         dy2 = dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16)
-        dyq, sdy = tcast(dy2)
-        da = fp8_gemm(dyq, sdy, w3qt, s3, None, False)           # [M, H]
-        dw3 = fp8_gemm_mn(dyq, sdy, aq, sa)                      # [M, C]^T . [M, H] = [C, H]
-        dzq, sdz = swiglu_bwd_q(z, da)                           # dz itself is not needed: never written
-        dx = fp8_gemm(dzq, sdz, w12qt, s12, None, False)         # [M, C]
-        dw12 = fp8_gemm_mn(dzq, sdz, xq, sx)                     # [M, 2H]^T . [M, C] = [2H, C]
+        dyq, sdy = L.call(tcast, dy2)
+        da = L.call(fp8_gemm, dyq, sdy, w3qt, s3, None, False)           # [M, H]
+        dw3 = L.call(fp8_gemm_mn, dyq, sdy, aq, sa)                      # [M, C]^T . [M, H] = [C, H]
+        dzq, sdz = L.call(swiglu_bwd_q, z, da)                           # dz itself is not needed: never written
+        dx = L.call(fp8_gemm, dzq, sdz, w12qt, s12, None, False)         # [M, C]
+        dw12 = L.call(fp8_gemm_mn, dzq, sdz, xq, sx)                     # [M, 2H]^T . [M, C] = [2H, C]
         return dx.view(ctx.shape), dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1]), None, None
 
 

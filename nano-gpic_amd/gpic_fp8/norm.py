@@ -52,7 +52,7 @@ def _vec(t, B, C):
     return t
 
 
-@torch.library.custom_op("gpic::fp8_res_mod_rmsnorm", mutates_args=())
+@L.custom_op("gpic::fp8_res_mod_rmsnorm")
 def res_mod_rmsnorm_q(x: torch.Tensor, a: torch.Tensor, gate: torch.Tensor, w: torch.Tensor, shift: torch.Tensor,
                       scale: torch.Tensor, eps: float, has_res: bool, want_h: bool, want_q: bool = True
                       ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -98,7 +98,7 @@ def _(x, a, gate, w, shift, scale, eps, has_res, want_h, want_q=True):
             x.new_empty(B * N, dtype=torch.float32))
 
 
-@torch.library.custom_op("gpic::fp8_res_mod_rmsnorm_bwd", mutates_args=())
+@L.custom_op("gpic::fp8_res_mod_rmsnorm_bwd")
 def res_mod_rmsnorm_bwd(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch.Tensor, a: Optional[torch.Tensor],
                         gate: Optional[torch.Tensor], w: torch.Tensor, scale: torch.Tensor, rstd: torch.Tensor
                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -148,7 +148,8 @@ def _(dh, dxn, xs, a, gate, w, scale, rstd):
 
 def _norm_backward(dh, dxn, xs, a, gate, w, scale, rstd):
     """The norm site's backward: (dx, da or None, d_gate or None, d_w, d_shift, d_scale), the column sums fp32."""
-    dx, da, dg, dw, dsh, dsc = res_mod_rmsnorm_bwd(dh, dxn if a is not None else None, xs, a, gate, w, scale, rstd)
+    dx, da, dg, dw, dsh, dsc = L.call(res_mod_rmsnorm_bwd, dh, dxn if a is not None else None, xs, a, gate, w, scale,
+                                      rstd)
     if a is None:
         return dx, None, None, dw, dsh, dsc
     return dx, da, dg, dw, dsh, dsc
@@ -164,7 +165,7 @@ class _ResModRMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, a, gate, w, shift, scale, eps, has_res):
         _check_bwd_width(x.shape[-1], ctx)
-        xn, h, _, _, rstd = res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, has_res, True, False)
+        xn, h, _, _, rstd = L.call(res_mod_rmsnorm_q, x, a, gate, w, shift, scale, eps, has_res, True, False)
         ctx.has_res = has_res
         ctx.save_for_backward(xn if has_res else x, a if has_res else None, gate if has_res else None, w, shift, scale,
                               rstd)
@@ -207,10 +208,10 @@ class _Fp8ModRMSNormLinear(torch.autograd.Function):
     def forward(ctx, x, w_norm, shift, scale, eps, weight, bias):
         B, N, C = x.shape
         _check_bwd_width(C, ctx)
-        _, _, hq, sh, rstd = res_mod_rmsnorm_q(x, x, x, w_norm, shift, scale, eps, False, False)
+        _, _, hq, sh, rstd = L.call(res_mod_rmsnorm_q, x, x, x, w_norm, shift, scale, eps, False, False)
         hq2 = hq.view(B * N, C)
-        wq, wqt, sw = tcast_t(weight)
-        y = fp8_gemm(hq2, sh, wq, sw, None if bias is None else bias.to(torch.bfloat16))
+        wq, wqt, sw = L.call(tcast_t, weight)
+        y = L.call(fp8_gemm, hq2, sh, wq, sw, None if bias is None else bias.to(torch.bfloat16))
         ctx.save_for_backward(x, w_norm, shift, scale, rstd, hq2, sh, wqt, sw)
         ctx.has_b, ctx.wdt = bias is not None, weight.dtype
         return y.view(B, N, weight.shape[0])
@@ -220,9 +221,9 @@ class _Fp8ModRMSNormLinear(torch.autograd.Function):
         x, w_norm, shift, scale, rstd, hq2, sh, wqt, sw = ctx.saved_tensors
         B, N, C = x.shape
         dy2 = dy.reshape(B * N, -1).to(torch.bfloat16)
-        dyq, sdy = tcast(dy2)
-        dh = fp8_gemm(dyq, sdy, wqt, sw, None, False).view(B, N, C)
-        dweight = fp8_gemm_mn(dyq, sdy, hq2, sh).to(ctx.wdt)
+        dyq, sdy = L.call(tcast, dy2)
+        dh = L.call(fp8_gemm, dyq, sdy, wqt, sw, None, False).view(B, N, C)
+        dweight = L.call(fp8_gemm_mn, dyq, sdy, hq2, sh).to(ctx.wdt)
         db = dy2.sum(0).to(ctx.wdt) if ctx.has_b else None
         dx, _, _, dw, dsh, dsc = _norm_backward(dh, None, x, None, None, w_norm, scale, rstd)
         _, dw, dshift, dscale = _param_grads(B, C, None, dw, dsh, dsc, None, w_norm, shift, scale)
@@ -237,13 +238,13 @@ class _Fp8ResModRMSNormMLP(torch.autograd.Function):
     def forward(ctx, x, a, gate, w_norm, shift, scale, eps, w12, w3):
         B, N, C = x.shape
         _check_bwd_width(C, ctx)
-        xn, _, hq, sh, rstd = res_mod_rmsnorm_q(x, a, gate, w_norm, shift, scale, eps, True, False)
+        xn, _, hq, sh, rstd = L.call(res_mod_rmsnorm_q, x, a, gate, w_norm, shift, scale, eps, True, False)
         hq2 = hq.view(B * N, C)
-        w12q, w12qt, s12 = tcast_t(w12)
-        z = fp8_gemm(hq2, sh, w12q, s12)
-        aq, sa = swiglu_tcast(z)
-        w3q, w3qt, s3 = tcast_t(w3)
-        y = fp8_gemm(aq, sa, w3q, s3)
+        w12q, w12qt, s12 = L.call(tcast_t, w12)
+        z = L.call(fp8_gemm, hq2, sh, w12q, s12)
+        aq, sa = L.call(swiglu_tcast, z)
+        w3q, w3qt, s3 = L.call(tcast_t, w3)
+        y = L.call(fp8_gemm, aq, sa, w3q, s3)
         ctx.save_for_backward(xn, a, gate, w_norm, shift, scale, rstd, hq2, sh, z, aq, sa, w12qt, s12, w3qt, s3)
         ctx.dt = (w12.dtype, w3.dtype)
         return xn, y.view(B, N, w3.shape[0])
@@ -253,12 +254,12 @@ class _Fp8ResModRMSNormMLP(torch.autograd.Function):
         xn, a, gate, w_norm, shift, scale, rstd, hq2, sh, z, aq, sa, w12qt, s12, w3qt, s3 = ctx.saved_tensors
         B, N, C = xn.shape
         dy2 = dy.reshape(B * N, -1).to(torch.bfloat16)
-        dyq, sdy = tcast(dy2)
-        da_ = fp8_gemm(dyq, sdy, w3qt, s3, None, False)
-        dw3 = fp8_gemm_mn(dyq, sdy, aq, sa)
-        dzq, sdz = swiglu_bwd_q(z, da_)
-        dh = fp8_gemm(dzq, sdz, w12qt, s12, None, False).view(B, N, C)
-        dw12 = fp8_gemm_mn(dzq, sdz, hq2, sh)
+        dyq, sdy = L.call(tcast, dy2)
+        da_ = L.call(fp8_gemm, dyq, sdy, w3qt, s3, None, False)
+        dw3 = L.call(fp8_gemm_mn, dyq, sdy, aq, sa)
+        dzq, sdz = L.call(swiglu_bwd_q, z, da_)
+        dh = L.call(fp8_gemm, dzq, sdz, w12qt, s12, None, False).view(B, N, C)
+        dw12 = L.call(fp8_gemm_mn, dzq, sdz, hq2, sh)
         dx, da, dg, dw, dsh, dsc = _norm_backward(dh, dxn, xn, a, gate, w_norm, scale, rstd)
         dgate, dw, dshift, dscale = _param_grads(B, C, dg, dw, dsh, dsc, gate, w_norm, shift, scale)
         return dx, da, dgate, dw, dshift, dscale, None, dw12.to(ctx.dt[0]), dw3.to(ctx.dt[1])
