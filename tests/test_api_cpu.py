@@ -359,3 +359,21 @@ def test_convert_fused_heads(monkeypatch):
     assert g["nn"] is AB.nn and g["attention"] is not AB.attention
     monkeypatch.setattr(AB, "_gpic_probe", 5, raising=False)
     assert g["_gpic_probe"] == 5                                                 # module globals read live
+
+
+def test_eager_calls_skip_the_dispatcher(monkeypatch):
+    """The path's own calls (L.call) run an op's function directly in eager mode and the registered custom op while
+    torch.compile traces; every op of the package is registered for it; any other callable is called as it is."""
+    from gpic_fp8 import _lib as L
+    from gpic_fp8 import norm as NM
+    ops = [F.tcast, F.tcast_t, F.tcast_heads, F.tcast_t_group, F.swiglu_tcast, F.swiglu_tcast_t, F.swiglu_bwd,
+           F.swiglu_bwd_q, F.swiglu_bwd_t, F.fp8_gemm, F.fp8_gemm_mn, NM.res_mod_rmsnorm_q, NM.res_mod_rmsnorm_bwd]
+    assert all(op in L._IMPL for op in ops) and len(L._IMPL) == len(ops)
+    seen = []
+    monkeypatch.setitem(L._IMPL, F.tcast, lambda x: seen.append("direct") or "direct")
+    x = torch.randn(4, 16)
+    assert L.call(F.tcast, x) == "direct"
+    monkeypatch.setattr(torch.compiler, "is_compiling", lambda: True)
+    with pytest.raises(RuntimeError, match="GPU only"):     # the registered op (its kernel refuses CPU tensors)
+        L.call(F.tcast, x)
+    assert L.call(lambda t: "stand-in", x) == "stand-in" and seen == ["direct"]
