@@ -655,7 +655,8 @@ def fp8_linear_f8(x, w, b=None, wcast=None):
     tcast_t(w) would give, cast beforehand with the block's other weights), else w is cast here. A wcast must come
     from w's current values: cast again after every update of w (an optimizer step). A WeightCast (weight_casts)
     that was cast from another tensor or before w's last in-place update is refused; of a plain tuple only the
-    shapes are checked."""
+    shapes are checked. The check reads w's version counter, which in-place ops on w advance (torch.optim's updates,
+    made under no_grad); writes through w.data do not (w.data has a counter of its own), so cast again after those."""
     with torch.autocast("cuda", enabled=False):
         return _Fp8LinearF8.apply(x.to(torch.bfloat16), w, b, _check_cast("wcast", w, wcast))
 
