@@ -5,6 +5,7 @@ There is no CPU path: a missing library, a CPU tensor or a failed launch raises 
 torch is imported before the library is opened, so libgpic_fp8.so binds to the HIP runtime torch already loaded
 (both are SONAME libamdhip64.so.7): torch's stream handles and device pointers are valid in our calls.
 """
+import contextlib
 import ctypes
 import os
 import threading
@@ -97,8 +98,26 @@ def require_gpu(*tensors):
             raise RuntimeError(f"gpic_fp8 runs on the GPU only (HIP kernels); got a tensor on {t.device}")
 
 
+# The current stream's raw handle without building a torch.cuda.Stream object (~1.5 us less host time per call)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _index(device):
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def stream_ptr(device):
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle (hipStream_t) of `device`'s current stream."""
+    index = _index(device)
+    return _raw_stream(index) if _raw_stream is not None else torch.cuda.current_stream(index).cuda_stream
+
+
+def on_device(device):
+    """`device` made current for the calls inside, as torch.cuda.device(device) does, skipping the two device switches
+    when it already is (the common case)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def ptr(t):
@@ -150,6 +169,17 @@ def _new_workspace(index, nbytes):
     return out["ws"]
 
 
+_GEMM_WS = {}   # (device index, M, N, K) -> gpic_fp8_gemm_workspace_bytes (the plan is fixed per device and shape)
+
+
+def gemm_workspace_bytes(device, M, N, K):
+    key = (_index(device), M, N, K)
+    n = _GEMM_WS.get(key)
+    if n is None:
+        n = _GEMM_WS[key] = lib().gpic_fp8_gemm_workspace_bytes(M, N, K)
+    return n
+
+
 def cast_workspace(device):
     """The cast workspace of `device`'s current stream: partial maxima, the SwiGLU sigmoid table and the single-pass
     casts' tagged partials with their call counter (an epoch word the kernels advance on the device). Created once per
@@ -158,8 +188,8 @@ def cast_workspace(device):
     capture the fill is part of the graph (clearing it again on every replay, which the epoch scheme allows) and no
     memset node is recorded."""
     device = torch.device(device)
-    index = device.index if device.index is not None else torch.cuda.current_device()
-    key = (index, torch.cuda.current_stream(index).cuda_stream)
+    index = _index(device)
+    key = (index, stream_ptr(device))
     ws = _WORKSPACES.get(key)
     if ws is None:
         ws = _new_workspace(index, lib().gpic_fp8_cast_workspace_bytes())

@@ -61,7 +61,7 @@ def tcast(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     xc = _prep(x)
     q = torch.empty(x.shape, dtype=E4, device=x.device)
     s = torch.empty(1, dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with L.on_device(x.device):
         ws = L.cast_workspace(x.device)
         L.check(L.lib().gpic_fp8_tcast(xc.data_ptr(), L.DTYPE_CODE[xc.dtype], xc.numel(), q.data_ptr(), s.data_ptr(),
                                        ws.data_ptr(), L.stream_ptr(x.device)), "gpic_fp8_tcast")
@@ -86,7 +86,7 @@ def tcast_t(x: torch.Tensor, want_q: bool = True) -> tuple[torch.Tensor, torch.T
     q = torch.empty((R, C) if want_q else (0,), dtype=E4, device=x.device)
     qt = torch.empty(C, _r16(R), dtype=E4, device=x.device)
     s = torch.empty(1, dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with L.on_device(x.device):
         ws = L.cast_workspace(x.device)
         L.check(L.lib().gpic_fp8_tcast_t(xc.data_ptr(), L.DTYPE_CODE[xc.dtype], R, C, q.data_ptr() if want_q else None,
                                          qt.data_ptr(), qt.shape[1], s.data_ptr(), ws.data_ptr(),
@@ -122,7 +122,7 @@ def tcast_heads(o: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         st = [0 if e == 1 else s for e, s in zip(o.shape, o.stride())]
     q = torch.empty(B, N, H * D, dtype=E4, device=o.device)
     s = torch.empty(1, dtype=torch.float32, device=o.device)
-    with torch.cuda.device(o.device):
+    with L.on_device(o.device):
         ws = L.cast_workspace(o.device)
         L.check(L.lib().gpic_fp8_tcast_heads(o.data_ptr() if o.numel() else None, B, H, N, D, st[0], st[1], st[2],
                                              q.data_ptr() if o.numel() else None, s.data_ptr(), ws.data_ptr(),
@@ -162,7 +162,7 @@ def tcast_t_group(xs: list[torch.Tensor]) -> list[torch.Tensor]:
                 torch.empty(1, dtype=torch.float32, device=dev)]
     n = len(xc)
     arr = lambda t, v: (t * n)(*v)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         ws = L.cast_workspace(dev)
         L.check(L.lib().gpic_fp8_tcast_t_group(
             n, arr(ctypes.c_void_p, [x.data_ptr() for x in xc]), L.DTYPE_CODE[xc[0].dtype],
@@ -223,7 +223,7 @@ def swiglu_tcast(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     q = torch.empty(M, H, dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
     a = torch.empty(M, H, dtype=torch.bfloat16, device=z.device)
-    with torch.cuda.device(z.device):
+    with L.on_device(z.device):
         ws = L.cast_workspace(z.device)
         L.check(L.lib().gpic_fp8_swiglu_tcast_t(zc.data_ptr(), M, H, zc.stride(0), a.data_ptr(), q.data_ptr(),
                                                 q.stride(0), None, 0, s.data_ptr(), ws.data_ptr(),
@@ -250,7 +250,7 @@ def swiglu_tcast_t(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.T
     s = torch.empty(1, dtype=torch.float32, device=z.device)
     # the product a goes through HBM once (written by the amax pass, read by the cast) instead of being recomputed
     a = torch.empty(M, H, dtype=torch.bfloat16, device=z.device)
-    with torch.cuda.device(z.device):
+    with L.on_device(z.device):
         ws = L.cast_workspace(z.device)
         L.check(L.lib().gpic_fp8_swiglu_tcast_t(zc.data_ptr(), M, H, zc.stride(0), a.data_ptr(), q.data_ptr(),
                                                 q.stride(0), qt.data_ptr(), qt.shape[1], s.data_ptr(), ws.data_ptr(),
@@ -280,7 +280,7 @@ def _swiglu_bwd(z, da, want_dz):
     dz = torch.empty(M, H2, dtype=torch.bfloat16, device=z.device) if want_dz else None
     dq = torch.empty(M, H2, dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
-    with torch.cuda.device(z.device):
+    with L.on_device(z.device):
         ws = L.cast_workspace(z.device)
         L.check(L.lib().gpic_fp8_swiglu_bwd(zc.data_ptr(), dac.data_ptr(), M, H2 // 2, zc.stride(0), dac.stride(0),
                                             L.ptr(dz), dq.data_ptr(), s.data_ptr(), ws.data_ptr(),
@@ -329,7 +329,7 @@ def swiglu_bwd_t(z: torch.Tensor, da: torch.Tensor,
     dq = torch.empty(M, H2, dtype=E4, device=z.device)
     dqt = torch.empty(H2, _r16(M), dtype=E4, device=z.device)
     s = torch.empty(1, dtype=torch.float32, device=z.device)
-    with torch.cuda.device(z.device):
+    with L.on_device(z.device):
         ws = L.cast_workspace(z.device)
         L.check(L.lib().gpic_fp8_swiglu_bwd_t(zc.data_ptr(), dac.data_ptr(), M, H2 // 2, zc.stride(0), dac.stride(0),
                                               dz.data_ptr() if want_dz else None, dq.data_ptr(), dqt.data_ptr(),
@@ -371,16 +371,18 @@ def fp8_gemm(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Tenso
         raise ValueError(f"fp8_gemm: a is [{M}, {K}] but b is {tuple(b.shape)}")
     if K % 16 or N % 16:
         raise ValueError(f"fp8_gemm needs K % 16 == 0 and N % 16 == 0, got M={M} N={N} K={K}")
-    sa = sa.to(torch.float32).reshape(1)
-    sb = sb.to(torch.float32).reshape(1)
+    if sa.dtype != torch.float32 or sa.shape != (1,):
+        sa = sa.to(torch.float32).reshape(1)
+    if sb.dtype != torch.float32 or sb.shape != (1,):
+        sb = sb.to(torch.float32).reshape(1)
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
         if bias.numel() != N:
             raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
         bias = bias if bias.data_ptr() % 8 == 0 else bias.clone()
     c = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
-    with torch.cuda.device(a.device):
-        nws = L.lib().gpic_fp8_gemm_workspace_bytes(M, N, K)
+    with L.on_device(a.device):
+        nws = L.gemm_workspace_bytes(a.device, M, N, K)
         ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=a.device) if nws else None
         L.check(L.lib().gpic_fp8_gemm(a.data_ptr(), a.stride(0), sa.data_ptr(), b.data_ptr(), b.stride(0),
                                       sb.data_ptr(), L.ptr(bias), c.data_ptr(), c.stride(0), M, N, K, int(fast),
@@ -427,16 +429,18 @@ def fp8_gemm_mn(a: torch.Tensor, sa: torch.Tensor, b: torch.Tensor, sb: torch.Te
             u[:, :K] = t.view(torch.uint8).t()
             return u.view(E4)
         return L.call(fp8_gemm, kmajor(a), sa, kmajor(b), sb, bias, False)
-    sa = sa.to(torch.float32).reshape(1)
-    sb = sb.to(torch.float32).reshape(1)
+    if sa.dtype != torch.float32 or sa.shape != (1,):
+        sa = sa.to(torch.float32).reshape(1)
+    if sb.dtype != torch.float32 or sb.shape != (1,):
+        sb = sb.to(torch.float32).reshape(1)
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
         if bias.numel() != N:
             raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
         bias = bias if bias.data_ptr() % 8 == 0 else bias.clone()
     c = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
-    with torch.cuda.device(a.device):
-        nws = L.lib().gpic_fp8_gemm_workspace_bytes(M, N, K)
+    with L.on_device(a.device):
+        nws = L.gemm_workspace_bytes(a.device, M, N, K)
         ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=a.device) if nws else None
         L.check(L.lib().gpic_fp8_gemm_mn(a.data_ptr(), a.stride(0), sa.data_ptr(), b.data_ptr(), b.stride(0),
                                          sb.data_ptr(), L.ptr(bias), c.data_ptr(), c.stride(0), M, N, K,

@@ -79,7 +79,7 @@ def res_mod_rmsnorm_q(x: torch.Tensor, a: torch.Tensor, gate: torch.Tensor, w: t
     hq = torch.empty((B, N, C) if want_q else (0,), dtype=E4, device=dev)
     s = torch.empty(1 if want_q else 0, dtype=torch.float32, device=dev)
     rstd = torch.empty(B * N, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         ws = L.cast_workspace(dev)
         L.check(L.lib().gpic_fp8_res_mod_rmsnorm(
             xc.data_ptr(), L.ptr(ac), L.ptr(g), g.stride(0) if has_res else 0, wf.data_ptr(), sh.data_ptr(),
@@ -125,7 +125,7 @@ def res_mod_rmsnorm_bwd(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch
         return dx, da, (z.clone() if res else torch.empty(0, **f32)), torch.zeros(C, **f32), z.clone(), z.clone()
     dg = torch.empty(B, C, **f32) if res else torch.empty(0, **f32)
     dw, dsh, dsc = torch.empty(C, **f32), torch.empty(B, C, **f32), torch.empty(B, C, **f32)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         nws = L.lib().gpic_fp8_res_mod_rmsnorm_bwd_workspace_bytes(B * N, max(N, 1), C)
         ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=dev)
         L.check(L.lib().gpic_fp8_res_mod_rmsnorm_bwd(
