@@ -11,7 +11,8 @@ forward runs unchanged: the converter rebinds only the name `attention` it calls
 torch.nn.functional.scaled_dot_product_attention under that name, attention_op.py:4), to a wrapper whose result keeps
 the transpose and the reshape pending (_PendingHeads) until proj takes them. Any other use of that result gives the
 tensor eager code would have had, so a forward that does something else with it computes what it always did.
-Eager mode only (the pending object is not a tensor for torch.compile to trace)."""
+The pending result exists in eager mode only: while torch.compile traces the forward, the wrapper returns the
+attention output itself, so a compiled model takes the head-merging copy and the plain phase-3 proj."""
 import builtins
 import types
 
@@ -104,7 +105,10 @@ class Fp8HeadsLinearF8(Fp8LinearF8):
 def _pending_attention(real):
     def attention(q, k, v, *args, **kwargs):
         o = real(q, k, v, *args, **kwargs)
-        if isinstance(o, torch.Tensor) and o.dim() == 4 and o.shape[3] % 16 == 0:
+        # (while torch.compile traces, the output as it is: the forward then computes what it always did, through the
+        # plain FP8 linear)
+        if (isinstance(o, torch.Tensor) and o.dim() == 4 and o.shape[3] % 16 == 0 and
+                not torch.compiler.is_compiling()):
             return _PendingHeads(o, 0)
         return o
     return attention

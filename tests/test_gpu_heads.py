@@ -195,3 +195,23 @@ def test_deep_copy_of_a_converted_model_runs_its_own_modules(dev):
         y2, y3 = net(x, c), twin(x, c)
     assert torch.equal(y2.view(torch.int16), y0.view(torch.int16)) and not torch.equal(y3, y0)
     assert all(b.attn.proj.heads_calls == 2 for b in twin.blocks)
+
+
+def test_compiled_converted_model_runs(dev):
+    """torch.compile of a native3+fused model (as the reference compiles its blocks): the norm sites stay fused (the
+    custom ops are traced opaque), the attention output takes the head-merging copy and the plain phase-3 proj (the
+    pending result exists in eager mode only), and the output and gradients agree with the eager model's within the
+    roundings the compiler may fuse differently (the block's elementwise ops)."""
+    C, heads, B, N = 512, 8, 2, 64
+    net, twin = _nets(C, heads, 2, dev)
+    G.convert_fp8(net, "native3+fused")
+    G.convert_fp8(twin, "native3+fused")
+    comp = torch.compile(twin)
+    x = torch.randn(B, N, C, device=dev).to(torch.bfloat16)
+    c = torch.randn(B, 1, C, device=dev).to(torch.bfloat16)
+    re, rc = _run(net, x, c, None), _run(comp, x, c, None)
+    rel = lambda a, b: (torch.linalg.norm(a.float() - b.float()) / torch.linalg.norm(b.float())).item()
+    for a, b in zip(rc, re):
+        assert rel(a, b) < 1e-2
+    assert all(b.attn.proj.heads_calls == 0 for b in twin.blocks)
+    assert all(b.attn.proj.heads_calls == 1 for b in net.blocks)
