@@ -11,8 +11,9 @@ forward runs unchanged: the converter rebinds only the name `attention` it calls
 torch.nn.functional.scaled_dot_product_attention under that name, attention_op.py:4), to a wrapper whose result keeps
 the transpose and the reshape pending (_PendingHeads) until proj takes them. Any other use of that result gives the
 tensor eager code would have had, so a forward that does something else with it computes what it always did.
-The pending result exists in eager mode only: while torch.compile traces the forward, the wrapper returns the
-attention output itself, so a compiled model takes the head-merging copy and the plain phase-3 proj."""
+The route is eager only: while torch.compile traces a converted attention it traces the class's own forward (and
+the wrapper would return the attention output itself), so a compiled model takes the head-merging copy and the plain
+phase-3 proj."""
 import builtins
 import types
 
@@ -136,12 +137,21 @@ def fused_heads_ok(attn):
             proj.in_features % 16 == 0)
 
 
-def _rebind(attn):
-    fwd = type(attn).forward
+def _rebound(cls):
+    """cls.forward with its global name `attention` bound to the pending wrapper."""
+    fwd = cls.forward
     g = _Globals(fwd.__globals__, attention=_pending_attention(SDPA))
     f = types.FunctionType(fwd.__code__, g, fwd.__name__, fwd.__defaults__, fwd.__closure__)
     f.__kwdefaults__ = fwd.__kwdefaults__
-    return types.MethodType(f, attn)
+    return f
+
+
+def _heads_forward(attn, *args, **kwargs):
+    """A converted attention's forward: in eager mode its class's forward with `attention` rebound; while
+    torch.compile traces, its class's forward itself (the tracer is given the function with the module's own globals)."""
+    if torch.compiler.is_compiling():
+        return type(attn).forward(attn, *args, **kwargs)
+    return attn._gpic_forward(attn, *args, **kwargs)
 
 
 def convert_fused_heads(net):
@@ -154,7 +164,8 @@ def convert_fused_heads(net):
         if attn is None or getattr(attn, "_gpic_fused_heads", False) or not fused_heads_ok(attn):
             continue
         attn.proj.__class__ = Fp8HeadsLinearF8
-        attn.forward = _rebind(attn)
+        attn._gpic_forward = _rebound(type(attn))
+        attn.forward = types.MethodType(_heads_forward, attn)
         attn._gpic_fused_heads = True
         n += 1
     return n

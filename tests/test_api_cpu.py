@@ -355,7 +355,7 @@ def test_convert_fused_heads(monkeypatch):
     for b, r in zip(net.blocks, ref.blocks):
         assert torch.allclose(b.attn(x, None, None), r.attn(x, None, None), rtol=1e-6, atol=1e-6)
     assert seen == [(3, 2, 7, 16)] * 2 and [b.attn.proj.heads_calls for b in net.blocks] == [1, 1]
-    g = net.blocks[0].attn.forward.__func__.__globals__
+    g = net.blocks[0].attn._gpic_forward.__globals__
     assert g["nn"] is AB.nn and g["attention"] is not AB.attention
     monkeypatch.setattr(AB, "_gpic_probe", 5, raising=False)
     assert g["_gpic_probe"] == 5                                                 # module globals read live
