@@ -10,7 +10,7 @@ from .fp8_native import (E4, FMAX, TINY, Fp8Linear, Fp8LinearF8, convert_native,
 from .fp8 import KEEP, convert_fp8, fp8_filter
 from .heads import Fp8HeadsLinearF8, convert_fused_heads
 from .norm import (Fp8NormLinearF8, convert_fused_norm, fp8_mod_rmsnorm_linear, fp8_res_mod_rmsnorm_mlp,
-                   mod_rmsnorm, res_mod_rmsnorm, res_mod_rmsnorm_q)
+                   mod_rmsnorm, res_mod_rmsnorm, res_mod_rmsnorm_bwd, res_mod_rmsnorm_fwd, res_mod_rmsnorm_q)
 from .norm import reference as norm_reference
 
 __all__ = ["E4", "FMAX", "TINY", "Fp8Linear", "Fp8LinearF8", "convert_native", "convert_fp8", "fp8_filter", "KEEP",
@@ -19,4 +19,4 @@ __all__ = ["E4", "FMAX", "TINY", "Fp8Linear", "Fp8LinearF8", "convert_native", "
            "weight_casts", "_mm",
            "mod_rmsnorm", "res_mod_rmsnorm", "res_mod_rmsnorm_q", "norm_reference", "fp8_mod_rmsnorm_linear",
            "fp8_res_mod_rmsnorm_mlp", "Fp8NormLinearF8", "convert_fused_norm", "tcast_heads", "fp8_heads_linear_f8",
-           "Fp8HeadsLinearF8", "convert_fused_heads"]
+           "Fp8HeadsLinearF8", "convert_fused_heads", "res_mod_rmsnorm_fwd", "res_mod_rmsnorm_bwd"]

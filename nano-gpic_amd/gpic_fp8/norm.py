@@ -9,14 +9,15 @@ The reference computes h in bf16 and its FP8 linear then reads h again for the a
 (fp8_native.py:3-6 names these separate passes as why FP8 lost end to end). Here one kernel writes h's tensorwise
 e4m3 bytes and scale directly, and h itself only when asked. Functions:
 
-- mod_rmsnorm / res_mod_rmsnorm / reference: the reference's API (fused_norm.py:293-313) with bf16 h, on the kernel;
+- mod_rmsnorm / res_mod_rmsnorm / reference: the reference's API (fused_norm.py:293-313) with bf16 h, on the kernel,
+  and its ops under their names and schemas: gpic::res_mod_rmsnorm_fwd (differentiable) and gpic::res_mod_rmsnorm_bwd;
 - fp8_mod_rmsnorm_linear(x, w_norm, shift, scale, eps, weight, bias): site 1 feeding a phase-3 FP8 linear (qkv_x);
 - fp8_res_mod_rmsnorm_mlp(x, a, gate, w_norm, shift, scale, eps, w12, w3): site 2 feeding the phase-3 FP8 SwiGLU MLP,
   returning (x_new, mlp output);
 - convert_fused_norm(net) (convert_native(..., fused_norm=True), recipes "native3+norm", "native3+text+norm"): the
   image blocks' forward routed through the two fused consumers, so a converted model takes the fused path.
 
-The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel (res_mod_rmsnorm_bwd);
+The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel (res_mod_rmsnorm_bwd_k);
 the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
 """
 import types
@@ -99,7 +100,7 @@ def _(x, a, gate, w, shift, scale, eps, has_res, want_h, want_q=True):
 
 
 @L.custom_op("gpic::fp8_res_mod_rmsnorm_bwd")
-def res_mod_rmsnorm_bwd(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch.Tensor, a: Optional[torch.Tensor],
+def res_mod_rmsnorm_bwd_k(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch.Tensor, a: Optional[torch.Tensor],
                         gate: Optional[torch.Tensor], w: torch.Tensor, scale: torch.Tensor, rstd: torch.Tensor
                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """The norm site's backward (fused_norm.py:94-147, op :249-275) on the HIP kernel: dh [B, N, C] (the gradient of
@@ -136,7 +137,7 @@ def res_mod_rmsnorm_bwd(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch
     return dx, da, dg, dw, dsh, dsc
 
 
-@res_mod_rmsnorm_bwd.register_fake
+@res_mod_rmsnorm_bwd_k.register_fake
 def _(dh, dxn, xs, a, gate, w, scale, rstd):
     B, N, C = xs.shape
     res = a is not None
@@ -148,8 +149,8 @@ def _(dh, dxn, xs, a, gate, w, scale, rstd):
 
 def _norm_backward(dh, dxn, xs, a, gate, w, scale, rstd):
     """The norm site's backward: (dx, da or None, d_gate or None, d_w, d_shift, d_scale), the column sums fp32."""
-    dx, da, dg, dw, dsh, dsc = L.call(res_mod_rmsnorm_bwd, dh, dxn if a is not None else None, xs, a, gate, w, scale,
-                                      rstd)
+    dx, da, dg, dw, dsh, dsc = L.call(res_mod_rmsnorm_bwd_k, dh, dxn if a is not None else None, xs, a, gate, w,
+                                      scale, rstd)
     if a is None:
         return dx, None, None, dw, dsh, dsc
     return dx, da, dg, dw, dsh, dsc
@@ -158,6 +159,71 @@ def _norm_backward(dh, dxn, xs, a, gate, w, scale, rstd):
 def _param_grads(B, C, dg, dw, dsh, dsc, gate, w, shift, scale):
     vec = lambda v, like: None if v is None else v.to(like.dtype).view(B, 1, C).reshape(like.shape)
     return vec(dg, gate) if gate is not None else None, dw.to(w.dtype), vec(dsh, shift), vec(dsc, scale)
+
+
+# ------------------------------------------------------------------ the reference's op names and schemas
+
+@L.custom_op("gpic::res_mod_rmsnorm_fwd")
+def res_mod_rmsnorm_fwd(x: torch.Tensor, a: torch.Tensor, gate: torch.Tensor, w: torch.Tensor, shift: torch.Tensor,
+                        scale: torch.Tensor, eps: float, has_res: bool
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The reference's op (fused_norm.py:151-171) on the HIP kernel: (x_new, or an empty tensor without the residual;
+    h [B, N, C] bf16; rstd [B * N] fp32). Differentiable (its backward is res_mod_rmsnorm_bwd, as the reference
+    registers it, :224-245). mod_rmsnorm / res_mod_rmsnorm below take the autograd Function instead, which refuses a
+    gradient at C > 2048 before the forward runs."""
+    xn, h, _, _, rstd = L.call(res_mod_rmsnorm_q, x, a, gate, w, shift, scale, eps, has_res, True, False)
+    return xn, h, rstd
+
+
+@res_mod_rmsnorm_fwd.register_fake
+def _(x, a, gate, w, shift, scale, eps, has_res):
+    B, N, C = x.shape
+    return (torch.empty_like(x) if has_res else x.new_empty(0), torch.empty_like(x),
+            x.new_empty(B * N, dtype=torch.float32))
+
+
+@L.custom_op("gpic::res_mod_rmsnorm_bwd")
+def res_mod_rmsnorm_bwd(dh: torch.Tensor, dxn: torch.Tensor, xn: torch.Tensor, a: torch.Tensor, gate: torch.Tensor,
+                        w: torch.Tensor, scale: torch.Tensor, rstd: torch.Tensor, has_res: bool, has_dxn: bool
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The reference's op (fused_norm.py:180-212) on the HIP kernel, with its argument meaning: xn is x_new (has_res)
+    or x; a, gate (and dxn unless has_dxn) are ignored without the residual. Returns dx, da, d_gate [B, C], d_w [C],
+    d_shift [B, C], d_scale [B, C] (fp32 column sums; da and d_gate empty without the residual)."""
+    dx, da, dg, dw, dsh, dsc = L.call(res_mod_rmsnorm_bwd_k, dh, dxn if (has_res and has_dxn) else None, xn,
+                                      a if has_res else None, gate if has_res else None, w, scale, rstd)
+    return dx, da, dg, dw, dsh, dsc
+
+
+@res_mod_rmsnorm_bwd.register_fake
+def _(dh, dxn, xn, a, gate, w, scale, rstd, has_res, has_dxn):
+    B, N, C = xn.shape
+    f32 = dict(dtype=torch.float32)
+    return (torch.empty_like(xn), torch.empty_like(xn) if has_res else xn.new_empty(0),
+            xn.new_empty((B, C) if has_res else (0,), **f32), xn.new_empty(C, **f32), xn.new_empty(B, C, **f32),
+            xn.new_empty(B, C, **f32))
+
+
+def _fwd_setup(ctx, inputs, output):
+    x, a, gate, w, shift, scale, eps, has_res = inputs
+    xn, h, rstd = output
+    ctx.has_res = has_res
+    ctx.save_for_backward(xn if has_res else x, a if has_res else None, gate if has_res else None, w, shift, scale,
+                          rstd)
+
+
+def _fwd_backward(ctx, dxn, dh, drstd):
+    xs, a, gate, w, shift, scale, rstd = ctx.saved_tensors
+    B, _, C = xs.shape
+    if C > BWD_MAX_C:
+        raise ValueError(f"the norm's backward kernel takes rows of at most {BWD_MAX_C} elements, got C = {C}")
+    has_dxn = ctx.has_res and dxn is not None
+    dx, da, dg, dw, dsh, dsc = L.call(res_mod_rmsnorm_bwd, dh, dxn if has_dxn else dh, xs, a if ctx.has_res else xs,
+                                      gate if ctx.has_res else w, w, scale, rstd, ctx.has_res, has_dxn)
+    dgate, dw, dshift, dscale = _param_grads(B, C, dg if ctx.has_res else None, dw, dsh, dsc, gate, w, shift, scale)
+    return (dx, da if ctx.has_res else None, dgate, dw, dshift, dscale, None, None)
+
+
+res_mod_rmsnorm_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup)
 
 
 class _ResModRMSNorm(torch.autograd.Function):

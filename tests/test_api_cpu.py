@@ -367,7 +367,8 @@ def test_eager_calls_skip_the_dispatcher(monkeypatch):
     from gpic_fp8 import _lib as L
     from gpic_fp8 import norm as NM
     ops = [F.tcast, F.tcast_t, F.tcast_heads, F.tcast_t_group, F.swiglu_tcast, F.swiglu_tcast_t, F.swiglu_bwd,
-           F.swiglu_bwd_q, F.swiglu_bwd_t, F.fp8_gemm, F.fp8_gemm_mn, NM.res_mod_rmsnorm_q, NM.res_mod_rmsnorm_bwd]
+           F.swiglu_bwd_q, F.swiglu_bwd_t, F.fp8_gemm, F.fp8_gemm_mn, NM.res_mod_rmsnorm_q, NM.res_mod_rmsnorm_bwd_k,
+           NM.res_mod_rmsnorm_fwd, NM.res_mod_rmsnorm_bwd]
     assert all(op in L._IMPL for op in ops) and len(L._IMPL) == len(ops)
     seen = []
     monkeypatch.setitem(L._IMPL, F.tcast, lambda x: seen.append("direct") or "direct")
@@ -377,3 +378,15 @@ def test_eager_calls_skip_the_dispatcher(monkeypatch):
     with pytest.raises(RuntimeError, match="GPU only"):     # the registered op (its kernel refuses CPU tensors)
         L.call(F.tcast, x)
     assert L.call(lambda t: "stand-in", x) == "stand-in" and seen == ["direct"]
+
+
+def test_reference_norm_op_schemas():
+    """The reference's norm ops exist under its names with its schemas (fused_norm.py:151-153,180-183), beside this
+    build's own (the cast folded in)."""
+    fwd = str(torch.ops.gpic.res_mod_rmsnorm_fwd.default._schema)
+    bwd = str(torch.ops.gpic.res_mod_rmsnorm_bwd.default._schema)
+    assert fwd.startswith("gpic::res_mod_rmsnorm_fwd(Tensor x, Tensor a, Tensor gate, Tensor w, Tensor shift, "
+                          "Tensor scale, float eps, bool has_res) -> (Tensor, Tensor, Tensor)"), fwd
+    assert bwd.startswith("gpic::res_mod_rmsnorm_bwd(Tensor dh, Tensor dxn, Tensor xn, Tensor a, Tensor gate, Tensor w, "
+                          "Tensor scale, Tensor rstd, bool has_res, bool has_dxn) -> (Tensor, Tensor, Tensor, Tensor, "
+                          "Tensor, Tensor)"), bwd

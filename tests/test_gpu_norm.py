@@ -157,6 +157,44 @@ def test_drop_in_api_and_backward(dev, res):
         assert r < 1e-2, (n, r)
 
 
+@pytest.mark.parametrize("C", [896, 1024])
+@pytest.mark.parametrize("res", [False, True])
+def test_reference_named_ops(dev, res, C):
+    """torch.ops.gpic.res_mod_rmsnorm_fwd / _bwd (the reference's op names and schemas, fused_norm.py:151-245): the
+    forward's outputs equal the kernel op's bit for bit, its registered backward gives the same gradients as
+    mod_rmsnorm / res_mod_rmsnorm bit for bit, and the backward op equals the kernel's backward op."""
+    from gpic_fp8 import norm as NM
+    B, N, eps = 4, 128, 1e-6
+    x, a, gate, w, shift, scale = inputs(B, N, C, 29 + res + C, dev, res)
+    xn, h, rstd = torch.ops.gpic.res_mod_rmsnorm_fwd(x, a, gate, w, shift, scale, eps, res)
+    xn1, h1, _, _, r1 = G.res_mod_rmsnorm_q(x, a, gate, w, shift, scale, eps, res, True, False)
+    assert torch.equal(h.view(torch.int16), h1.view(torch.int16)) and torch.equal(rstd.view(torch.int32), r1.view(torch.int32))
+    assert (xn.numel() == 0) if not res else torch.equal(xn.view(torch.int16), xn1.view(torch.int16))
+    dh = (torch.randn_like(h) * 0.1).to(torch.bfloat16)
+    dxn = (torch.randn_like(h) * 0.1).to(torch.bfloat16)
+    grads = []
+    for via_op in (True, False):
+        leaves = [t.detach().clone().requires_grad_() for t in (x, a, gate, w, shift, scale)]
+        xl, al, gl, wl, shl, scl = leaves
+        if via_op:
+            on, oh, _ = torch.ops.gpic.res_mod_rmsnorm_fwd(xl, al if res else xl, gl if res else xl, wl, shl, scl, eps,
+                                                           res)
+        elif res:
+            on, oh = G.res_mod_rmsnorm(xl, al, gl, wl, shl, scl, eps)
+        else:
+            on, oh = None, G.mod_rmsnorm(xl, wl, shl, scl, eps)
+        torch.autograd.backward([oh, on] if res else [oh], [dh, dxn] if res else [dh])
+        grads.append([t.grad for t in (leaves if res else (xl, wl, shl, scl))])
+    for got, want in zip(*grads):
+        assert torch.equal(got, want)
+    xs = xn if res else x
+    out = torch.ops.gpic.res_mod_rmsnorm_bwd(dh, dxn, xs, a, gate, w, scale, rstd, res, res)
+    ref = NM.res_mod_rmsnorm_bwd_k(dh, dxn if res else None, xs, a if res else None, gate if res else None, w, scale,
+                                   rstd)
+    for got, want in zip(out, ref):
+        assert torch.equal(got, want)
+
+
 def test_fused_site1_linear_equals_unfused(dev):
     """fp8_mod_rmsnorm_linear (h cast in the norm, never written in bf16) against mod_rmsnorm then fp8_linear_f8 (h
     written in bf16 and cast by tcast): the same output and gradients bit for bit."""
@@ -253,7 +291,7 @@ def test_backward_kernel(dev, B, N, C, res, dxn):
     dh = (torch.randn(B, N, C, generator=g, device=dev) * 0.1).to(torch.bfloat16)
     dx_up = (torch.randn(B, N, C, generator=g, device=dev) * 0.1).to(torch.bfloat16) if (res and dxn) else None
     args = (dh, dx_up, xs, a if res else None, gate if res else None, w, scale, rstd)
-    out = NM.res_mod_rmsnorm_bwd(*args)
+    out = NM.res_mod_rmsnorm_bwd_k(*args)
     ref = torch_backward(*args)
     dx, da, dg, dwk, dsh, dsc = out
     _close_bf16(dx, ref[0], "dx")
@@ -263,7 +301,7 @@ def test_backward_kernel(dev, B, N, C, res, dxn):
     if res:
         _close_bf16(da, ref[1], "da")
         _close_f32(dg, ref[2], "d_gate")
-    again = NM.res_mod_rmsnorm_bwd(*args)
+    again = NM.res_mod_rmsnorm_bwd_k(*args)
     for u, v in zip(out, again):
         assert torch.equal(u.view(torch.int32) if u.dtype == torch.float32 else u.view(torch.int16),
                            v.view(torch.int32) if v.dtype == torch.float32 else v.view(torch.int16))
@@ -274,7 +312,7 @@ def test_backward_kernel_empty(dev):
     from gpic_fp8 import norm as NM
     x, a, gate, w, shift, scale = inputs(2, 8, 256, 42, dev, True)
     e = x[:, :0]
-    dx, da, dg, dw, dsh, dsc = NM.res_mod_rmsnorm_bwd(e, e, e, e, gate, w, scale,
+    dx, da, dg, dw, dsh, dsc = NM.res_mod_rmsnorm_bwd_k(e, e, e, e, gate, w, scale,
                                                       torch.empty(0, device=dev, dtype=torch.float32))
     assert dx.numel() == 0 and da.numel() == 0 and torch.equal(dw, torch.zeros_like(dw))
     assert not dg.any() and not dsh.any() and not dsc.any() and dg.shape == (2, 256)
