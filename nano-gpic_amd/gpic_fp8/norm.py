@@ -17,8 +17,8 @@ e4m3 bytes and scale directly, and h itself only when asked. Functions:
 - convert_fused_norm(net) (convert_native(..., fused_norm=True), recipes "native3+norm", "native3+text+norm"): the
   image blocks' forward routed through the two fused consumers, so a converted model takes the fused path.
 
-The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel (res_mod_rmsnorm_bwd_k);
-the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
+The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel
+(res_mod_rmsnorm_bwd_k); the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
 """
 import types
 from typing import Optional
@@ -101,8 +101,8 @@ def _(x, a, gate, w, shift, scale, eps, has_res, want_h, want_q=True):
 
 @L.custom_op("gpic::fp8_res_mod_rmsnorm_bwd")
 def res_mod_rmsnorm_bwd_k(dh: torch.Tensor, dxn: Optional[torch.Tensor], xs: torch.Tensor, a: Optional[torch.Tensor],
-                        gate: Optional[torch.Tensor], w: torch.Tensor, scale: torch.Tensor, rstd: torch.Tensor
-                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+                          gate: Optional[torch.Tensor], w: torch.Tensor, scale: torch.Tensor, rstd: torch.Tensor
+                          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """The norm site's backward (fused_norm.py:94-147, op :249-275) on the HIP kernel: dh [B, N, C] (the gradient of
     h), dxn (that of x_new, site 2) or None, xs = x_new (site 2) or x, a and gate (site 2) or None, rstd [B * N].
     Returns dx, da (empty at site 1), d_gate [B, C] (empty at site 1), d_w [C], d_shift [B, C], d_scale [B, C]: fp32
