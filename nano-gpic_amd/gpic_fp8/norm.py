@@ -18,7 +18,8 @@ e4m3 bytes and scale directly, and h itself only when asked. Functions:
   image blocks' forward routed through the two fused consumers, so a converted model takes the fused path.
 
 The backward of the norm is the reference's analytic one (fused_norm.py:94-147) on a HIP kernel
-(res_mod_rmsnorm_bwd_k); the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes kept from the forward.
+(res_mod_rmsnorm_bwd_k); the linears' backward is phase 3's (FP8 dgrad and wgrad), the wgrad reading h's e4m3 bytes
+kept from the forward.
 """
 import types
 from typing import Optional
