@@ -51,6 +51,10 @@ def flash_layout(B, H, N, D, dev, seed, scale=1.0):
     (3, 3, 7, 16),        # odd head and token counts: every division of the source index by a non-power of two
     (2, 5, 33, 128),
     (1, 1, 9, 32),        # extents of 1
+    (48, 16, 512, 64),    # 48 MiB: the 256-thread kernel's limit before the wide one
+    (48, 16, 513, 64),    # just past it: the wide kernel
+    (100, 16, 512, 64),   # 100 MiB: all that the wide kernel holds on 256 CUs
+    (100, 16, 513, 64),   # just past it: a hybrid streaming one group of words twice
 ])
 def test_flash_layout_equals_copy_cast(dev, B, H, N, D):
     """o as scaled_dot_product_attention's flash backend writes it ([B, H, N, D] in memory)."""
