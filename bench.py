@@ -60,7 +60,8 @@ def parse():
                    help="only run each of the 12 GEMM shapes once, in the printed order (one counter row per shape)")
     p.add_argument("--cast-traffic", action="store_true",
                    help="only run the casts once each, in the printed order (one counter row per dispatch): config 2 "
-                        "warm and with L2 / MALL flushed, an fp32 weight-shaped cast, the d12 SwiGLU casts")
+                        "warm and with L2 / MALL flushed, an fp32 weight-shaped cast, the d12 SwiGLU casts, the "
+                        "weights' grouped cast and the attention output's head-merging cast")
     p.add_argument("--step-only", type=int, default=0, metavar="N",
                    help="only run the d12 step N times (for a kernel-by-kernel trace of one step)")
     return p.parse_args()
