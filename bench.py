@@ -223,6 +223,50 @@ def run_gemm(G, op):
     return G.fp8_gemm(aq, sa, bq, sb, None, False)
 
 
+def gemm_sclk(fn, seconds=1.5, samples=3):
+    """The shader clock while fn (one pass of the 12 GEMMs) runs back to back for about `seconds`: `amd-smi metric
+    --clock` read `samples` times from a helper thread after the first 0.3 s, the mean over every XCD's GFX clock and
+    every sample, in MHz. None when amd-smi is missing or its output cannot be read (the figure is then not reported)."""
+    import shutil
+    import subprocess
+    import threading
+    import torch
+    exe = shutil.which("amd-smi")
+    if exe is None:
+        return None
+    idx = torch.cuda.current_device()
+    vals, stop = [], threading.Event()
+
+    def sample():
+        time.sleep(0.3)
+        for _ in range(samples):
+            if stop.is_set():
+                return
+            try:
+                r = subprocess.run([exe, "metric", "-g", str(idx), "--clock", "--json"], capture_output=True, text=True,
+                                   timeout=5)
+                d = json.loads(r.stdout)
+                d = d["gpu_data"][0] if isinstance(d, dict) and "gpu_data" in d else (d[0] if isinstance(d, list) else d)
+                clk = d["clock"]
+                vals.extend(float(v["clk"]["value"]) for k, v in clk.items() if k.startswith("gfx"))
+            except Exception:   # a missing or changed output format: no figure
+                return
+
+    t = threading.Thread(target=sample, daemon=True)
+    t0 = time.perf_counter()
+    t.start()
+    n = 0
+    while (time.perf_counter() - t0 < seconds or t.is_alive()) and n < 100000:
+        fn()
+        n += 1
+        if n % 20 == 0:
+            torch.cuda.synchronize()   # keep the queue short so the clock is read while GEMMs run
+    stop.set()
+    torch.cuda.synchronize()
+    t.join(timeout=15)
+    return round(sum(vals) / len(vals), 1) if vals else None
+
+
 def norm_sites(G, dev, B=128, N=256, eps=1e-6):
     """The two norm sites of a d12 block over one GPU's 32768 tokens: fused (the norm kernel writes h's e4m3 bytes
     and scale; h never exists in bf16) against unfused (the norm writes bf16 h, then tcast reads it), device time, with
@@ -607,6 +651,7 @@ def main():
             run_gemm(G, op)
 
     gemm_ms = time_region(gemms, max(args.steps, 10), 3)
+    sclk = gemm_sclk(gemms)   # after the timed passes: the reading does not touch them
     per_shape = {}
     for (name, m, n, k), op in zip(shapes, ops):
         tm = time_region(lambda: run_gemm(G, op), 10, 2)
@@ -761,7 +806,11 @@ def main():
                      "avg_launch_us": round(gemm_ms * 1e3 / len(shapes), 1), "gemm_ms_per_step": round(gemm_ms, 4),
                      "per_shape": per_shape,
                      "mfma_ceiling": ceiling,
-                     "frac_of_data_ceiling": round(gemm_tflops / ceiling["tcast_randn"]["TFLOPs"], 4) if ceiling else None},
+                     "frac_of_data_ceiling": round(gemm_tflops / ceiling["tcast_randn"]["TFLOPs"], 4) if ceiling else None,
+                     # the same against the peak at the shader clock amd-smi reported while the 12 GEMMs ran
+                     "sclk_mhz_during_gemms": sclk,
+                     "peak_at_sclk": round(PEAK_FP8_TFLOPS * sclk / 2400.0, 1) if sclk else None,
+                     "frac_at_sclk": round(gemm_tflops / (PEAK_FP8_TFLOPS * sclk / 2400.0), 4) if sclk else None},
         "cast": {"workload": "config 2: [32768 x 1024] bf16 -> e4m3 + amax + scale, L2 / MALL flushed before each "
                              "call (a 512 MB write; median of 20); the warm figures are back-to-back calls",
                  "us": round(cast_cold_ms * 1e3, 2), "achieved_GBs": round(cast_bytes / cast_cold_ms / 1e6, 1),
