@@ -371,6 +371,57 @@ def norm_block(G, dev, B=128, N=256, eps=1e-6, steps=20):
             "fused_ms": round(f, 4), "unfused_ms": round(u, 4), "saved_us": round((u - f) * 1e3, 1)}
 
 
+def block_producers(G, dev, B=128, N=256, heads=16, eps=1e-6, steps=10):
+    """A d12 block's lever-K forward + backward over 32768 tokens (JiT_T2I.py:201-207 with the attention of :166-186
+    minus the q / k norms and the rotary embedding): both norm sites, qkv_x, scaled_dot_product_attention (flash
+    backend), proj (with bias), the residual and the SwiGLU MLP, every GEMM FP8. Fused (recipe native3+fused's path):
+    the norm kernels write h's e4m3 bytes and proj casts the attention output in its own layout; unfused (native3's):
+    the norms write bf16 h, the attention output is copied to [B, N, C], and the linears cast both. The same bits
+    either way; ms per step, best of 2 alternating runs."""
+    import torch
+    D = C // heads
+    g = torch.Generator(device=dev).manual_seed(14)
+
+    def bf(*shape, std=1.0, grad=True):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16).requires_grad_(grad)
+
+    x = bf(B, N, C)
+    mod = bf(B, 1, 6 * C, std=0.2)
+    wn1 = (1 + 0.1 * torch.randn(C, generator=g, device=dev)).requires_grad_()
+    wn2 = (1 + 0.1 * torch.randn(C, generator=g, device=dev)).requires_grad_()
+    wqkv, wproj, bproj = bf(3 * C, C, std=C ** -0.5), bf(C, C, std=C ** -0.5), bf(C, std=0.1)
+    w12, w3 = bf(2 * H, C, std=C ** -0.5), bf(C, H, std=H ** -0.5)
+    dy = bf(B, N, C, std=0.1, grad=False)
+
+    def run(fused):
+        sh1, sc1, g1, sh2, sc2, g2 = (mod[..., i * C:(i + 1) * C] for i in range(6))
+        if fused:
+            qkv = G.fp8_mod_rmsnorm_linear(x, wn1, sh1, sc1, eps, wqkv)
+        else:
+            qkv = G.fp8_linear_f8(G.mod_rmsnorm(x, wn1, sh1, sc1, eps), wqkv)
+        q, k, v = (t.contiguous() for t in qkv.view(B, N, 3, heads, D).permute(2, 0, 3, 1, 4))
+        o = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+        if fused:
+            a = G.fp8_heads_linear_f8(o, wproj, bproj)
+            xn, y = G.fp8_res_mod_rmsnorm_mlp(x, a, g1, wn2, sh2, sc2, eps, w12, w3)
+        else:
+            a = G.fp8_linear_f8(o.transpose(1, 2).reshape(B, N, C), wproj, bproj)
+            xn, h2 = G.res_mod_rmsnorm(x, a, g1, wn2, sh2, sc2, eps)
+            y = G.fp8_mlp_f8(h2, w12, w3)
+        (xn + g2 * y).backward(dy)
+
+    t = {"fused": [], "unfused": []}
+    for _ in range(2):
+        for k in ("fused", "unfused"):
+            t[k].append(time_region(lambda: run(k == "fused"), steps, 2))
+    f, u = min(t["fused"]), min(t["unfused"])
+    return {"workload": f"d12 lever-K block fwd + bwd over {B * N} tokens ({heads} heads of {D}; attention by "
+                        "scaled_dot_product_attention, no q / k norms or rotary embedding): native3+fused's path "
+                        "(norm sites writing h's e4m3 bytes, proj casting the attention output in its own layout) "
+                        f"against native3's (ms per step, best of 2 alternating runs of {steps})",
+            "fused_ms": round(f, 4), "unfused_ms": round(u, 4), "saved_us": round((u - f) * 1e3, 1)}
+
+
 def mfma_ceiling(G, dev):
     """The FP8 MFMA rate the device sustains at 100% issue (tests/hip/mfma_ceiling.hip: every SIMD issuing MFMAs back to
     back, no memory traffic), measured live, in the 16 x 16 x 128 form the GEMM uses on three kinds of operands -- the
@@ -707,6 +758,8 @@ def main():
     nblock = norm_block(G, dev)
     # ---- the attention output's producer: proj's e4m3 input read from o [B, H, N, D] in its own layout
     heads = heads_site(G, dev)
+    # ---- a whole lever-K block with both producers fused against native3's path
+    pblock = block_producers(G, dev)
 
     # ---- config 5: the d18 block (C = 1792, H = 7168) with 1% outlier activation channels, fwd + bwd
     C18, H18 = 1792, 7168
@@ -837,6 +890,7 @@ def main():
         "norm_sites": norm,
         "norm_block": nblock,
         "heads_site": heads,
+        "block_producers": pblock,
         "d18_block": {"workload": "config 5: d18 block (C 1792, H 7168), 1% outlier channels x50, fwd+bwd, native3",
                       "ms": round(ms18, 4), "gemm_tflop": round(fl18 / 1e12, 4),
                       "tflops": round(fl18 / ms18 / 1e9, 1)},
